@@ -1,0 +1,153 @@
+"""Benchmark of the angle-domain paged decode on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]`
+
+A step is one decode over the whole paged context of one layer (all kv heads)
+for the workload named in BASELINE.json's metric: config 2, Llama-3.1-8B
+attention shape (32 q / 8 kv heads, dh 128), 32K context, 60/30/10 tier mix,
+randomly permuted page table.  Inputs are resident in HBM before timing; the
+Infinity Cache (256 MB) is defeated by rotating through ROTATE independent
+copies of the KV pool (each ~80 MB).  Timing uses HIP events on the stream the
+kernels run on (torch's current stream), around exactly K steps.
+
+Prints one JSON line (see the "roofline" and "cpu_baseline" objects).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "spherical-kv_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+import sphkv_format as fmt  # noqa: E402
+import sphkv_ops as ops  # noqa: E402
+import sphkv_synth as synth  # noqa: E402
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "µs/decode step + achieved HBM GB/s (compressed KV), 8B shape, 32K ctx, 1 GPU"
+ROTATE = 6
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
+    """An independent copy of the KV bytes (pages and V) at new addresses."""
+    return ops.PagedPool(**{**pool.__dict__, "pages": pool.pages.clone(), "v_pool": pool.v_pool.clone()})
+
+
+def cpu_baseline(wl, pool: ops.PagedPool, budget_s: float = 20.0):
+    """Reference Mode-B path restated in torch (oracle/torch_port.py), on the
+    host cores, over a bounded sample of the same workload: whole kv heads of
+    the config, as many as fit the time budget (at least one)."""
+    sys.path.insert(0, ROOT)
+    from oracle import torch_port
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    pages = pool.pages.cpu().numpy()
+    v_pool = pool.v_pool.cpu().numpy()
+    cos_t, sin_t = fmt.rope_tables(max(wl.lengths) + 64, wl.dh, wl.rope_theta)
+    cos_t, sin_t = torch.from_numpy(cos_t), torch.from_numpy(sin_t)
+    times, heads_done = [], 0
+    t_start = time.perf_counter()
+    for sh in range(wl.plan.num_seqs * wl.plan.num_kv):
+        s, h = divmod(sh, wl.plan.num_kv)
+        blocks = torch_port.head_blocks(pages, v_pool, wl.plan, sh)
+        cbs = {t: torch.from_numpy(c[h]) for t, c in wl.codebooks.items()}
+        q = torch.from_numpy(wl.q[s, h * wl.gqa:(h + 1) * wl.gqa].astype(np.float32))
+        torch_port.decode_head(q, blocks, cbs, cos_t, sin_t)          # warm-up
+        t0 = time.perf_counter()
+        torch_port.decode_head(q, blocks, cbs, cos_t, sin_t)
+        times.append(time.perf_counter() - t0)
+        heads_done += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    per_head = float(np.median(times))
+    step_us = per_head * wl.plan.num_seqs * wl.plan.num_kv * 1e6
+    return {"value": round(step_us, 1), "unit": "µs/decode step (extrapolated from per-head time)",
+            "cores": threads, "kind": "port",
+            "sample": f"{heads_done} of {wl.plan.num_seqs * wl.plan.num_kv} kv heads of {wl.name}, "
+                      f"median per-head time x {wl.plan.num_seqs * wl.plan.num_kv} heads; torch CPU "
+                      f"restatement of spherical_kv_pipeline.py:2143-2177,2348,2367"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--rotate", type=int, default=ROTATE)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the decode "
+              f"shards by kv head or context with no exchange inside the kernel, and multi-GPU runs "
+              f"are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    log(f"[bench] building config{args.config} workload")
+    wl = synth.make_decode_workload(args.config)
+    pool0, _, _ = ops.build_pool_gpu(wl, dev)
+    pools = [pool0] + [clone_pool(pool0) for _ in range(args.rotate - 1)]
+    torch.cuda.synchronize()
+    q = torch.as_tensor(wl.q, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(pool0.workspace_bytes(wl.gqa), 4), dtype=torch.uint8, device=dev)
+    nbytes = fmt.decode_bytes(wl.plan)
+    log(f"[bench] rows={wl.plan.num_rows} items={pool0.num_items} algorithmic bytes/step={nbytes}")
+
+    for i in range(args.warmup):
+        ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    us = ms * 1e3
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (torch restatement of the reference path)")
+        cpu = cpu_baseline(wl, pool0)
+        log(f"[bench] CPU {cpu['value']} us/step on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC, "value": round(us, 3), "unit": "µs/decode step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16 I/O, fp32 math",
+        "data": "synthetic (seeded generator, config spec of BASELINE.json)",
+        "achieved_hbm_gbps": round(gbps, 1),
+        "config": {"workload": f"config{args.config}: {wl.num_q} q / {wl.num_kv} kv heads, dh {wl.dh}, "
+                               f"{wl.num_seqs} seq x {max(wl.lengths)} ctx, 16-token pages, tier mix of BASELINE",
+                   "num_seqs": wl.num_seqs, "ctx": max(wl.lengths), "pages": wl.plan.num_rows,
+                   "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "decode_split_kernel + decode_merge_kernel (whole step)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+// extern "C" boundary of libsphkv.so (declarations: include/sphkv.h).
+// Host code only: argument validation, error reporting, kernel dispatch.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/sphkv.h"
+#include "sphkv_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return SPHKV_OK;
+}
+
+int launch_status(int rc, const char* what) {
+  if (rc != 0) {
+    hipError_t e = hipGetLastError();
+    return fail(SPHKV_ELAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  }
+  return ok();
+}
+
+bool dh_ok(int32_t dh) { return dh == 64 || dh == 128; }
+bool gqa_ok(int32_t g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+
+}  // namespace
+
+extern "C" {
+
+const char* sphkv_last_error(void) { return g_err; }
+
+const char* sphkv_version(void) { return "sphkv 0.1 gfx950"; }
+
+int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int64_t num_src_rows,
+                       const int64_t* src_rows, const int32_t* tier, const int32_t* count,
+                       const int32_t* ptable, const int32_t* vslot, const int32_t* seq_head,
+                       int32_t num_pages, int32_t num_kv,
+                       const float* cb1, const float* cb2, const float* cb3,
+                       uint8_t* pages, int64_t pages_bytes, uint16_t* v_pool, int64_t num_vpages,
+                       float* r_out, int32_t* code_out, int32_t dh, int32_t page_size, void* stream) {
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "sphkv_encode_pages: dh must be 64 or 128 (got %d)", dh);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "sphkv_encode_pages: page_size must be 16 (got %d)", page_size);
+  if (num_pages < 0 || num_kv <= 0 || num_src_rows < 0 || pages_bytes < 0 || num_vpages < 0)
+    return fail(SPHKV_EINVAL, "sphkv_encode_pages: negative size");
+  if (num_pages == 0) return ok();
+  if (!k || !v || !src_rows || !tier || !count || !ptable || !vslot || !seq_head || !pages || !v_pool)
+    return fail(SPHKV_EINVAL, "sphkv_encode_pages: null pointer argument");
+  sphkv::EncodeLaunch L{k, k_is_fp32, v, num_src_rows, src_rows, tier, count, ptable, vslot, seq_head,
+                        num_pages, num_kv, cb1, cb2, cb3, pages, pages_bytes, v_pool, num_vpages,
+                        r_out, code_out, dh};
+  return launch_status(sphkv::launch_encode(L, (hipStream_t)stream), "sphkv_encode_pages");
+}
+
+int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32_t dh) {
+  if (num_items < 0 || !gqa_ok(gqa) || !dh_ok(dh)) return -1;
+  return (int64_t)num_items * sphkv::partial_floats(gqa, dh) * (int64_t)sizeof(float);
+}
+
+int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                       const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                       const uint16_t* v_pool, int64_t num_vpages,
+                       const float* cb1, const float* cb2, const float* cb3,
+                       const int32_t* work, int32_t num_items, const int32_t* work_start,
+                       int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                       const uint16_t* q, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                       int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                       void* stream) {
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: dh must be 64 or 128 (got %d)", dh);
+  if (!gqa_ok(gqa)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: gqa must be 1, 2, 4 or 8 (got %d)", gqa);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "sphkv_decode_paged: page_size must be 16 (got %d)", page_size);
+  if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || num_rows < 0)
+    return fail(SPHKV_EINVAL, "sphkv_decode_paged: negative size");
+  if (!(rope_theta > 1.0)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: rope_theta must be > 1");
+  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
+  if (workspace_bytes < need)
+    return fail(SPHKV_EINVAL, "sphkv_decode_paged: workspace too small (%lld < %lld bytes)",
+                (long long)workspace_bytes, (long long)need);
+  if (num_seqs == 0) return ok();
+  if (!q || !out || !work_start || (num_items > 0 && (!work || !workspace || !pages || !ptable ||
+                                                      !vslot || !positions || !v_pool)))
+    return fail(SPHKV_EINVAL, "sphkv_decode_paged: null pointer argument");
+  sphkv::DecodeLaunch L{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
+                        cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q, out,
+                        static_cast<float*>(workspace), dh, sm_scale, rope_theta};
+  return launch_status(sphkv::launch_decode(L, (hipStream_t)stream), "sphkv_decode_paged");
+}
+
+int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                              const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
+                              const float* cos_tbl, const float* sin_tbl, int32_t max_pos,
+                              const float* q, int32_t grp, int32_t num_kv, const float* codebooks,
+                              int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
+                              int32_t page_size, float* logits_out, void* stream) {
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: dh must be 64 or 128 (got %d)", dh);
+  if (group_size <= 0 || groups * group_size != dh || (group_size % 8) != 0)
+    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: groups*group_size must equal dh, group_size %% 8 == 0");
+  if (b_theta < 1 || b_theta > 8) return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: b_theta must be 1..8");
+  if (page_size < 1 || page_size > 128)
+    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: page_size must be 1..128 (got %d)", page_size);
+  if (num_pages < 0 || grp <= 0 || num_kv <= 0 || max_pos <= 0)
+    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: bad size");
+  if (num_pages == 0) return ok();
+  if (!pages || !ptable || !head_ids || !positions || !cos_tbl || !sin_tbl || !q || !codebooks || !logits_out)
+    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: null pointer argument");
+  sphkv::RaggedLaunch L{pages, pages_bytes, ptable, head_ids, positions, num_pages, cos_tbl, sin_tbl,
+                        max_pos, q, grp, num_kv, codebooks, dh, groups, group_size, b_theta,
+                        page_size, logits_out};
+  return launch_status(sphkv::launch_ragged(L, (hipStream_t)stream), "sphkv_fused_decode_ragged");
+}
+
+}  // extern "C"

@@ -1,0 +1,39 @@
+// Shared device-side definitions of the angle-domain compressed-KV kernels
+// (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace sphkv {
+
+constexpr int kHeaderBytes = 8;     // paging.py:2 HEADER_BYTES (config.py:3)
+constexpr int kDenseTier = 0xFF;    // header tier id of a dense fp16 K page
+constexpr int kTile = 16;           // tokens per page handled as one MFMA tile
+constexpr int kWave = 64;
+
+// Tier geometry of tiers.py:35-41 (tier id -> group size, bits per code).
+__host__ __device__ constexpr int tier_g(int tid) { return tid == 3 ? 32 : 16; }
+__host__ __device__ constexpr int tier_b(int tid) { return tid == 1 ? 6 : (tid == 2 ? 4 : 3); }
+__host__ __device__ constexpr int tier_C(int tid) { return 1 << tier_b(tid); }
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Orders this wave's LDS traffic: every LDS access issued before the call is
+// complete before any issued after it.  Waves do not wait for each other.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// xor-shuffle within a wave (ds_bpermute / DPP chosen by the compiler).
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+}  // namespace sphkv

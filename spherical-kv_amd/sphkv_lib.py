@@ -1,0 +1,67 @@
+"""ctypes binding of libsphkv.so (the C ABI declared in include/sphkv.h).
+
+Loads the in-tree library built by `make -C spherical-kv_amd`.  There is no
+fallback: if the library is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsphkv.so")
+_lib = None
+_lock = threading.Lock()
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+F64 = ctypes.c_double
+
+# name -> (restype, argtypes); must match include/sphkv.h
+SIGNATURES = {
+    "sphkv_last_error": (ctypes.c_char_p, []),
+    "sphkv_version": (ctypes.c_char_p, []),
+    "sphkv_encode_pages": (ctypes.c_int, [P, I32, P, I64, P, P, P, P, P, P, I32, I32, P, P, P,
+                                          P, I64, P, I64, P, P, I32, I32, P]),
+    "sphkv_decode_paged_workspace_bytes": (I64, [I32, I32, I32]),
+    "sphkv_decode_paged": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P,
+                                          I32, I32, I32, P, P, P, I64, I32, I32, F32, F64, P]),
+    "sphkv_fused_decode_ragged": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
+                                                 I32, I32, I32, I32, I32, P, P]),
+}
+
+
+class SphkvError(RuntimeError):
+    pass
+
+
+def load():
+    """Return the loaded library; raise SphkvError if it is not there."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise SphkvError(f"libsphkv.so not found at {LIB_PATH}; build it with "
+                                 f"`make -C {_HERE}` (or __graft_entry__.build())")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().sphkv_last_error().decode(errors="replace")
+        raise SphkvError(f"{what} failed ({rc}): {msg}")
+
+
+def version() -> str:
+    return load().sphkv_version().decode()

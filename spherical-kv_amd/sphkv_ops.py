@@ -1,0 +1,232 @@
+"""torch-facing operations over the paged angle-domain KV pool.
+
+PyTorch provides device memory and the stream; all compute runs in
+libsphkv.so (HIP, gfx950).  No CPU or torch fallback exists: inputs on the
+wrong device, or a missing library, raise.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+
+import sphkv_format as fmt
+from sphkv_lib import check, load
+
+ROWS_PER_ITEM = 32     # pointer-table rows per decode work item (8 pages per wave)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, dtype, name: str, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU device (the library has no CPU path)")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM):
+    """Split each (seq, head) row range into items of <= rows_per_item rows.
+    Returns (work int32 [n_items, 3], work_start int32 [num_sh + 1])."""
+    rs = np.asarray(row_start, np.int64)
+    work, ws = [], [0]
+    for sh in range(rs.shape[0] - 1):
+        b, e = int(rs[sh]), int(rs[sh + 1])
+        for r0 in range(b, e, rows_per_item):
+            work.append((sh, r0, min(e, r0 + rows_per_item)))
+        ws.append(len(work))
+    w = np.asarray(work, np.int32).reshape(-1, 3)
+    return w, np.asarray(ws, np.int32)
+
+
+def validate_plan(plan: fmt.PagePlan) -> None:
+    """Host-side checks of a plan's pointer table against the kernels' needs."""
+    pt = plan.ptable.astype(np.int64)
+    if plan.page_size != 16:
+        raise ValueError("page_size must be 16")
+    if (plan.count < 0).any() or (plan.count > plan.page_size).any():
+        raise ValueError("page counts must be in [0, page_size]")
+    for tid in np.unique(plan.tier):
+        m = plan.tier == tid
+        n = plan.count[m].astype(np.int64)
+        if int(tid) == fmt.DENSE_TIER_ID:
+            end = pt[m, 1] + n * plan.dh * 2
+            if (pt[m, 1] % 16).any():
+                raise ValueError("dense page payloads must be 16-byte aligned")
+        elif int(tid) in fmt.TIER_GEOMETRY:
+            g, b = fmt.TIER_GEOMETRY[int(tid)]
+            G = plan.dh // g
+            end = pt[m, 2] + n * G
+            if ((pt[m, 2] - (pt[m, 0] & ~15)) + n * G > 512).any():
+                raise ValueError("compressed page sections must lie within 512 bytes of the page's 16-byte line")
+        else:
+            raise ValueError(f"unknown tier id {int(tid)}")
+        if (pt[m, 0] % 4).any():
+            raise ValueError("page offsets must be 4-byte aligned")
+        if (pt[m, 0] < 0).any() or (end > plan.pages_bytes).any():
+            raise ValueError("page extends beyond the byte pool")
+    if (plan.vslot < 0).any() or (plan.vslot >= plan.num_vpages).any():
+        raise ValueError("vslot out of range")
+
+
+@dataclass
+class PagedPool:
+    """Device-resident paged KV of one layer: byte pool, pointer table,
+    positions, token-minor V pages, per-tier codebooks and the decode work
+    list."""
+    plan: fmt.PagePlan
+    pages: torch.Tensor        # uint8 [pages_bytes]
+    ptable: torch.Tensor       # int32 [P, 3]
+    vslot: torch.Tensor        # int32 [P]
+    positions: torch.Tensor    # int32 [P, 16]
+    v_pool: torch.Tensor       # fp16 [num_vpages, dh, 16]
+    codebooks: Dict[int, torch.Tensor]   # tier -> fp32 [num_kv, G, C, g]
+    work: torch.Tensor         # int32 [n_items, 3]
+    work_start: torch.Tensor   # int32 [num_seqs*num_kv + 1]
+    tier: torch.Tensor         # int32 [P]
+    count: torch.Tensor        # int32 [P]
+    seq_head: torch.Tensor     # int32 [P]
+
+    @property
+    def device(self):
+        return self.pages.device
+
+    @property
+    def num_items(self) -> int:
+        return int(self.work.shape[0])
+
+    @staticmethod
+    def allocate(plan: fmt.PagePlan, codebooks: Dict[int, np.ndarray], device="cuda",
+                 rows_per_item: int = ROWS_PER_ITEM) -> "PagedPool":
+        validate_plan(plan)
+        dev = torch.device(device)
+        work, ws = make_work(plan.row_start, rows_per_item)
+        cbs = {int(t): torch.as_tensor(np.ascontiguousarray(c, np.float32), device=dev)
+               for t, c in codebooks.items()}
+        for tid in np.unique(plan.tier):
+            tid = int(tid)
+            if tid != fmt.DENSE_TIER_ID and tid not in cbs:
+                raise ValueError(f"no codebook for tier {tid}")
+        for tid, c in cbs.items():
+            g, b = fmt.TIER_GEOMETRY[tid]
+            want = (plan.num_kv, plan.dh // g, 2 ** b, g)
+            if tuple(c.shape) != want:
+                raise ValueError(f"tier {tid} codebook shape {tuple(c.shape)} != {want}")
+        return PagedPool(
+            plan=plan,
+            pages=torch.zeros(plan.pages_bytes, dtype=torch.uint8, device=dev),
+            ptable=torch.as_tensor(plan.ptable, device=dev),
+            vslot=torch.as_tensor(plan.vslot, device=dev),
+            positions=torch.as_tensor(plan.positions, device=dev),
+            v_pool=torch.zeros((plan.num_vpages, plan.dh, plan.page_size), dtype=torch.float16, device=dev),
+            codebooks=cbs,
+            work=torch.as_tensor(work, device=dev),
+            work_start=torch.as_tensor(ws, device=dev),
+            tier=torch.as_tensor(plan.tier, device=dev),
+            count=torch.as_tensor(plan.count, device=dev),
+            seq_head=torch.as_tensor(plan.seq_head, device=dev),
+        )
+
+    def cb_ptrs(self):
+        return tuple(_ptr(self.codebooks.get(t)) for t in (1, 2, 3))
+
+    def workspace_bytes(self, gqa: int) -> int:
+        n = load().sphkv_decode_paged_workspace_bytes(self.num_items, gqa, self.plan.dh)
+        if n < 0:
+            raise ValueError("bad gqa / dh for the decode workspace")
+        return int(n)
+
+
+def encode_pages(pool: PagedPool, k: torch.Tensor, v: torch.Tensor, src_rows: torch.Tensor,
+                 r_out: Optional[torch.Tensor] = None, code_out: Optional[torch.Tensor] = None) -> None:
+    """Fused encode + bitpack of every page of the pool's plan (GPU).
+    k: [rows, dh] fp16 or fp32; v: [rows, dh] fp16; src_rows int64 [P, 16]."""
+    plan = pool.plan
+    dev = pool.device
+    if k.dtype not in (torch.float16, torch.float32):
+        raise TypeError("k must be fp16 or fp32")
+    _need(k, k.dtype, "k", dev)
+    _need(v, torch.float16, "v", dev)
+    _need(src_rows, torch.int64, "src_rows", dev)
+    if k.dim() != 2 or k.shape[1] != plan.dh or v.shape != k.shape:
+        raise ValueError("k and v must be [rows, dh]")
+    if tuple(src_rows.shape) != (plan.num_rows, plan.page_size):
+        raise ValueError("src_rows must be [P, page_size]")
+    for t, name in ((r_out, "r_out"), (code_out, "code_out")):
+        if t is not None:
+            _need(t, torch.float32 if name == "r_out" else torch.int32, name, dev)
+            if tuple(t.shape) != (plan.num_rows, plan.page_size, plan.dh // 16):
+                raise ValueError(f"{name} must be [P, page_size, dh/16]")
+    c1, c2, c3 = pool.cb_ptrs()
+    rc = load().sphkv_encode_pages(
+        k.data_ptr(), 1 if k.dtype == torch.float32 else 0, v.data_ptr(), k.shape[0],
+        src_rows.data_ptr(), pool.tier.data_ptr(), pool.count.data_ptr(), pool.ptable.data_ptr(),
+        pool.vslot.data_ptr(), pool.seq_head.data_ptr(), plan.num_rows, plan.num_kv,
+        c1, c2, c3, pool.pages.data_ptr(), plan.pages_bytes, pool.v_pool.data_ptr(), plan.num_vpages,
+        _ptr(r_out), _ptr(code_out), plan.dh, plan.page_size, _stream())
+    check(rc, "sphkv_encode_pages")
+
+
+def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
+                 sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Angle-domain paged attention decode.  q fp16 [num_seqs, num_kv*gqa, dh]
+    -> out fp16 of the same shape."""
+    plan = pool.plan
+    dev = pool.device
+    _need(q, torch.float16, "q", dev)
+    want = (plan.num_seqs, plan.num_kv * gqa, plan.dh)
+    if tuple(q.shape) != want:
+        raise ValueError(f"q must be {want}, got {tuple(q.shape)}")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.float16, "out", dev)
+    if out.shape != q.shape:
+        raise ValueError("out must match q")
+    wsb = pool.workspace_bytes(gqa)
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
+    _need(workspace, torch.uint8, "workspace", dev)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(plan.dh)
+    c1, c2, c3 = pool.cb_ptrs()
+    rc = load().sphkv_decode_paged(
+        pool.pages.data_ptr(), plan.pages_bytes, pool.ptable.data_ptr(), pool.vslot.data_ptr(),
+        pool.positions.data_ptr(), plan.num_rows, pool.v_pool.data_ptr(), plan.num_vpages,
+        c1, c2, c3, pool.work.data_ptr(), pool.num_items, pool.work_start.data_ptr(),
+        plan.num_seqs, plan.num_kv, gqa, q.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+        workspace.numel(), plan.dh, plan.page_size, float(sm_scale), float(rope_theta), _stream())
+    check(rc, "sphkv_decode_paged")
+    return out
+
+
+def build_pool_gpu(wl, device="cuda", rows_per_item: int = ROWS_PER_ITEM, with_codes: bool = False):
+    """Allocate a pool for a synthetic workload and encode it on the GPU.
+    Returns (pool, r_out, code_out) (the last two None unless with_codes)."""
+    pool = PagedPool.allocate(wl.plan, wl.codebooks, device, rows_per_item)
+    k = torch.as_tensor(wl.k_rows(), device=pool.device)
+    v = torch.as_tensor(wl.v_rows(), device=pool.device)
+    src = torch.as_tensor(wl.src_rows(), device=pool.device)
+    r_out = code_out = None
+    if with_codes:
+        shp = (wl.plan.num_rows, wl.plan.page_size, wl.dh // 16)
+        r_out = torch.zeros(shp, dtype=torch.float32, device=pool.device)
+        code_out = torch.zeros(shp, dtype=torch.int32, device=pool.device)
+    encode_pages(pool, k, v, src, r_out, code_out)
+    del k, v, src
+    return pool, r_out, code_out

@@ -1,0 +1,163 @@
+"""Writes the committed golden fixtures under tests/golden/.
+
+The reference has no tests, fixtures or golden vectors for this path, so these
+fixtures are the pins.  They are produced by torch on the CPU executing the
+reference's own op sequence, restated here op for op (the reference module is
+not imported):
+
+* encode:  spherical_kv_pipeline.py:1136-1144
+           K.view(N,G,g); r = K.norm(dim=-1); dir = K / (r[...,None] + EPS);
+           sims = einsum('ngi,gci->ngc', dir, cb); codes = sims.argmax(-1)
+* page:    pagebuilder.py:17-33, paging.py:20-31, bitpacking.py:5-29
+* decode:  spherical_kv_pipeline.py:2143-2177 (logits), 2348 (softmax),
+           2367 (attn @ V), in torch fp32, with fp32 cos/sin tables built from
+           fp64 angles (the documented RoPE convention of this build).
+
+Recorded with every encode case: torch version and the fp64 top-2 similarity
+margin of every group (a margin of a few 1e-7 is where summation order decides
+the argmax).
+
+Run from the repository root:  python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+EPS = 1e-8
+HEADER_BYTES = 8
+
+
+def t_encode(K: torch.Tensor, cb: torch.Tensor, g: int, G: int):
+    N = K.shape[0]
+    Kg = K.view(N, G, g)
+    r = Kg.norm(dim=-1)
+    Kd = Kg / (r.unsqueeze(-1) + EPS)
+    sims = torch.einsum('ngi,gci->ngc', Kd, cb)
+    return r, sims.argmax(dim=-1).to(torch.int32)
+
+
+def t_pack_bits(values: torch.Tensor, bits: int) -> torch.Tensor:
+    n = values.numel()
+    out = torch.zeros((n * bits + 7) // 8, dtype=torch.uint8)
+    bit_idx = torch.arange(bits)
+    bit_matrix = ((values.unsqueeze(1) >> bit_idx) & 1).bool()
+    global_bits = torch.arange(n).unsqueeze(1) * bits + bit_idx
+    byte_idx = (global_bits >> 3).long().reshape(-1)
+    bit_shift = (global_bits & 7).long().reshape(-1)
+    contrib = bit_matrix.reshape(-1).to(torch.uint8) << bit_shift.to(torch.uint8)
+    out.scatter_add_(0, byte_idx, contrib)
+    return out
+
+
+def t_build_page(r: torch.Tensor, codes: torch.Tensor, tier_id: int, b_theta: int) -> torch.Tensor:
+    N, G = r.shape
+    r_scale = r.abs().max(dim=0).values
+    safe = r_scale.clamp(min=1e-8).unsqueeze(0)
+    rc = (r / safe * 127).round().clamp(-127, 127).to(torch.int8)
+    packed = t_pack_bits(codes.flatten().to(torch.int32), b_theta)
+    hdr = torch.zeros(HEADER_BYTES + 4 * G, dtype=torch.uint8)
+    hdr[0] = tier_id & 0xFF
+    hdr[1] = N & 0xFF
+    hdr[HEADER_BYTES:] = r_scale.to(torch.float32).view(torch.uint8)
+    return torch.cat([hdr, packed, rc.flatten().view(torch.uint8)])
+
+
+def margins(K: np.ndarray, cb: np.ndarray, g: int, G: int) -> np.ndarray:
+    Kg = K.astype(np.float64).reshape(-1, G, g)
+    d = Kg / (np.linalg.norm(Kg, axis=-1, keepdims=True) + EPS)
+    s = np.einsum('ngi,gci->ngc', d, cb.astype(np.float64))
+    s.sort(axis=-1)
+    return s[..., -1] - s[..., -2]
+
+
+def encode_case(name, rng, N, tier_id, g, b, dh=128, kind="normal"):
+    G, C = dh // g, 2 ** b
+    cb = rng.standard_normal((G, C, g))
+    cb = (cb / np.linalg.norm(cb, axis=-1, keepdims=True)).astype(np.float32)
+    if kind == "normal":
+        K = rng.standard_normal((N, dh)).astype(np.float16)
+    else:  # config-3 style: lognormal channel scale, 1% outlier channels x8
+        sc = np.exp(rng.normal(0, 0.5, size=dh))
+        sc[rng.choice(dh, size=max(1, dh // 100), replace=False)] *= 8
+        K = (rng.standard_normal((N, dh)) * sc).astype(np.float16)
+    if kind == "zeros":
+        K[:] = 0
+    Kt = torch.from_numpy(K.astype(np.float32))
+    r, codes = t_encode(Kt, torch.from_numpy(cb), g, G)
+    page = t_build_page(r, codes, tier_id, b)
+    return {f"{name}__K": K, f"{name}__cb": cb, f"{name}__r": r.numpy(), f"{name}__codes": codes.numpy(),
+            f"{name}__page": page.numpy(), f"{name}__margin": margins(K, cb, g, G).astype(np.float64),
+            f"{name}__meta": np.array([N, tier_id, g, b, dh], np.int64)}
+
+
+def decode_case(name, rng, n_tok, gqa, dh, theta=500000.0):
+    """Torch fp32 restatement of the Mode-B reference decode on one KV head
+    with one tier-1 block, positions spread over [0, 40000)."""
+    g, b = 16, 6
+    G, C = dh // g, 2 ** b
+    cb = rng.standard_normal((G, C, g))
+    cb = (cb / np.linalg.norm(cb, axis=-1, keepdims=True)).astype(np.float32)
+    codes = rng.integers(0, C, size=(n_tok, G)).astype(np.int32)
+    r_hat = np.abs(rng.standard_normal((n_tok, G)) * 4).astype(np.float32)
+    pos = np.sort(rng.choice(40000, size=n_tok, replace=False)).astype(np.int64)
+    q = rng.standard_normal((gqa, dh)).astype(np.float16)
+    V = rng.standard_normal((n_tok, dh)).astype(np.float16)
+    j = np.arange(dh // 2, dtype=np.float64)
+    ang = pos[:, None].astype(np.float64) * (theta ** (-2.0 * j / dh))[None, :]
+    ang = np.concatenate([ang, ang], axis=1)
+    cos_i, sin_i = torch.from_numpy(np.cos(ang).astype(np.float32)), torch.from_numpy(np.sin(ang).astype(np.float32))
+    qt = torch.from_numpy(q.astype(np.float32))
+    qe = qt.unsqueeze(1)
+    half = dh // 2
+    qh = torch.cat([-qe[..., half:], qe[..., :half]], dim=-1)
+    q_rot = qe * cos_i.unsqueeze(0) - qh * sin_i.unsqueeze(0)
+    q_rot_g = q_rot.view(gqa, n_tok, G, g)
+    q_norms = q_rot_g.norm(dim=-1, keepdim=True).clamp(min=1e-6)
+    q_normed = q_rot_g / q_norms
+    cbt = torch.from_numpy(cb)
+    cw = cbt[torch.arange(G).unsqueeze(1), torch.from_numpy(codes).long().T].permute(1, 0, 2)
+    cos_pg = (q_normed * cw.unsqueeze(0)).sum(-1).clamp(-1.0, 1.0)
+    logits = (q_norms.squeeze(-1) * cos_pg * torch.from_numpy(r_hat).unsqueeze(0)).sum(-1) / math.sqrt(dh)
+    attn = torch.softmax(logits, dim=1)
+    out = attn @ torch.from_numpy(V.astype(np.float32))
+    return {f"{name}__cb": cb, f"{name}__codes": codes, f"{name}__r_hat": r_hat, f"{name}__pos": pos,
+            f"{name}__q": q, f"{name}__V": V, f"{name}__logits": logits.numpy(), f"{name}__out": out.numpy(),
+            f"{name}__meta": np.array([n_tok, gqa, dh], np.int64)}
+
+
+def main():
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(20260101)
+    enc = {}
+    enc.update(encode_case("t1_n16", rng, 16, 1, 16, 6))
+    enc.update(encode_case("t1_n16_c3", rng, 16, 1, 16, 6, kind="config3"))
+    enc.update(encode_case("t2_n16", rng, 16, 2, 16, 4))
+    enc.update(encode_case("t3_n16", rng, 16, 3, 32, 3))
+    enc.update(encode_case("t1_n7", rng, 7, 1, 16, 6))
+    enc.update(encode_case("t2_n2", rng, 2, 2, 16, 4))
+    enc.update(encode_case("t2_n1", rng, 1, 2, 16, 4))       # torch naive bmm path
+    enc.update(encode_case("t3_n1", rng, 1, 3, 32, 3))       # torch naive bmm path
+    enc.update(encode_case("t1_n16_dh64", rng, 16, 1, 16, 6, dh=64))
+    enc.update(encode_case("t1_zero", rng, 16, 1, 16, 6, kind="zeros"))
+    for i in range(24):                                        # 384 more tier-1 tokens, config-3 data
+        enc.update(encode_case(f"t1_bulk{i}", rng, 16, 1 + (i % 2), 16, 6 - 2 * (i % 2), kind="config3"))
+    enc["torch_version"] = np.array(torch.__version__)
+    np.savez_compressed(os.path.join(HERE, "encode_golden.npz"), **enc)
+
+    dec = {}
+    dec.update(decode_case("d128_g4", rng, 300, 4, 128))
+    dec.update(decode_case("d64_g4", rng, 200, 4, 64))
+    dec.update(decode_case("d128_g8", rng, 100, 8, 128))
+    dec["torch_version"] = np.array(torch.__version__)
+    np.savez_compressed(os.path.join(HERE, "decode_golden.npz"), **dec)
+    print("wrote", sorted(os.listdir(HERE)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,156 @@
+"""GPU parity of the paged angle-domain decode and the ragged logits kernel.
+
+Tolerance (north star): max-abs error <= 2e-3 of the fp16 decode output
+against the fp64 oracle evaluated on the page-decoded radius
+r_hat = int8 / 127 * scale, the same centroids, positions and fp16 V.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sphkv_format as fmt
+import sphkv_ops as ops
+import sphkv_synth as synth
+from gpu_helpers import log, max_err, pool_from_oracle
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _decode(pool, wl, gpu):
+    q = torch.as_tensor(wl.q, device=gpu)
+    out = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("config,ctx", [(1, None), (2, 4096), (2, None), (5, 4096), (4, 3000)])
+def test_decode_matches_oracle(gpu, config, ctx):
+    kw = {"num_seqs_override": 6} if config == 4 else ({"num_seqs_override": 2} if config == 5 else {})
+    wl = synth.make_decode_workload(config, ctx_override=ctx, **kw)
+    log(f"decode config{config} ctx={ctx} seqs={wl.num_seqs} rows={wl.plan.num_rows} gqa={wl.gqa}")
+    pool, cpu = pool_from_oracle(wl, gpu)
+    got = _decode(pool, wl, gpu)
+    want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+    err = max_err(got, want)
+    log(f"  max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_gpu_encoded_pool_matches_oracle_pool(gpu):
+    # end to end: GPU encode then GPU decode equals decode of the oracle pool
+    wl = synth.make_decode_workload(2, ctx_override=6000)
+    pool_g, _, _ = ops.build_pool_gpu(wl, gpu)
+    pool_c, cpu = pool_from_oracle(wl, gpu)
+    a, b = _decode(pool_g, wl, gpu), _decode(pool_c, wl, gpu)
+    assert (a == b).all()
+
+
+def test_decode_work_split_invariance(gpu):
+    # splitting the context into more / fewer work items only reorders the
+    # log-sum-exp merge
+    wl = synth.make_decode_workload(2, ctx_override=5000)
+    outs = []
+    for rpi in (4, 32, 4096):
+        pool, cpu = pool_from_oracle(wl, gpu, rows_per_item=rpi)
+        outs.append(_decode(pool, wl, gpu))
+    assert max_err(outs[0], outs[1]) < 2e-3 * 0.25 and max_err(outs[1], outs[2]) < 2e-3 * 0.25
+
+
+def test_decode_edge_cases(gpu):
+    rng = np.random.default_rng(3)
+    dh, num_kv, gqa = 128, 4, 4
+    # head 0: 1 token; head 1: empty; head 2: 17 tokens mixed tiers; head 3: all dense 33
+    Ls = [1, 0, 17, 33]
+    L = 40
+    tier_of = []
+    for h, n in enumerate(Ls):
+        t = np.zeros(L, np.int32)
+        if h == 2:
+            t[:n] = rng.choice(np.array([1, 2, 3, fmt.DENSE_TIER_ID], np.int32), size=n)
+        elif h == 3:
+            t[:n] = fmt.DENSE_TIER_ID
+        else:
+            t[:n] = 1
+        tier_of.append(t)
+    cbs = synth.make_codebooks(rng, num_kv, dh, [1, 2, 3])
+    K = [(rng.standard_normal((num_kv, L, dh)) * 2).astype(np.float16)]
+    V = [rng.standard_normal((num_kv, L, dh)).astype(np.float16)]
+    q = (rng.standard_normal((1, num_kv * gqa, dh)) * 2).astype(np.float16)
+    pos = [np.sort(rng.choice(120000, size=L, replace=False))]
+    plan = fmt.plan_pages(tier_of, pos, 1, num_kv, dh, 16, rng=rng)
+    wl = synth.Workload(name="edge", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=1, lengths=[L],
+                        rope_theta=5e5, codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan)
+    pool, cpu = pool_from_oracle(wl, gpu)
+    got = _decode(pool, wl, gpu)
+    want = oracle.decode_mode_b(cpu, plan, cbs, q, gqa, 5e5)
+    assert max_err(got, want) <= TOL
+    assert (got[0, gqa:2 * gqa] == 0).all()             # empty head -> zeros
+    # single token -> exactly its V row (fp16)
+    assert max_err(got[0, :gqa], np.broadcast_to(V[0][0, 0].astype(np.float32), (gqa, dh))) == 0.0
+
+
+def test_decode_masked_positions(gpu):
+    # slots with position -1 are excluded even inside full pages
+    wl = synth.make_decode_workload(1, ctx_override=512)
+    pool, cpu = pool_from_oracle(wl, gpu)
+    pos = wl.plan.positions.copy()
+    rng = np.random.default_rng(5)
+    drop = rng.random(pos.shape) < 0.3
+    pos[drop] = -1
+    pool.positions.copy_(torch.from_numpy(pos))
+    got = _decode(pool, wl, gpu)
+    plan2 = fmt.PagePlan(**{**wl.plan.__dict__, "positions": pos})
+    # oracle: rebuild the token lists without the dropped slots
+    want = np.zeros_like(got, np.float64)
+    inv = oracle.rope_inv_freq(wl.dh, wl.rope_theta)
+    for h in range(wl.num_kv):
+        lg, vs = [], []
+        qh = wl.q[0, h * wl.gqa:(h + 1) * wl.gqa].astype(np.float64)
+        for p in range(int(plan2.row_start[h]), int(plan2.row_start[h + 1])):
+            n = int(plan2.count[p])
+            keep = np.nonzero(pos[p, :n] >= 0)[0]
+            if keep.size == 0:
+                continue
+            codes, r_hat = oracle.unpack_page(cpu["pages"], plan2.ptable[p], 1, n, wl.dh)
+            cb = wl.codebooks[1][h].astype(np.float64)
+            cw = cb[np.arange(4)[None, :], codes[keep]]
+            ang = pos[p, keep][:, None].astype(np.float64) * inv[None]
+            ang = np.concatenate([ang, ang], 1)
+            lg.append(oracle.mode_b_logits(qh, None, np.cos(ang), np.sin(ang), cw, r_hat[keep], None, 4, 16))
+            vs.append(cpu["v_pool"][plan2.vslot[p], :, keep].astype(np.float64))
+        lgc = np.concatenate(lg, 1)
+        e = np.exp(lgc - lgc.max(1, keepdims=True))
+        want[0, h * wl.gqa:(h + 1) * wl.gqa] = (e / e.sum(1, keepdims=True)) @ np.concatenate(vs, 0)
+    assert max_err(got, want) <= TOL
+
+
+def test_ragged_logits_matches_oracle(gpu):
+    import fused_decode
+    wl = synth.make_decode_workload(2, ctx_override=3000)
+    cpu = oracle.build_pool(wl)
+    plan = wl.plan
+    for tid, (g, b) in ((1, (16, 6)), (2, (16, 4))):
+        rows = [p for p in range(plan.num_rows) if plan.tier[p] == tid]
+        heads = (plan.seq_head[rows] % plan.num_kv).astype(np.int32)
+        G = wl.dh // g
+        max_pos = 3100
+        cos_t, sin_t = fmt.rope_tables(max_pos, wl.dh, wl.rope_theta)
+        pos = plan.positions[rows].reshape(-1).astype(np.int32)
+        q = wl.q[0].astype(np.float32)
+        cb = wl.codebooks[tid].reshape(plan.num_kv * G, 2 ** b, g)
+        log(f"ragged tier {tid}: pages={len(rows)}")
+        got = fused_decode.fused_decode_ragged(
+            torch.as_tensor(cpu["pages"], device=gpu), torch.as_tensor(plan.ptable[rows], device=gpu),
+            torch.as_tensor(heads, device=gpu), torch.as_tensor(pos, device=gpu),
+            torch.as_tensor(cos_t, device=gpu), torch.as_tensor(sin_t, device=gpu),
+            torch.as_tensor(q, device=gpu), wl.gqa, plan.num_kv, torch.as_tensor(cb, device=gpu),
+            wl.dh, G, g, b, 16)
+        torch.cuda.synchronize()
+        want = oracle.ragged_logits(cpu["pages"], plan.ptable[rows], heads, pos, cos_t, sin_t, q, wl.gqa,
+                                    cb, wl.dh, G, g, b, 16)
+        got = got.cpu().numpy()
+        fin = np.isfinite(want)
+        assert (np.isneginf(got) == ~fin).all()
+        assert max_err(got[fin], want[fin]) < 2e-4
