@@ -65,7 +65,7 @@ __device__ __forceinline__ float torch_norm(const float* x, int g) {
     for (int l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(x[d + l], x[d + l], acc[l]);
   float b = acc[0];
   for (int l = 1; l < 8; ++l) b = __fadd_rn(b, acc[l]);
-  return __fsqrt_rn(b);
+  return __builtin_sqrtf(b);  // correctly rounded expansion (v_sqrt_f32 alone is not)
 }
 
 template <int DH>
