@@ -88,6 +88,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rotate", type=int, default=ROTATE)
+    ap.add_argument("--layout", default="default", choices=["default", "sequential"],
+                    help="page placement: the config's own (random for configs 2-5) or sequential")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the decode "
@@ -101,13 +103,13 @@ def main():
     torch.cuda.set_device(dev)
 
     log(f"[bench] building config{args.config} workload")
-    wl = synth.make_decode_workload(args.config)
+    wl = synth.make_decode_workload(args.config, layout=args.layout)
     pool0, _, _ = ops.build_pool_gpu(wl, dev)
     pools = [pool0] + [clone_pool(pool0) for _ in range(args.rotate - 1)]
     torch.cuda.synchronize()
     q = torch.as_tensor(wl.q, device=dev)
     out = torch.empty_like(q)
-    ws = torch.empty(max(pool0.workspace_bytes(wl.gqa), 4), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(pool0.workspace_bytes(wl.gqa), 4), dtype=torch.uint8, device=dev)
     nbytes = fmt.decode_bytes(wl.plan)
     log(f"[bench] rows={wl.plan.num_rows} items={pool0.num_items} algorithmic bytes/step={nbytes}")
 
@@ -143,7 +145,7 @@ def main():
                    "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "decode_split_kernel + decode_merge_kernel (whole step)"},
+                     "kernel": "decode_kernel (one launch per step)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

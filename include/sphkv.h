@@ -80,7 +80,9 @@ int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int6
                        float* r_out, int32_t* code_out, int32_t dh, int32_t page_size, void* stream);
 
 /*
- * Workspace bytes sphkv_decode_paged needs for num_items work items.
+ * Workspace bytes sphkv_decode_paged needs for num_items work items: one
+ * (m, l, acc) partial per item.  No initialisation is needed; calls that share
+ * a workspace must not run concurrently.
  */
 int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32_t dh);
 
@@ -97,9 +99,10 @@ int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32
  * page-resident context and the missing fused_decode_ragged kernel's callers
  * (:1102-1125, :1865-1870).
  *
- *   row_start  host-computed work list: work int32 [num_items, 3] =
+ *   work       host-computed work list: work int32 [num_items, 3] =
  *              (seq*num_kv + head, row_begin, row_end) with the items of one
- *              (seq, head) contiguous and in order; work_start int32
+ *              (seq, head) contiguous and in order, and at least one item
+ *              (possibly empty) per (seq, head); work_start int32
  *              [num_seqs*num_kv + 1] = first item of each (seq, head).
  *   q          fp16 [num_seqs, num_kv*gqa, dh];  out fp16, same shape.
  *   workspace  device scratch of sphkv_decode_paged_workspace_bytes() bytes.

@@ -40,7 +40,8 @@ int launch_encode(const EncodeLaunch& L, hipStream_t stream);
 int launch_decode(const DecodeLaunch& L, hipStream_t stream);
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream);
 
-// fp32 elements of one work item's partial: gqa * (dh + 2)
-inline int64_t partial_floats(int gqa, int dh) { return (int64_t)gqa * (dh + 2); }
+// fp32 elements of one work item's partial: 16 (m, l, padding) + gqa * dh
+inline int64_t partial_floats(int gqa, int dh) { return 16 + (int64_t)gqa * dh; }
+
 
 }  // namespace sphkv

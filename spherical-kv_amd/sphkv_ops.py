@@ -16,7 +16,7 @@ import torch
 import sphkv_format as fmt
 from sphkv_lib import check, load
 
-ROWS_PER_ITEM = 32     # pointer-table rows per decode work item (8 pages per wave)
+ROWS_PER_ITEM = 64     # pointer-table rows per decode work item (8 pages per wave, 8 waves)
 
 
 def _stream() -> int:
@@ -40,6 +40,23 @@ def _need(t: torch.Tensor, dtype, name: str, device=None):
         raise ValueError(f"{name} is on {t.device}, expected {device}")
 
 
+def auto_rows_per_item(row_start: np.ndarray, num_cus: int, slots_per_cu: int = 1) -> int:
+    """Rows per work item so that the items fill the chip in whole waves of
+    workgroups: about num_cus * slots_per_cu items (one 8-wave workgroup per
+    CU at the decode kernel's register budget), at least 8 rows per item."""
+    rs = np.asarray(row_start, np.int64)
+    total = int(rs[-1] - rs[0])
+    target = max(1, num_cus * slots_per_cu)
+    rpi = max(8, -(-total // target))
+    # the per-head rounding adds up to one item per head: shrink until it fits
+    while rpi > 8:
+        n = int(np.sum(np.maximum(1, -(-(rs[1:] - rs[:-1]) // rpi))))
+        if n <= target or n > 2 * target:
+            break
+        rpi += 1
+    return rpi
+
+
 def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM):
     """Split each (seq, head) row range into items of <= rows_per_item rows.
     Returns (work int32 [n_items, 3], work_start int32 [num_sh + 1])."""
@@ -47,6 +64,8 @@ def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM):
     work, ws = [], [0]
     for sh in range(rs.shape[0] - 1):
         b, e = int(rs[sh]), int(rs[sh + 1])
+        if e == b:
+            work.append((sh, b, b))          # empty context still writes its output
         for r0 in range(b, e, rows_per_item):
             work.append((sh, r0, min(e, r0 + rows_per_item)))
         ws.append(len(work))
@@ -72,6 +91,9 @@ def validate_plan(plan: fmt.PagePlan) -> None:
             g, b = fmt.TIER_GEOMETRY[int(tid)]
             G = plan.dh // g
             end = pt[m, 2] + n * G
+            if (pt[m, 1] != pt[m, 0] + fmt.HEADER_BYTES + 4 * G).any() or \
+               (pt[m, 2] != pt[m, 1] + (n * G * b + 7) // 8).any():
+                raise ValueError("pointer-table theta/radius offsets disagree with the page layout")
             if ((pt[m, 2] - (pt[m, 0] & ~15)) + n * G > 512).any():
                 raise ValueError("compressed page sections must lie within 512 bytes of the page's 16-byte line")
         else:
@@ -112,9 +134,11 @@ class PagedPool:
 
     @staticmethod
     def allocate(plan: fmt.PagePlan, codebooks: Dict[int, np.ndarray], device="cuda",
-                 rows_per_item: int = ROWS_PER_ITEM) -> "PagedPool":
+                 rows_per_item: Optional[int] = None) -> "PagedPool":
         validate_plan(plan)
         dev = torch.device(device)
+        if rows_per_item is None:
+            rows_per_item = auto_rows_per_item(plan.row_start, torch.cuda.get_device_properties(dev).multi_processor_count)
         work, ws = make_work(plan.row_start, rows_per_item)
         cbs = {int(t): torch.as_tensor(np.ascontiguousarray(c, np.float32), device=dev)
                for t, c in codebooks.items()}
@@ -215,7 +239,7 @@ def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
     return out
 
 
-def build_pool_gpu(wl, device="cuda", rows_per_item: int = ROWS_PER_ITEM, with_codes: bool = False):
+def build_pool_gpu(wl, device="cuda", rows_per_item: Optional[int] = None, with_codes: bool = False):
     """Allocate a pool for a synthetic workload and encode it on the GPU.
     Returns (pool, r_out, code_out) (the last two None unless with_codes)."""
     pool = PagedPool.allocate(wl.plan, wl.codebooks, device, rows_per_item)

@@ -93,7 +93,7 @@ def _assign_tiers(rng, L: int, fracs, sink: int = 0, recent: int = 0) -> np.ndar
 
 
 def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: Optional[int] = None,
-                         num_seqs_override: Optional[int] = None) -> Workload:
+                         num_seqs_override: Optional[int] = None, layout: str = "default") -> Workload:
     """Decode configs 1, 2, 4, 5.  ctx_override shrinks
     the context (for oracle-sized parity cases) keeping everything else."""
     D = fmt.DENSE_TIER_ID
@@ -133,8 +133,10 @@ def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: 
             tier_of.append(_assign_tiers(rng, L, fracs, sink, recent))
     V = [rng.standard_normal((num_kv, L, dh)).astype(np.float16) for L in lengths]
     q = rng.standard_normal((num_seqs, num_kv * gqa, dh)).astype(np.float16)
-    plan = fmt.plan_pages(tier_of, None, num_seqs, num_kv, dh, 16,
-                          rng=None if config == 1 else rng)
+    # config 1 uses an identity page table, the others a random placement;
+    # layout="sequential" forces the identity placement (for locality studies)
+    permute = config != 1 and layout != "sequential"
+    plan = fmt.plan_pages(tier_of, None, num_seqs, num_kv, dh, 16, rng=rng if permute else None)
     return Workload(name=f"config{config}", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=num_seqs,
                     lengths=lengths, rope_theta=theta, codebooks=cbs, K=K, V=V, q=q,
                     tier_of=tier_of, plan=plan)

@@ -14,7 +14,7 @@ def log(msg: str) -> None:
     sys.stdout.flush()
 
 
-def pool_from_oracle(wl, dev, rows_per_item=ops.ROWS_PER_ITEM):
+def pool_from_oracle(wl, dev, rows_per_item=None):
     """Upload a CPU-oracle-built pool to the GPU (isolates the decode kernel
     from the GPU encoder)."""
     cpu = oracle.build_pool(wl)
