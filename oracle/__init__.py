@@ -35,6 +35,7 @@ attention).
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import subprocess
 import sys
@@ -145,14 +146,32 @@ def unpack_page(pages: np.ndarray, row: np.ndarray, tier_id: int, n: int, dh: in
     return codes, rc / 127.0 * scale[None, :]
 
 
+@functools.lru_cache(maxsize=None)
+def v_page_index(dh: int) -> np.ndarray:
+    """Position of element (token k, dim d) inside a V page of the decode pool:
+    d = 16*mm + t, k = 4*u + i  ->  ((t*4 + u) * (dh/16) + mm) * 4 + i."""
+    out = np.zeros((16, dh), np.int64)
+    for k in range(16):
+        for d in range(dh):
+            mm, t, u, i = d // 16, d % 16, k // 4, k % 4
+            out[k, d] = ((t * 4 + u) * (dh // 16) + mm) * 4 + i
+    return out
+
+
+def v_page_rows(v_pool: np.ndarray, vs: int, n: int, dh: int) -> np.ndarray:
+    """The first n V rows [n, dh] of V page vs."""
+    return v_pool[vs][v_page_index(dh)][:n]
+
+
 def build_pool(wl, with_codes: bool = False):
     """Encode every page of a synthetic workload on the CPU and place it as the
-    plan says.  Returns dict(pages uint8, v_pool fp16 [nv, dh, ps], and, if
+    plan says.  Returns dict(pages uint8, v_pool fp16 [nv, 16*dh], and, if
     with_codes, r [P, ps, Gmax] fp32 / codes [P, ps, Gmax] int32)."""
     plan = wl.plan
     dh, ps = wl.dh, plan.page_size
     pages = np.zeros(plan.pages_bytes, np.uint8)
-    v_pool = np.zeros((plan.num_vpages, dh, ps), np.float16)
+    v_pool = np.zeros((plan.num_vpages, ps * dh), np.float16)
+    vidx = v_page_index(dh)
     krows = wl.k_rows()
     vrows = wl.v_rows()
     src = wl.src_rows()
@@ -163,7 +182,7 @@ def build_pool(wl, with_codes: bool = False):
         tid, n = int(plan.tier[p]), int(plan.count[p])
         rows = src[p, :n]
         off, th, rad = (int(x) for x in plan.ptable[p])
-        v_pool[plan.vslot[p], :, :n] = vrows[rows].T
+        v_pool[plan.vslot[p], vidx[:n]] = vrows[rows]
         if tid == DENSE_TIER_ID:
             pages[off] = tid
             pages[off + 1] = n
@@ -235,7 +254,7 @@ def decode_mode_b(pool: Dict[str, np.ndarray], plan, codebooks: Dict[int, np.nda
             ang = pos[:, None] * inv_freq[None, :]
             ang = np.concatenate([ang, ang], axis=1)
             cos_t, sin_t = np.cos(ang), np.sin(ang)
-            vs.append(v_pool[plan.vslot[p], :, :n].T.astype(np.float64))
+            vs.append(v_page_rows(v_pool, plan.vslot[p], n, dh).astype(np.float64))
             if tid == DENSE_TIER_ID:
                 Kd = unpack_page(pages, plan.ptable[p], tid, n, dh).astype(np.float64)
                 logits.append(mode_b_logits(qh, pos, cos_t, sin_t, None, None, Kd, 0, 0))

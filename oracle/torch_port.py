@@ -40,7 +40,7 @@ def head_blocks(pages: np.ndarray, v_pool: np.ndarray, plan, sh: int) -> List[di
             d["codes"].append(codes)
             d["r"].append(r_hat.astype(np.float32))
         d["pos"].append(plan.positions[p, :n].astype(np.int64))
-        d["v"].append(v_pool[plan.vslot[p], :, :n].T)
+        d["v"].append(oracle.v_page_rows(v_pool, plan.vslot[p], n, dh))
     out = []
     for tid, d in by_tier.items():
         blk = {"tier": tid, "pos": torch.from_numpy(np.concatenate(d["pos"])),

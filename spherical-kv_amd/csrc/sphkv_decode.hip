@@ -59,46 +59,99 @@ struct DecodeArgs {
   double log2_theta;
 };
 
+// Codebooks in LDS: rows padded by 4 floats (g=16 -> 20, g=32 -> 36) so that
+// rows of random codes start in different 16-byte bank slots.
 template <int DH>
 struct CbLayout {
-  static constexpr int n1 = (DH / 16) * 64 * 16;   // tier 1 [G][64][16]
-  static constexpr int n2 = (DH / 16) * 16 * 16;   // tier 2 [G][16][16]
-  static constexpr int n3 = (DH / 32) * 8 * 32;    // tier 3 [G][8][32]
+  __host__ __device__ static constexpr int pad(int g) { return g + 4; }
+  static constexpr int n1 = (DH / 16) * 64 * 20;   // tier 1 [G][64][20]
+  static constexpr int n2 = (DH / 16) * 16 * 20;   // tier 2 [G][16][20]
+  static constexpr int n3 = (DH / 32) * 8 * 36;    // tier 3 [G][8][36]
   static constexpr int total = n1 + n2 + n3;
   __host__ __device__ static constexpr int off(int tid) { return tid == 3 ? n1 + n2 : (tid == 2 ? n1 : 0); }
 };
 
 constexpr float kRescaleLog2 = 8.0f;   // reference-max hysteresis (log2 units)
 
-// Pointer-table row of one page, wave-uniform.
+// Every per-page load is a buffer load against a resource that covers exactly
+// the bytes that page may need; a resource of 0 bytes makes the load return
+// zeros without touching memory.  So each loop iteration issues the same
+// loads in the same order whatever the page holds, and the vmcnt waits the
+// compiler derives are exact (a branch around a load makes them conservative,
+// down to waiting for every prefetch in flight).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kOOB = 0x7FFFFF00;       // offset beyond any resource
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const uint32_t n = bytes <= 0 ? 0u : (bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+// Pointer-table row of one page (wave-uniform): lanes 0..2 fetch the row,
+// lane 3 the V slot; the values are read out (readlane) only when needed.
+struct RowLd { int x, y; };
 struct Row {
   int64_t page_off, th_off, rad_off, vs;
   bool ok;
 };
 
-__device__ __forceinline__ Row load_row(const DecodeArgs& a, int p, int re) {
+__device__ __forceinline__ RowLd row_issue(const DecodeArgs& a, int p, int re, int lane) {
+  const bool ok = p < re;
+  const rsrc_t rp = make_rsrc(a.ptable + 3 * (int64_t)(ok ? p : 0), ok ? 12 : 0);
+  const rsrc_t rv = make_rsrc(a.vslot + (ok ? p : 0), ok ? 4 : 0);
+  RowLd l;
+  l.x = __builtin_amdgcn_raw_buffer_load_b32(rp, lane < 3 ? 4 * lane : kOOB, 0, 0);
+  l.y = __builtin_amdgcn_raw_buffer_load_b32(rv, lane == 3 ? 0 : kOOB, 0, 0);
+  return l;
+}
+
+__device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int p, int re) {
   Row r;
-  r.ok = p < re;
-  if (r.ok) {
-    r.page_off = a.ptable[3 * p];
-    r.th_off = a.ptable[3 * p + 1];
-    r.rad_off = a.ptable[3 * p + 2];
-    r.vs = a.vslot[p];
-    r.ok = r.page_off >= 0 && r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
-           r.vs >= 0 && r.vs < a.num_vpages;
-  }
+  r.page_off = __builtin_amdgcn_readlane(l.x, 0);
+  r.th_off = __builtin_amdgcn_readlane(l.x, 1);
+  r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
+  r.vs = __builtin_amdgcn_readlane(l.y, 3);
+  r.ok = p < re && r.page_off >= 0 && r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
+         r.vs >= 0 && r.vs < a.num_vpages;
   if (!r.ok) { r.page_off = 0; r.th_off = 0; r.rad_off = 0; r.vs = 0; }
   return r;
 }
 
+// A dense page's theta section holds n*DH*2 bytes; a compressed page's at most
+// ceil(16*G*b/8) < 2*DH.  Used only to decide what to prefetch; the page header
+// decides how the page is processed.
+template <int DH>
+__device__ __forceinline__ bool row_looks_dense(const Row& r) {
+  return r.ok && (r.rad_off - r.th_off) >= 2 * DH && (r.th_off & 15) == 0;
+}
+
 // 512-byte staging window [page_off & ~15, +512) of a page: lanes < 32 hold 16 bytes each.
 __device__ __forceinline__ uint4 load_stage(const DecodeArgs& a, const Row& r, int lane) {
-  uint4 w = {0u, 0u, 0u, 0u};
-  if (r.ok && lane < 32) {
-    const int64_t src = (r.page_off & ~(int64_t)15) + 16 * lane;
-    if (src + 16 <= a.pages_bytes) w = *reinterpret_cast<const uint4*>(a.pages + src);
+  const int64_t base = r.page_off & ~(int64_t)15;
+  const rsrc_t rs = make_rsrc(a.pages + base, r.ok ? (a.pages_bytes - base < 512 ? a.pages_bytes - base : 512) : 0);
+  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane < 32 ? 16 * lane : kOOB, 0, 0);
+  return uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
+}
+
+__device__ __forceinline__ int load_pos(const DecodeArgs& a, const Row& r, int p, int t) {
+  const rsrc_t rs = make_rsrc(a.positions + (int64_t)(r.ok ? p : 0) * kTile, r.ok ? 4 * kTile : 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * t, 0, 0);
+}
+
+// V page layout ("MFMA order"): element (token 4u+i, dim 16mm+t) at half offset
+// ((t*4 + u) * (DH/16) + mm) * 4 + i, so lane (u, t) reads its PV B operands
+// for all mm as DH/2 contiguous bytes.
+template <int DH>
+__device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int t, int u, half4 (&vreg)[DH / 16]) {
+  const rsrc_t rs = make_rsrc(a.v_pool + r.vs * DH * kTile, r.ok ? DH * kTile * 2 : 0);
+  const int base = (t * 4 + u) * (DH / 16) * 8;     // bytes
+#pragma unroll
+  for (int m2 = 0; m2 < DH / 32; ++m2) {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * m2, 0, 0);
+    const uint2 lo = {(uint32_t)w[0], (uint32_t)w[1]}, hi = {(uint32_t)w[2], (uint32_t)w[3]};
+    vreg[2 * m2] = __builtin_bit_cast(half4, lo);
+    vreg[2 * m2 + 1] = __builtin_bit_cast(half4, hi);
   }
-  return w;
 }
 
 // Codes and radii of this lane's NC chunks from the staged page (LDS).
@@ -146,42 +199,78 @@ __device__ __forceinline__ void unpack_page(const uint8_t* st, int rel, int thr,
   }
 }
 
+// LDS offset (floats) of the centroid chunk a lane needs for chunk c, and
+// the radius factor, for every chunk of the page.
 template <int DH, int TID>
-__device__ __forceinline__ void gather_k(const float* cb_s, const uint8_t* st, int rel, int thr, int rdr,
-                                         int t, int u, int n, bool ok, float (&k)[DH / 32][8]) {
+__device__ __forceinline__ void locate_k(const uint8_t* st, int rel, int thr, int rdr, int t, int u, int n,
+                                         bool ok, int (&cofs)[DH / 32], float (&rh)[DH / 32]) {
   constexpr int NC = DH / 32;
   constexpr int g = tier_g(TID), C = tier_C(TID);
   int code[NC];
-  float rh[NC];
   unpack_page<DH, TID>(st, rel, thr, rdr, t, u, n, ok, code, rh);
-  const float* cbt = cb_s + CbLayout<DH>::off(TID);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d0 = 32 * c + 8 * u;
     const int gi = d0 / g, off = d0 - gi * g;
-    const float4* cen = reinterpret_cast<const float4*>(cbt + (gi * C + code[c]) * g + off);
-    const float4 c0 = cen[0], c1 = cen[1];
-    k[c][0] = rh[c] * c0.x; k[c][1] = rh[c] * c0.y; k[c][2] = rh[c] * c0.z; k[c][3] = rh[c] * c0.w;
-    k[c][4] = rh[c] * c1.x; k[c][5] = rh[c] * c1.y; k[c][6] = rh[c] * c1.z; k[c][7] = rh[c] * c1.w;
+    cofs[c] = CbLayout<DH>::off(TID) + (gi * C + code[c]) * CbLayout<DH>::pad(g) + off;
   }
 }
 
-constexpr int kWaves = 8;              // waves per decode workgroup
+constexpr int kWaves = 12;             // waves per decode workgroup (3 per SIMD)
+constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| <= 63
 
 // Partial of one work item: [16 floats: m[GQA], l[GQA], pad] [acc: GQA * DH]
 template <int DH, int GQA>
 __host__ __device__ constexpr int partial_stride() { return 16 + GQA * DH; }
 
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with the gfx950 row-swap instructions (VALU, no LDS round trip).
+// v_permlane32_swap a, b: a's upper 32 lanes <-> b's lower 32 lanes;
+// v_permlane16_swap a, b: a's odd rows <-> b's even rows.  With a = b = x the
+// sum a + b pairs every lane with its partner row.  Issued as inline asm: the
+// clang builtin of this toolchain reads the first result twice when both
+// inputs are the same value, and the instructions need the s_nop guard
+// (measured: results are wrong without it, right with it).
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  asm volatile("s_nop 4\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  asm volatile("s_nop 4\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float rows_max(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  float c = fmaxf(a, b), d = c;
+  swap16(c, d);
+  return fmaxf(c, d);
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  float c = a + b, d = c;
+  swap16(c, d);
+  return c + d;
+}
+
+// e^{i 2 pi x} with x a phase in turns (fp32 hardware sine/cosine take turns).
+__device__ __forceinline__ float2 turn_phasor(double x) {
+  const float ph = (float)__builtin_amdgcn_fract(x);
+  return float2{__builtin_amdgcn_cosf(ph), __builtin_amdgcn_sinf(ph)};
+}
+
 template <int DH, int GQA>
-__global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeArgs a) {
   constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
   constexpr int NP = NC / 2;         // chunks holding the first RoPE half
   constexpr int NM = DH / 16;        // PV MFMA blocks
-  constexpr int RG = (GQA + 3) / 4;  // 16-lane row groups holding heads
+  constexpr int NJ = DH / 2;         // RoPE frequencies
   using CB = CbLayout<DH>;
   __shared__ __attribute__((aligned(16))) float cb_s[CB::total];
+  __shared__ __attribute__((aligned(16))) float2 dtab[kDelta][NJ + 2]; // e^{i 2pi f_j d}; rows padded 16 B
+  __shared__ __attribute__((aligned(16))) double ftab[NJ];             // f_j in turns per token
   __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][512];
-  __shared__ __attribute__((aligned(16))) _Float16 pbuf[kWaves][16 * 16];
+  __shared__ __attribute__((aligned(16))) float2 bbuf[kWaves][NJ];     // page base phasors
+  __shared__ __attribute__((aligned(16))) _Float16 q_s[16][DH];        // q rows (rows >= GQA zero)
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -194,173 +283,224 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
   const int t = lane & 15;
   const int u = lane >> 4;
 
-  // ---- pipeline prologue: rows of the first two pages, stage of the first --
   int p = rb + wave;
-  Row row_c = load_row(a, p, re);
-  Row row_n = load_row(a, p + kWaves, re);
-  uint4 stg_c = load_stage(a, row_c, lane);
-  int pos_c = row_c.ok ? a.positions[(int64_t)p * kTile + t] : -1;
-
-  // ---- stage this head's codebooks -----------------------------------------
+  // ---- shared tables: codebooks, RoPE frequencies, delta phasors ---------
   for (int tid = 1; tid <= 3; ++tid) {
     const float* src = a.cb[tid];
     if (!src) continue;
-    const int n = tid == 1 ? CB::n1 : (tid == 2 ? CB::n2 : CB::n3);
-    const float4* s4 = reinterpret_cast<const float4*>(src + (int64_t)h * n);
-    float4* d4 = reinterpret_cast<float4*>(cb_s + CB::off(tid));
-    for (int i = threadIdx.x; i < n / 4; i += kWaves * 64) d4[i] = s4[i];
-  }
-  for (int i = threadIdx.x; i < kWaves * 16 * 16; i += kWaves * 64) (&pbuf[0][0])[i] = (_Float16)0.f;
-
-  // ---- per-lane constants: query A operand, RoPE frequencies (turns/token) -
-  half8 qa[NC];
-  {
-    const int hr = lane & 15;
-    const _Float16* qrow = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA + hr) * DH;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (hr < GQA) qa[c] = *reinterpret_cast<const half8*>(qrow + 32 * c + 8 * u);
-      else for (int s = 0; s < 8; ++s) qa[c][s] = (_Float16)0.f;
+    const int g = tier_g(tid), gp = CB::pad(g);
+    const int rows = (DH / g) * tier_C(tid);
+    const float4* s4 = reinterpret_cast<const float4*>(src + (int64_t)h * rows * g);
+    float* dst = cb_s + CB::off(tid);
+    for (int i = threadIdx.x; i < rows * g / 4; i += kWaves * 64) {
+      const int r = (4 * i) / g, col = (4 * i) % g;
+      *reinterpret_cast<float4*>(dst + r * gp + col) = s4[i];
     }
   }
-  double fturn[NP][8];
-#pragma unroll
-  for (int c = 0; c < NP; ++c)
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int j = 32 * c + 8 * u + s;
-      fturn[c][s] = exp2(-(2.0 * j / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
-    }
+  if (threadIdx.x < NJ)
+    ftab[threadIdx.x] = exp2(-(2.0 * threadIdx.x / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
   __syncthreads();
+  for (int i = threadIdx.x; i < kDelta * NJ; i += kWaves * 64)
+    dtab[i / NJ][i % NJ] = turn_phasor((double)(i / NJ) * ftab[i % NJ]);
+  {
+    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+    for (int i = threadIdx.x; i < 16 * DH / 8; i += kWaves * 64) {
+      const int r = i / (DH / 8), c8 = i % (DH / 8);
+      half8 v;
+      if (r < GQA) v = *reinterpret_cast<const half8*>(qh + r * DH + 8 * c8);
+      else for (int s = 0; s < 8; ++s) v[s] = (_Float16)0.f;
+      *reinterpret_cast<half8*>(&q_s[r][8 * c8]) = v;
+    }
+  }
+  const double f_lane = ftab[lane % NJ];
+  __syncthreads();
+  // everything loaded so far is complete before the page pipeline starts, so
+  // no wait inside the loop has to account for it
+  __builtin_amdgcn_s_waitcnt(0);
 
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) { m_run[s] = -INFINITY; l_run[s] = 0.f; }
+  // ---- pipeline prologue: rows of the first two pages, data of the first --
+  Row row_c = row_take(a, row_issue(a, p, re, lane), p, re);
+  RowLd rl_n = row_issue(a, p + kWaves, re, lane);
+  uint4 stg_c = load_stage(a, row_c, lane);
+  int pos_c = load_pos(a, row_c, p, t);
+  half4 vreg[NM];
+  load_v<DH>(a, row_c, t, u, vreg);
+  Row row_n = row_take(a, rl_n, p + kWaves, re);
+
+  // online-softmax state of head hl = lane % 16 (replicated over the 4 rows)
+  const int hl = lane & 15;
+  float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NM];
 #pragma unroll
   for (int mm = 0; mm < NM; ++mm) acc[mm] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
   uint8_t* st = stage[wave];
-  _Float16* pb = pbuf[wave];
+  float2* bb = bbuf[wave];
 
   for (; p < re; p += kWaves) {
-    // ---- issue: V of this page, stage/positions of p+4, row of p+8 --------
-    half4 vreg[NM];
-    {
-      const _Float16* vp = a.v_pool + (row_c.vs * DH + t) * kTile + 4 * u;
-#pragma unroll
-      for (int mm = 0; mm < NM; ++mm) vreg[mm] = *reinterpret_cast<const half4*>(vp + mm * 16 * kTile);
-    }
+    // Lane-derived addresses are recomputed each iteration (a few VALU ops)
+    // instead of being hoisted out of the loop, where they would not fit in
+    // the register budget of 3 waves per SIMD and would be spilled.
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    const int t = lane_v & 15;
+    const int u = lane_v >> 4;
+    // ---- issue: row two pages ahead, stage/positions one page ahead -------
+    const RowLd rl_nn = row_issue(a, p + 2 * kWaves, re, lane);
     const uint4 stg_n = load_stage(a, row_n, lane);
-    const int pos_n = row_n.ok ? a.positions[(int64_t)(p + kWaves) * kTile + t] : -1;
-    const Row row_nn = load_row(a, p + 2 * kWaves, re);
+    const int pos_n = load_pos(a, row_n, p + kWaves, t);
 
-    // ---- this page's header (in lane 0's 16 bytes of the stage) -----------
+    // ---- this page's header (lane 0's 16 bytes of the stage) --------------
     const int rel = (int)(row_c.page_off & 15);
     uint32_t hw = rel == 0 ? stg_c.x : (rel == 4 ? stg_c.y : (rel == 8 ? stg_c.z : stg_c.w));
     hw = (uint32_t)__builtin_amdgcn_readfirstlane((int)hw);
     const int tid = row_c.ok ? (int)(hw & 0xFF) : 0;
     const int n = min((int)((hw >> 8) & 0xFF), kTile);
+    if (!row_c.ok) pos_c = -1;
     const bool valid = (t < n) && (pos_c >= 0);
 
-    float k[NC][8];
-    if (tid == kDenseTier) {
-      const bool ok = (row_c.th_off & 15) == 0 && row_c.th_off + (int64_t)n * DH * 2 <= a.pages_bytes;
+    // ---- page base phasors e^{i 2pi f_j t_mid} (one per lane) -------------
+    int t_lo = __builtin_amdgcn_readlane(pos_c, 0);
+    int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
+    const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
+    if (lane < NJ) bb[lane] = turn_phasor((double)t_mid * f_lane);
+
+    // ---- locate this page's keys: dense rows, or centroid offsets + radii --
+    const bool dense = tid == kDenseTier;
+    uint4 kd[NC];
+    int cofs[NC];
+    float rh[NC];
+    if (dense) {
+      const bool ok = (row_c.th_off & 15) == 0;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        half8 kv;
-        if (ok && t < n) kv = *reinterpret_cast<const half8*>(a.pages + row_c.th_off + ((int64_t)t * DH + 32 * c + 8 * u) * 2);
-        else for (int s = 0; s < 8; ++s) kv[s] = (_Float16)0.f;
-        for (int s = 0; s < 8; ++s) k[c][s] = (float)kv[s];
+        const int64_t src = row_c.th_off + ((int64_t)t * DH + 32 * c + 8 * u) * 2;
+        kd[c] = (ok && t < n && src + 16 <= a.pages_bytes) ? *reinterpret_cast<const uint4*>(a.pages + src)
+                                                            : uint4{0u, 0u, 0u, 0u};
+        cofs[c] = 0;
+        rh[c] = 0.f;
       }
-    } else if (tid >= 1 && tid <= 3) {
-      if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
-      wave_lds_sync();
-      const int64_t base = row_c.page_off & ~(int64_t)15;
-      const int64_t thr64 = row_c.th_off - base, rdr64 = row_c.rad_off - base;
-      const int g = tier_g(tid), b = tier_b(tid);
-      const int G = DH / g;
-      const bool ok = thr64 >= 0 && rdr64 >= 0 && rdr64 + n * G <= 512 && thr64 + (n * G * b + 7) / 8 + 2 < 512;
-      const int thr = ok ? (int)thr64 : 0, rdr = ok ? (int)rdr64 : 0;
-      if (tid == 1) gather_k<DH, 1>(cb_s, st, rel, thr, rdr, t, u, n, ok, k);
-      else if (tid == 2) gather_k<DH, 2>(cb_s, st, rel, thr, rdr, t, u, n, ok, k);
-      else gather_k<DH, 3>(cb_s, st, rel, thr, rdr, t, u, n, ok, k);
     } else {
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        for (int s = 0; s < 8; ++s) k[c][s] = 0.f;
+      for (int c = 0; c < NC; ++c) { cofs[c] = 0; rh[c] = 0.f; kd[c] = uint4{0u, 0u, 0u, 0u}; }
+      if (tid >= 1 && tid <= 3) {
+        if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
+        wave_lds_sync();
+        const int64_t base = row_c.page_off & ~(int64_t)15;
+        const int64_t thr64 = row_c.th_off - base, rdr64 = row_c.rad_off - base;
+        const int g = tier_g(tid), b = tier_b(tid);
+        const int G = DH / g;
+        const bool ok = thr64 >= 0 && rdr64 >= 0 && rdr64 + n * G <= 512 && thr64 + (n * G * b + 7) / 8 + 2 < 512;
+        const int thr = ok ? (int)thr64 : 0, rdr = ok ? (int)rdr64 : 0;
+        if (tid == 1) locate_k<DH, 1>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+        else if (tid == 2) locate_k<DH, 2>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+        else locate_k<DH, 3>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+      }
     }
+    wave_lds_sync();
 
-    // ---- RoPE: k_rot = R(pos) k_hat, then fp16 B operand -------------------
+    // ---- RoPE per chunk pair (c, c + NP): k_rot = R(pos) k_hat, phasor =
+    //      base(t_mid) * delta(pos - t_mid) -> fp16 MFMA operand -------------
     half8 kb[NC];
     {
-      const double pd = (double)(valid ? pos_c : 0);
+      const int dl = pos_c - t_mid;
+      const int ad = dl < 0 ? -dl : dl;
+      const float sg = dl < 0 ? -1.f : 1.f;
+      const bool near = valid && ad < kDelta;
 #pragma unroll
-      for (int c = 0; c < NP; ++c)
+      for (int c = 0; c < NP; ++c) {
+        float k0[8], k1[8];                      // chunks c and c + NP
+        if (dense) {
+          const half8 h0 = __builtin_bit_cast(half8, kd[c]), h1 = __builtin_bit_cast(half8, kd[c + NP]);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const float ph = (float)__builtin_amdgcn_fract(pd * fturn[c][s]);
-          const float sn = __builtin_amdgcn_sinf(ph);
-          const float cs = __builtin_amdgcn_cosf(ph);
-          const float x0 = k[c][s], x1 = k[c + NP][s];
-          kb[c][s] = (_Float16)(x0 * cs - x1 * sn);
-          kb[c + NP][s] = (_Float16)(x1 * cs + x0 * sn);
+          for (int s = 0; s < 8; ++s) { k0[s] = (float)h0[s]; k1[s] = (float)h1[s]; }
+        } else {
+          const float4* c0 = reinterpret_cast<const float4*>(cb_s + cofs[c]);
+          const float4* c1 = reinterpret_cast<const float4*>(cb_s + cofs[c + NP]);
+          const float4 a0 = c0[0], a1 = c0[1], b0 = c1[0], b1 = c1[1];
+          const float r0 = rh[c], r1 = rh[c + NP];
+          k0[0] = r0 * a0.x; k0[1] = r0 * a0.y; k0[2] = r0 * a0.z; k0[3] = r0 * a0.w;
+          k0[4] = r0 * a1.x; k0[5] = r0 * a1.y; k0[6] = r0 * a1.z; k0[7] = r0 * a1.w;
+          k1[0] = r1 * b0.x; k1[1] = r1 * b0.y; k1[2] = r1 * b0.z; k1[3] = r1 * b0.w;
+          k1[4] = r1 * b1.x; k1[5] = r1 * b1.y; k1[6] = r1 * b1.z; k1[7] = r1 * b1.w;
         }
+        const float4* bq = reinterpret_cast<const float4*>(bb + 32 * c + 8 * u);
+        const float4* dq = reinterpret_cast<const float4*>(&dtab[near ? ad : 0][32 * c + 8 * u]);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          const float4 b2 = bq[s2];              // two base phasors (j, j+1)
+          float zr[2], zi[2];
+          if (near) {
+            const float4 d2 = dq[s2];
+            const float di0 = sg * d2.y, di1 = sg * d2.w;
+            zr[0] = b2.x * d2.x - b2.y * di0; zi[0] = b2.x * di0 + b2.y * d2.x;
+            zr[1] = b2.z * d2.z - b2.w * di1; zi[1] = b2.z * di1 + b2.w * d2.z;
+          } else {
+            const double pd = (double)(valid ? pos_c : 0);
+            const float2 z0 = turn_phasor(pd * ftab[32 * c + 8 * u + 2 * s2]);
+            const float2 z1 = turn_phasor(pd * ftab[32 * c + 8 * u + 2 * s2 + 1]);
+            zr[0] = z0.x; zi[0] = z0.y; zr[1] = z1.x; zi[1] = z1.y;
+          }
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int s = 2 * s2 + e;
+            kb[c][s] = (_Float16)(k0[s] * zr[e] - k1[s] * zi[e]);
+            kb[c + NP][s] = (_Float16)(k1[s] * zr[e] + k0[s] * zi[e]);
+          }
+        }
+      }
     }
+    // ---- S^T = K_rot q^T on MFMA: lane (u, hl) gets head hl, tokens 4u..4u+3
     floatx4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < NC; ++c) S = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], S, 0, 0, 0);
+    for (int c = 0; c < NC; ++c) {
+      const half8 qa = *reinterpret_cast<const half8*>(&q_s[lane & 15][32 * c + 8 * u]);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[c], qa, S, 0, 0, 0);
+    }
 
-    // ---- online softmax (lane row group u holds heads 4u + s, column t) ----
-    float pv[4];
-    float alpha[4];
-    bool any_upd = false;
+    // ---- online softmax over the page, per head, in the log2 domain -------
+    const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
+    float x[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      x[s] = ((vmask >> (4 * u + s)) & 1u) ? S[s] * a.scale_log2 : -INFINITY;
+    const float mx = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+    const bool upd = mx > m_run + kRescaleLog2;
+    const float m_new = upd ? mx : m_run;
+    const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+    half4 pa;
+    float es = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const float x = valid ? S[s] * a.scale_log2 : -INFINITY;
-      float mx = x;
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, shfl_xor(mx, o));
-      const bool upd = mx > m_run[s] + kRescaleLog2;
-      const float m_new = upd ? mx : m_run[s];
-      alpha[s] = upd ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;
-      any_upd |= upd;
-      const float e = (x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x - m_new);
-      const _Float16 e16 = (_Float16)e;
-      float es = (float)e16;
-      pv[s] = es;
-      for (int o = 1; o < 16; o <<= 1) es += shfl_xor(es, o);
-      l_run[s] = alpha[s] * l_run[s] + es;
-      m_run[s] = m_new;
+      const float e = (x[s] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[s] - m_new);
+      pa[s] = (_Float16)e;
+      es += (float)pa[s];
     }
-    if (__ballot(any_upd) != 0) {
+    l_run = alpha * l_run + rows_sum(es);
+    m_run = m_new;
+    if (__ballot(upd) != 0) {
 #pragma unroll
-      for (int mm = 0; mm < NM; ++mm)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[mm][s] *= alpha[s];
+      for (int mm = 0; mm < NM; ++mm) acc[mm] *= alpha;
     }
 
-    // ---- P^T through LDS into the A-operand layout -----------------------
-    if (u < RG) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (4 * u + s < GQA) pb[(4 * u + s) * 16 + t] = (_Float16)pv[s];
-    }
-    wave_lds_sync();
-    const half4 pa = *reinterpret_cast<const half4*>(pb + (lane & 15) * 16 + 4 * u);
-
-    // ---- O += P V on MFMA: B[k = token 4u + i][n = dim 16mm + t] --------
-    const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
+    // ---- O^T += V^T P^T on MFMA: A[i = dim 16mm + t][k = token 4u + i'] ----
 #pragma unroll
     for (int mm = 0; mm < NM; ++mm) {
-      half4 bv = vreg[mm];
+      half4 av = vreg[mm];
       if (vmask != 0xFFFFu)
         for (int i = 0; i < 4; ++i)
-          if (!((vmask >> (4 * u + i)) & 1u)) bv[i] = (_Float16)0.f;
-      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bv, acc[mm], 0, 0, 0);
+          if (!((vmask >> (4 * u + i)) & 1u)) av[i] = (_Float16)0.f;
+      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pa, acc[mm], 0, 0, 0);
     }
+
+    // ---- issue V / dense K of the next page into the freed registers ------
+    load_v<DH>(a, row_n, t, u, vreg);
     wave_lds_sync();
 
-    row_c = row_n; row_n = row_nn; stg_c = stg_n; pos_c = pos_n;
+    row_c = row_n;
+    row_n = row_take(a, rl_nn, p + 2 * kWaves, re);
+    stg_c = stg_n;
+    pos_c = pos_n;
   }
 
   // ---- merge the waves' states in LDS, write this item's partial ----------
@@ -368,14 +508,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
   __syncthreads();
   float* mrg = cb_s;                                  // reuse codebook space: [kWaves][GQA][DH]
   float* mrg_ml = mrg + kWaves * GQA * DH;            // [kWaves][GQA][2]
-  if (u < RG) {
+  if (hl < GQA) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int hh = 4 * u + s;
-      if (hh >= GQA) continue;
-      for (int mm = 0; mm < NM; ++mm) mrg[(wave * GQA + hh) * DH + 16 * mm + t] = acc[mm][s];
-      if (t == 0) { mrg_ml[(wave * GQA + hh) * 2] = m_run[s]; mrg_ml[(wave * GQA + hh) * 2 + 1] = l_run[s]; }
-    }
+    for (int mm = 0; mm < NM; ++mm)
+      *reinterpret_cast<floatx4*>(mrg + (wave * GQA + hl) * DH + 16 * mm + 4 * u) = acc[mm];
+    if (u == 0) { mrg_ml[(wave * GQA + hl) * 2] = m_run; mrg_ml[(wave * GQA + hl) * 2 + 1] = l_run; }
   }
   __syncthreads();
   float* part = a.partials + (int64_t)item * PS;
@@ -395,7 +532,6 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     part[16 + hh * DH + d] = A;
     if (d == 0) { part[hh] = M; part[GQA + hh] = L; }
   }
-
 }
 
 // Log-sum-exp merge of the partials of each (sequence, kv head).  One

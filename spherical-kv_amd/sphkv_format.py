@@ -22,10 +22,11 @@ Two additions, both encoded without changing the header layout:
   aligned theta offsets) so that the decode kernel can use 128-bit loads.  The
   pointer table stores absolute offsets, so placement is free.
 
-V is kept beside the pages in a pool of fp16 V pages laid out token-minor,
-[num_vpages, dh, page_size]: element (d, t) of page v lives at
-((v * dh) + d) * page_size + t.  Row p of the pointer table uses V page
-vslot[p].
+V is kept beside the pages in a pool of fp16 V pages, [num_vpages,
+page_size * dh], each page in the decode kernel's MFMA operand order: element
+(token k, dim d) with d = 16*mm + t and k = 4*u + i lives at
+((t*4 + u) * (dh/16) + mm) * 4 + i within its page (see v_page_index).  Row p
+of the pointer table uses V page vslot[p].
 """
 from __future__ import annotations
 
@@ -191,6 +192,15 @@ def plan_pages(tier_of: Sequence[np.ndarray], positions_of: Optional[Sequence[np
                     count=count, tokens=tokens, positions=positions, seq_head=seq_head,
                     row_start=np.asarray(row_start, np.int32), ptable=ptable.astype(np.int32),
                     vslot=vslot, pages_bytes=int(pages_bytes), num_vpages=nv)
+
+
+def v_page_index(dh: int) -> np.ndarray:
+    """[16, dh] int: position of element (token k, dim d) inside a V page."""
+    k = np.arange(16)[:, None]
+    d = np.arange(dh)[None, :]
+    mm, t = d // 16, d % 16
+    u, i = k // 4, k % 4
+    return ((t * 4 + u) * (dh // 16) + mm) * 4 + i
 
 
 def rope_inv_freq(dh: int, theta: float) -> np.ndarray:

@@ -116,7 +116,7 @@ class PagedPool:
     ptable: torch.Tensor       # int32 [P, 3]
     vslot: torch.Tensor        # int32 [P]
     positions: torch.Tensor    # int32 [P, 16]
-    v_pool: torch.Tensor       # fp16 [num_vpages, dh, 16]
+    v_pool: torch.Tensor       # fp16 [num_vpages, 16 * dh] (MFMA operand order)
     codebooks: Dict[int, torch.Tensor]   # tier -> fp32 [num_kv, G, C, g]
     work: torch.Tensor         # int32 [n_items, 3]
     work_start: torch.Tensor   # int32 [num_seqs*num_kv + 1]
@@ -157,7 +157,7 @@ class PagedPool:
             ptable=torch.as_tensor(plan.ptable, device=dev),
             vslot=torch.as_tensor(plan.vslot, device=dev),
             positions=torch.as_tensor(plan.positions, device=dev),
-            v_pool=torch.zeros((plan.num_vpages, plan.dh, plan.page_size), dtype=torch.float16, device=dev),
+            v_pool=torch.zeros((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
             codebooks=cbs,
             work=torch.as_tensor(work, device=dev),
             work_start=torch.as_tensor(ws, device=dev),

@@ -119,7 +119,7 @@ def test_decode_masked_positions(gpu):
             ang = pos[p, keep][:, None].astype(np.float64) * inv[None]
             ang = np.concatenate([ang, ang], 1)
             lg.append(oracle.mode_b_logits(qh, None, np.cos(ang), np.sin(ang), cw, r_hat[keep], None, 4, 16))
-            vs.append(cpu["v_pool"][plan2.vslot[p], :, keep].astype(np.float64))
+            vs.append(oracle.v_page_rows(cpu["v_pool"], plan2.vslot[p], n, wl.dh)[keep].astype(np.float64))
         lgc = np.concatenate(lg, 1)
         e = np.exp(lgc - lgc.max(1, keepdims=True))
         want[0, h * wl.gqa:(h + 1) * wl.gqa] = (e / e.sum(1, keepdims=True)) @ np.concatenate(vs, 0)

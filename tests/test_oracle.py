@@ -163,7 +163,7 @@ def _textbook(wl, pool):
                 cb = wl.codebooks[tid][h].astype(np.float64)
                 k = (cb[np.arange(G)[None, :], codes] * r_hat[..., None]).reshape(n, wl.dh)
             keys.append(k)
-            vals.append(pool["v_pool"][plan.vslot[p], :, :n].T.astype(np.float64))
+            vals.append(oracle.v_page_rows(pool["v_pool"], plan.vslot[p], n, wl.dh).astype(np.float64))
             poss.append(plan.positions[p, :n].astype(np.float64))
         K, V, pos = np.concatenate(keys), np.concatenate(vals), np.concatenate(poss)
         q = wl.q[s, h * wl.gqa:(h + 1) * wl.gqa].astype(np.float64)
