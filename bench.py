@@ -34,6 +34,7 @@ import sphkv_synth as synth  # noqa: E402
 PEAK_HBM_GBPS = 8000.0
 METRIC = "µs/decode step + achieved HBM GB/s (compressed KV), 8B shape, 32K ctx, 1 GPU"
 ROTATE = 6
+COPY_BYTES = 256 << 20
 
 
 def log(msg):
@@ -43,6 +44,19 @@ def log(msg):
 def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
     """An independent copy of the KV bytes (pages and V) at new addresses."""
     return ops.PagedPool(**{**pool.__dict__, "pages": pool.pages.clone(), "v_pool": pool.v_pool.clone()})
+
+
+# HBM bytes per decode_kernel launch from rocprofv3 counters on MI355X:
+# (FETCH_SIZE * 2 + WRITE_SIZE) KiB per dispatch.  On this part FETCH_SIZE
+# reads exactly half of a plain device copy's bytes (256 MiB copy -> 131083
+# KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
+# with `bench.py --calibrate`; re-measured whenever the kernel changes.
+TRAFFIC_BYTES = {}
+
+
+def measured_traffic(config, layout):
+    v = TRAFFIC_BYTES.get((config, layout))
+    return None if v is None else int(v)
 
 
 def cpu_baseline(wl, pool: ops.PagedPool, budget_s: float = 20.0):
@@ -90,6 +104,9 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
                     help="page placement: the config's own (random for configs 2-5) or sequential")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="after timing, run plain device copies of COPY_BYTES (torch copy_), the "
+                         "reference kernel of known traffic for FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the decode "
@@ -127,6 +144,29 @@ def main():
     gbps = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
 
+    # the dominant kernel alone: the same steps' first phase (partials), timed
+    # with HIP events on the stream it runs on
+    for i in range(args.warmup):
+        ops.decode_paged_partials(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, ws)
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record()
+    for i in range(args.steps):
+        ops.decode_paged_partials(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, ws)
+    k1.record()
+    torch.cuda.synchronize()
+    kern_ms = k0.elapsed_time(k1) / args.steps
+    kern_gbps = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"[bench] decode_kernel alone {kern_ms * 1e3:.2f} us  {kern_gbps:.1f} GB/s")
+
+    if args.calibrate:
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration: 4 device copies of {COPY_BYTES} bytes")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (torch restatement of the reference path)")
@@ -143,9 +183,11 @@ def main():
                                f"{wl.num_seqs} seq x {max(wl.lengths)} ctx, 16-token pages, tier mix of BASELINE",
                    "num_seqs": wl.num_seqs, "ctx": max(wl.lengths), "pages": wl.plan.num_rows,
                    "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "decode_kernel (one launch per step)"},
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": measured_traffic(args.config, args.layout),
+                     "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
+                     "step_frac": round(gbps / PEAK_HBM_GBPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -119,6 +119,36 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
                        void* stream);
 
 /*
+ * The two phases of sphkv_decode_paged as separate calls, for callers that
+ * combine partials themselves (a context split over several devices, each
+ * merging the gathered partials) or time the phases apart.  No reference
+ * counterpart: the reference's Mode-A split/reduce pair
+ * (decode_kernel.cu:108-246) is internal to its single entry point.
+ *
+ * sphkv_decode_paged_partials: the arguments of sphkv_decode_paged without
+ * the output; writes one partial per work item into the workspace:
+ *   float [num_items][16 + gqa*dh]: m[gqa], l[gqa], 16 - 2*gqa unused,
+ *   acc[gqa][dh];  m = running max of logit * sm_scale * log2(e) (log2
+ *   domain, -inf for an empty item), l = sum of 2^(s - m), acc = sum of
+ *   2^(s - m) * V (unnormalised).
+ * sphkv_decode_merge_partials: out[seq, head*gqa + i, :] = sum_items
+ *   2^(m - M) acc / sum_items 2^(m - M) l over the items of work_start's
+ *   ranges (zeros where every item is empty).
+ */
+int sphkv_decode_paged_partials(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                                const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                                const uint16_t* v_pool, int64_t num_vpages,
+                                const float* cb1, const float* cb2, const float* cb3,
+                                const int32_t* work, int32_t num_items, const int32_t* work_start,
+                                int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                                const uint16_t* q, void* workspace, int64_t workspace_bytes,
+                                int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                                void* stream);
+int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, int32_t num_items,
+                                const int32_t* work_start, int32_t num_seqs, int32_t num_kv,
+                                int32_t gqa, int32_t dh, uint16_t* out, void* stream);
+
+/*
  * Logits-only ragged kernel with the contract of the reference's missing
  * fused_decode_ragged (call sites spherical_kv_pipeline.py:1102-1125,
  * :1865-1870, :1906-1910): pages of one tier, RoPE from the caller's HF-layout

@@ -69,6 +69,46 @@ int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32
   return (int64_t)num_items * sphkv::partial_floats(gqa, dh) * (int64_t)sizeof(float);
 }
 
+}  // extern "C"
+
+namespace {
+
+int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_bytes,
+                const int32_t* ptable, const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                const uint16_t* v_pool, int64_t num_vpages, const float* cb1, const float* cb2,
+                const float* cb3, const int32_t* work, int32_t num_items, const int32_t* work_start,
+                int32_t num_seqs, int32_t num_kv, int32_t gqa, const uint16_t* q, uint16_t* out,
+                void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size,
+                float sm_scale, double rope_theta, void* stream) {
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (!gqa_ok(gqa)) return fail(SPHKV_EINVAL, "%s: gqa must be 1, 2, 4 or 8 (got %d)", fn, gqa);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
+  if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || num_rows < 0)
+    return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if ((phases & sphkv::kPhasePartials) && !(rope_theta > 1.0))
+    return fail(SPHKV_EINVAL, "%s: rope_theta must be > 1", fn);
+  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
+  if (workspace_bytes < need)
+    return fail(SPHKV_EINVAL, "%s: workspace too small (%lld < %lld bytes)", fn,
+                (long long)workspace_bytes, (long long)need);
+  if (num_seqs == 0) return ok();
+  if (num_items < num_seqs * num_kv)
+    return fail(SPHKV_EINVAL, "%s: need at least one work item per (seq, head)", fn);
+  if (!work_start || !workspace) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  if ((phases & sphkv::kPhaseMerge) && !out) return fail(SPHKV_EINVAL, "%s: null output", fn);
+  if ((phases & sphkv::kPhasePartials) &&
+      (!q || !work || !pages || !ptable || !vslot || !positions || !v_pool))
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::DecodeLaunch L{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
+                        cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q, out,
+                        static_cast<float*>(workspace), dh, sm_scale, rope_theta};
+  return launch_status(sphkv::launch_decode(L, phases, (hipStream_t)stream), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
 int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
                        const int32_t* vslot, const int32_t* positions, int32_t num_rows,
                        const uint16_t* v_pool, int64_t num_vpages,
@@ -78,24 +118,34 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
                        const uint16_t* q, uint16_t* out, void* workspace, int64_t workspace_bytes,
                        int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
                        void* stream) {
-  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: dh must be 64 or 128 (got %d)", dh);
-  if (!gqa_ok(gqa)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: gqa must be 1, 2, 4 or 8 (got %d)", gqa);
-  if (page_size != 16) return fail(SPHKV_EINVAL, "sphkv_decode_paged: page_size must be 16 (got %d)", page_size);
-  if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || num_rows < 0)
-    return fail(SPHKV_EINVAL, "sphkv_decode_paged: negative size");
-  if (!(rope_theta > 1.0)) return fail(SPHKV_EINVAL, "sphkv_decode_paged: rope_theta must be > 1");
-  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
-  if (workspace_bytes < need)
-    return fail(SPHKV_EINVAL, "sphkv_decode_paged: workspace too small (%lld < %lld bytes)",
-                (long long)workspace_bytes, (long long)need);
-  if (num_seqs == 0) return ok();
-  if (!q || !out || !work_start || (num_items > 0 && (!work || !workspace || !pages || !ptable ||
-                                                      !vslot || !positions || !v_pool)))
-    return fail(SPHKV_EINVAL, "sphkv_decode_paged: null pointer argument");
-  sphkv::DecodeLaunch L{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
-                        cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q, out,
-                        static_cast<float*>(workspace), dh, sm_scale, rope_theta};
-  return launch_status(sphkv::launch_decode(L, (hipStream_t)stream), "sphkv_decode_paged");
+  return decode_call("sphkv_decode_paged", sphkv::kPhasePartials | sphkv::kPhaseMerge, pages, pages_bytes,
+                     ptable, vslot, positions, num_rows, v_pool, num_vpages, cb1, cb2, cb3, work,
+                     num_items, work_start, num_seqs, num_kv, gqa, q, out, workspace, workspace_bytes,
+                     dh, page_size, sm_scale, rope_theta, stream);
+}
+
+int sphkv_decode_paged_partials(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                                const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                                const uint16_t* v_pool, int64_t num_vpages,
+                                const float* cb1, const float* cb2, const float* cb3,
+                                const int32_t* work, int32_t num_items, const int32_t* work_start,
+                                int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                                const uint16_t* q, void* workspace, int64_t workspace_bytes,
+                                int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                                void* stream) {
+  return decode_call("sphkv_decode_paged_partials", sphkv::kPhasePartials, pages, pages_bytes, ptable,
+                     vslot, positions, num_rows, v_pool, num_vpages, cb1, cb2, cb3, work, num_items,
+                     work_start, num_seqs, num_kv, gqa, q, nullptr, workspace, workspace_bytes, dh,
+                     page_size, sm_scale, rope_theta, stream);
+}
+
+int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, int32_t num_items,
+                                const int32_t* work_start, int32_t num_seqs, int32_t num_kv,
+                                int32_t gqa, int32_t dh, uint16_t* out, void* stream) {
+  return decode_call("sphkv_decode_merge_partials", sphkv::kPhaseMerge, nullptr, 0, nullptr, nullptr,
+                     nullptr, 0, nullptr, 0, nullptr, nullptr, nullptr, nullptr, num_items, work_start,
+                     num_seqs, num_kv, gqa, nullptr, out, const_cast<void*>(workspace), workspace_bytes,
+                     dh, 16, 1.f, 0.0, stream);
 }
 
 int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,

@@ -1,39 +1,44 @@
 // Angle-domain paged attention decode (gfx950).
 //
-// Work decomposition: one workgroup (8 waves) per work item = a contiguous
-// range of pointer-table rows of one (sequence, kv head).  The workgroup
-// stages that head's tier codebooks in LDS once; each wave walks every 8th
-// page of the range with its own online-softmax state; the eight states are
-// merged in LDS and written as one (m, l, acc) partial.  A second, widely
-// parallel kernel merges the partials of each (sequence, kv head) (log-sum-exp)
-// and writes the fp16 output.  (Merging in the last-arriving workgroup needs an
-// agent-scope release fence per workgroup, which writes back the XCD's L2 and
-// measured tens of microseconds on MI355X.)
+// Work decomposition: one workgroup (kWaves waves) per work item = a
+// contiguous range of pointer-table rows of one (sequence, kv head).  The
+// workgroup stages that head's tier codebooks and the RoPE tables in LDS once;
+// each wave walks every kWaves-th page of the range with its own online-softmax
+// state; the states are merged in LDS and written as one (m, l, acc) partial.
+// A second, widely parallel kernel merges the partials of each (sequence, kv
+// head) (log-sum-exp) and writes the fp16 output.  (Merging in the
+// last-arriving workgroup needs an agent-scope release fence per workgroup,
+// which writes back the XCD's L2 and measured tens of microseconds on MI355X.)
 //
 // Page loop, software pipelined per wave: while page p is computed, the
-// 512-byte staging window and positions of the wave's next page and the
-// pointer-table row of the one after are in flight, and V of page p is loaded
-// before its K math.
+// 512-byte staging window and positions of the wave's next page, its V and
+// (dense pages) its K rows, and the pointer-table row of the one after are in
+// flight.
 //
-// Per page (16 tokens), lane l = (token t = l % 16, quarter u = l / 16):
-//   1. reconstruct k_hat for dims d = 32c + 8u + s (c < DH/32, s < 8):
+// Per page (16 tokens, positions pos_t), lane l = (token t = l % 16, quarter
+// u = l / 16), page centre t_mid = (min pos + max pos) / 2:
+//   1. the query rows are rotated once per page by -t_mid (fp32, lanes = RoPE
+//      frequencies j) and kept in LDS as hi + lo fp16 halves;
+//   2. k_hat of token t on this lane's 32 dimensions (chunk_dim):
 //      compressed  k_hat_d = r_hat_g * centroid_g[code][d mod g],
 //                  r_hat_g = int8 / 127 * scale_g         (pagebuilder.py:17-21)
-//      dense       k_hat_d = K[t][d] (fp16)
-//   2. rotate by the token's RoPE angle: k_rot = R(pos) k_hat.  The RoPE pair
-//      (j, j + DH/2) lives in chunks c and c + DH/64 of the same lane.
-//      <R(-pos) q, k_hat> = <q, R(pos) k_hat>, so this equals the reference's
-//      back-rotated query (spherical_kv_pipeline.py:2143-2176; its clip of the
-//      cosine to [-1, 1] only acts on rounding error).  The phase pos * f_j is
-//      formed in fp64 and reduced to [0, 1) turns before the fp32 sin / cos.
-//   3. S[h][t] = q_h . k_rot on MFMA (16x16x32 f16): A = q rows (fp16 input,
-//      exact), B = k_rot rounded to fp16 (relative error 2^-11 per element).
-//   4. online softmax in the log2 domain.  The running reference max of a head
+//      dense       k_hat_d = K[t][d] (fp16);
+//   3. k_rot = R(pos_t - t_mid) k_hat in fp32 with phasors from an LDS table
+//      of e^{i 2 pi f_j d}, |d| < kDelta (formed directly beyond), split as
+//      hi + lo fp16.  Since <R(-pos) q, k_hat> = <R(-t_mid) q, R(pos - t_mid)
+//      k_hat>, this is the reference's back-rotated query
+//      (spherical_kv_pipeline.py:2143-2176; its clip of the cosine to [-1, 1]
+//      only acts on rounding error).  Phases are formed in fp64 turns and
+//      reduced to [0, 1) before the fp32 hardware sine / cosine;
+//   4. S[h][t] = q_rot_h . k_rot on MFMA (16x16x32 f16) as hi*hi + lo*hi +
+//      hi*lo: about fp32 accuracy whatever the logit scale;
+//   5. online softmax in the log2 domain.  The running reference max of a head
 //      only moves when a page's max exceeds it by more than 2^8, so the
 //      accumulator rescale is rare; p = 2^(s - m) <= 256 is rounded to fp16 and
 //      the same rounded p is summed into l, so the output stays an exact
-//      convex combination of V rows.
-//   5. O[h][d] += P[h][t] V[t][d] on MFMA (16x16x16 f16), V read token-minor.
+//      convex combination of V rows;
+//   6. O[h][d] += P[h][t] V[t][d] on MFMA (16x16x16 f16), V read in the
+//      pool's MFMA operand order.
 #include "sphkv_common.h"
 #include "sphkv_internal.h"
 
@@ -57,18 +62,6 @@ struct DecodeArgs {
   int32_t num_rows;
   float scale_log2;      // sm_scale * log2(e)
   double log2_theta;
-};
-
-// Codebooks in LDS: rows padded by 4 floats (g=16 -> 20, g=32 -> 36) so that
-// rows of random codes start in different 16-byte bank slots.
-template <int DH>
-struct CbLayout {
-  __host__ __device__ static constexpr int pad(int g) { return g + 4; }
-  static constexpr int n1 = (DH / 16) * 64 * 20;   // tier 1 [G][64][20]
-  static constexpr int n2 = (DH / 16) * 16 * 20;   // tier 2 [G][16][20]
-  static constexpr int n3 = (DH / 32) * 8 * 36;    // tier 3 [G][8][36]
-  static constexpr int total = n1 + n2 + n3;
-  __host__ __device__ static constexpr int off(int tid) { return tid == 3 ? n1 + n2 : (tid == 2 ? n1 : 0); }
 };
 
 constexpr float kRescaleLog2 = 8.0f;   // reference-max hysteresis (log2 units)
@@ -154,13 +147,84 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int t,
   }
 }
 
-// Codes and radii of this lane's NC chunks from the staged page (LDS).
-template <int DH, int TID>
-__device__ __forceinline__ void unpack_page(const uint8_t* st, int rel, int thr, int rdr, int t, int u,
-                                            int n, bool ok, int* code, float* rh) {
-  constexpr int NC = DH / 32;
-  constexpr int g = tier_g(TID), b = tier_b(TID);
+// Dimension of element s of chunk c for lane quarter u.  A lane's chunks
+// cover two runs of DH/8 dimensions: [(DH/8)u, (DH/8)(u+1)) of the first RoPE
+// half (chunks c < NP) and the same run of the second half (chunks c >= NP),
+// so every RoPE pair (j, j + DH/2) lies in one lane and a lane touches exactly
+// two codebook groups.  The QK MFMA's reduction index follows this order on
+// both operands.
+template <int DH>
+__host__ __device__ constexpr int chunk_dim(int c, int u) {
+  return (c >= DH / 64 ? DH / 2 : 0) + (DH / 8) * u + 8 * (c % (DH / 64));
+}
+
+// Dense K rows of a page (fp16 [n][DH] at th_off, 16-byte aligned): lane
+// (t, u) loads chunks c = 0..NC-1 (dims chunk_dim(c, u) .. +8) of token t.  The
+// resource covers the page's theta section only when the pointer-table row
+// describes a dense page, so compressed pages cost no traffic here.
+template <int DH>
+__device__ __forceinline__ void load_dense(const DecodeArgs& a, const Row& r, int t, int u, uint4 (&kd)[DH / 32]) {
+  const bool dense = row_looks_dense<DH>(r);
+  const int64_t room = a.pages_bytes - r.th_off;
+  const int64_t len = r.rad_off - r.th_off;
+  const int64_t nb = dense ? (len < room ? len : room) : 0;
+  const rsrc_t rs = make_rsrc(a.pages + (dense ? r.th_off : 0), nb);
+#pragma unroll
+  for (int c = 0; c < DH / 32; ++c) {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, (t * DH + chunk_dim<DH>(c, u)) * 2, 0, 0);
+    kd[c] = uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
+  }
+}
+
+constexpr int kWaves = 12;             // waves per decode workgroup (3 per SIMD)
+constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| < kDelta
+
+__host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
+
+// LDS of one decode workgroup (byte offsets).
+//  * codebooks of the work item's kv head, fp32, [G][C][g + 4] per tier (rows
+//    padded by 16 bytes so rows of random codes start in different banks);
+//  * delta-phasor table, row d = |pos - page centre|: for each block of 4
+//    RoPE frequencies j, 4 x cos(2 pi f_j d) then 4 x sin(2 pi f_j d), fp32,
+//    rows padded by 16 bytes;
+//  * f_j in turns per token (fp64);
+//  * per wave: the 512-byte staging window of its page, and the query rows
+//    rotated to the page centre split as hi + lo fp16 ([2][GQA][DH + 8]).
+template <int DH, int GQA>
+struct DecodeLds {
+  static constexpr int NJ = DH / 2;
+  __host__ __device__ static constexpr int cb_pad(int g) { return g + 4; }
+  static constexpr int cb_n1 = (DH / 16) * 64 * 20;
+  static constexpr int cb_n2 = (DH / 16) * 16 * 20;
+  static constexpr int cb_n3 = (DH / 32) * 8 * 36;
+  __host__ __device__ static constexpr int cb_off(int tid) {   // floats
+    return tid == 3 ? cb_n1 + cb_n2 : (tid == 2 ? cb_n1 : 0);
+  }
+  static constexpr int drow = NJ * 8 + 16;                       // bytes
+  static constexpr int qrow = DH + 8;                            // halves
+  static constexpr int o_cb = 0;
+  static constexpr int o_dtab = align16(4 * (cb_n1 + cb_n2 + cb_n3));
+  static constexpr int o_ftab = o_dtab + kDelta * drow;
+  static constexpr int o_stage = o_ftab + NJ * 8;
+  static constexpr int o_qr = o_stage + kWaves * 512;
+  static constexpr int qr_wave = 2 * GQA * qrow;                 // halves per wave
+  static constexpr int total = o_qr + kWaves * qr_wave * 2;
+  // the end-of-item wave merge reuses the space: [kWaves][GQA][DH] acc,
+  // [kWaves][GQA][2] (m, l), [GQA][kWaves] weights
+  static constexpr int merge_bytes = kWaves * GQA * (DH + 3) * 4;
+  static_assert(merge_bytes <= total, "merge buffer exceeds the workgroup's LDS");
+  static_assert(total <= 160 * 1024, "LDS budget");
+};
+
+// This lane's two codebook groups (one per RoPE half) of token t on a staged
+// compressed page: LDS offset (floats) of the centroid run the lane needs and
+// the radius r_hat = int8 / 127 * scale (pagebuilder.py:17-21).
+template <int DH, int GQA, int TID>
+__device__ __forceinline__ void locate_k(const uint8_t* st, int rel, int thr, int rdr, int t, int u, int n,
+                                         bool ok, int (&cofs)[2], float (&rh)[2]) {
+  constexpr int g = tier_g(TID), b = tier_b(TID), C = tier_C(TID);
   constexpr int G = DH / g;
+  using L = DecodeLds<DH, GQA>;
   const bool live = ok && t < n;
   uint64_t bits = 0;
   uint32_t rad[2] = {0u, 0u};
@@ -190,38 +254,30 @@ __device__ __forceinline__ void unpack_page(const uint8_t* st, int rel, int thr,
     }
   }
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int gi = (32 * c + 8 * u) / g;
-    code[c] = (int)((bits >> (gi * b)) & ((1u << b) - 1));
+  for (int hf = 0; hf < 2; ++hf) {
+    const int d0 = hf * (DH / 2) + (DH / 8) * u;
+    const int gi = d0 / g, off = d0 - gi * g;
+    const int code = (int)((bits >> (gi * b)) & ((1u << b) - 1));
     const int rc = (int)(int8_t)((rad[gi >> 2] >> (8 * (gi & 3))) & 0xFFu);
     const float sc = live ? *reinterpret_cast<const float*>(st + rel + kHeaderBytes + 4 * gi) : 0.f;
-    rh[c] = (float)rc * sc * (1.0f / 127.0f);
+    rh[hf] = (float)rc * sc * (1.0f / 127.0f);
+    cofs[hf] = L::cb_off(TID) + (gi * C + code) * L::cb_pad(g) + off;
   }
 }
-
-// LDS offset (floats) of the centroid chunk a lane needs for chunk c, and
-// the radius factor, for every chunk of the page.
-template <int DH, int TID>
-__device__ __forceinline__ void locate_k(const uint8_t* st, int rel, int thr, int rdr, int t, int u, int n,
-                                         bool ok, int (&cofs)[DH / 32], float (&rh)[DH / 32]) {
-  constexpr int NC = DH / 32;
-  constexpr int g = tier_g(TID), C = tier_C(TID);
-  int code[NC];
-  unpack_page<DH, TID>(st, rel, thr, rdr, t, u, n, ok, code, rh);
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int d0 = 32 * c + 8 * u;
-    const int gi = d0 / g, off = d0 - gi * g;
-    cofs[c] = CbLayout<DH>::off(TID) + (gi * C + code[c]) * CbLayout<DH>::pad(g) + off;
-  }
-}
-
-constexpr int kWaves = 12;             // waves per decode workgroup (3 per SIMD)
-constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| <= 63
 
 // Partial of one work item: [16 floats: m[GQA], l[GQA], pad] [acc: GQA * DH]
 template <int DH, int GQA>
 __host__ __device__ constexpr int partial_stride() { return 16 + GQA * DH; }
+
+// Work item of workgroup b.  Workgroups are dispatched to the 8 XCDs round
+// robin (b mod 8); consecutive items belong to the same (sequence, kv head),
+// so this mapping gives each XCD a contiguous block of items and its L2 the
+// codebooks of few heads.
+__device__ __forceinline__ int xcd_item(int b, int nb) {
+  const int full = nb & ~7;
+  if (b >= full) return b;
+  return (b & 7) * (full >> 3) + (b >> 3);
+}
 
 // Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
 // with the gfx950 row-swap instructions (VALU, no LDS round trip).
@@ -258,23 +314,44 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
   return float2{__builtin_amdgcn_cosf(ph), __builtin_amdgcn_sinf(ph)};
 }
 
+// x = hi + lo with hi, lo fp16: hi = x rounded toward zero (v_cvt_pkrtz), lo =
+// fp16(x - hi) formed by one mixed-precision FMA (fp32 x, fp16 hi) that
+// writes one half of the packed result.  The pair carries x to about 2^-22
+// relative, so products on the fp16 MFMA lose nothing that matters against
+// the 2e-3 tolerance.
+__device__ __forceinline__ uint32_t pk_rtz(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+__device__ __forceinline__ uint32_t pk_rest(float a, float b, uint32_t hi) {
+  uint32_t d = 0;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "+v"(d) : "v"(a), "v"(hi));
+  asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(d) : "v"(b), "v"(hi));
+  return d;
+}
+__device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8& lo) {
+  uint4 h, l;
+  h.x = pk_rtz(x[0], x[1]); h.y = pk_rtz(x[2], x[3]); h.z = pk_rtz(x[4], x[5]); h.w = pk_rtz(x[6], x[7]);
+  l.x = pk_rest(x[0], x[1], h.x); l.y = pk_rest(x[2], x[3], h.y);
+  l.z = pk_rest(x[4], x[5], h.z); l.w = pk_rest(x[6], x[7], h.w);
+  hi = __builtin_bit_cast(half8, h);
+  lo = __builtin_bit_cast(half8, l);
+}
+
 template <int DH, int GQA>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeArgs a) {
   constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
   constexpr int NP = NC / 2;         // chunks holding the first RoPE half
   constexpr int NM = DH / 16;        // PV MFMA blocks
   constexpr int NJ = DH / 2;         // RoPE frequencies
-  using CB = CbLayout<DH>;
-  __shared__ __attribute__((aligned(16))) float cb_s[CB::total];
-  __shared__ __attribute__((aligned(16))) float2 dtab[kDelta][NJ + 2]; // e^{i 2pi f_j d}; rows padded 16 B
-  __shared__ __attribute__((aligned(16))) double ftab[NJ];             // f_j in turns per token
-  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][512];
-  __shared__ __attribute__((aligned(16))) float2 bbuf[kWaves][NJ];     // page base phasors
-  __shared__ __attribute__((aligned(16))) _Float16 q_s[16][DH];        // q rows (rows >= GQA zero)
+  using L = DecodeLds<DH, GQA>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[L::total];
+  float* cb_s = reinterpret_cast<float*>(smem + L::o_cb);
+  const uint8_t* dtab = smem + L::o_dtab;
+  double* ftab = reinterpret_cast<double*>(smem + L::o_ftab);
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  const int item = blockIdx.x;
+  const int item = xcd_item(blockIdx.x, gridDim.x);
   const int sh = a.work[3 * item];
   const int rb = a.work[3 * item + 1];
   const int re = min(a.work[3 * item + 2], a.num_rows);
@@ -282,35 +359,79 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   const int seq = sh / a.num_kv;
   const int t = lane & 15;
   const int u = lane >> 4;
+  uint8_t* st = smem + L::o_stage + wave * 512;
+  _Float16* qr = reinterpret_cast<_Float16*>(smem + L::o_qr) + wave * L::qr_wave;   // [hi, lo][GQA][qrow]
 
   int p = rb + wave;
-  // ---- shared tables: codebooks, RoPE frequencies, delta phasors ---------
-  for (int tid = 1; tid <= 3; ++tid) {
-    const float* src = a.cb[tid];
-    if (!src) continue;
-    const int g = tier_g(tid), gp = CB::pad(g);
-    const int rows = (DH / g) * tier_C(tid);
-    const float4* s4 = reinterpret_cast<const float4*>(src + (int64_t)h * rows * g);
-    float* dst = cb_s + CB::off(tid);
-    for (int i = threadIdx.x; i < rows * g / 4; i += kWaves * 64) {
-      const int r = (4 * i) / g, col = (4 * i) % g;
-      *reinterpret_cast<float4*>(dst + r * gp + col) = s4[i];
+  // ---- first pages' pointer-table rows, then the shared tables' loads ----
+  RowLd rl_c = row_issue(a, p, re, lane);
+  RowLd rl_n = row_issue(a, p + kWaves, re, lane);
+  RowLd rl_2 = row_issue(a, p + 2 * kWaves, re, lane);
+  // codebooks: every load of a thread is issued before its first LDS store
+  constexpr int kT = kWaves * 64;
+  constexpr int n4_1 = L::cb_n1 / 20 * 4, n4_2 = L::cb_n2 / 20 * 4, n4_3 = L::cb_n3 / 36 * 8;  // float4s
+  constexpr int k1 = (n4_1 + kT - 1) / kT, k2 = (n4_2 + kT - 1) / kT, k3 = (n4_3 + kT - 1) / kT;
+  floatx4 cbv[k1 + k2 + k3];
+  {
+    int slot = 0;
+#pragma unroll
+    for (int tid = 1; tid <= 3; ++tid) {
+      const int g = tier_g(tid), rows = (DH / g) * tier_C(tid);
+      const int nf4 = rows * g / 4;
+      const rsrc_t rs = make_rsrc(a.cb[tid] ? a.cb[tid] + (int64_t)h * rows * g : nullptr, a.cb[tid] ? nf4 * 16 : 0);
+      const int kk = tid == 1 ? k1 : (tid == 2 ? k2 : k3);
+#pragma unroll
+      for (int k = 0; k < kk; ++k) {
+        const int i = threadIdx.x + k * kT;
+        cbv[slot++] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, i < nf4 ? 16 * i : kOOB, 0, 0));
+      }
+    }
+  }
+  // this lane's query pair (j, j + NJ) of every head of the item, fp32
+  float qv0[GQA], qv1[GQA];
+  {
+    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+    const int j = lane % NJ;
+#pragma unroll
+    for (int hh = 0; hh < GQA; ++hh) {
+      qv0[hh] = (float)qh[hh * DH + j];
+      qv1[hh] = (float)qh[hh * DH + j + NJ];
+    }
+  }
+  // first page's data and the next page's row
+  Row row_c = row_take(a, rl_c, p, re);
+  uint4 stg_c = load_stage(a, row_c, lane);
+  int pos_c = load_pos(a, row_c, p, t);
+  half4 vreg[NM];
+  load_v<DH>(a, row_c, t, u, vreg);
+  uint4 kd[NC];
+  load_dense<DH>(a, row_c, t, u, kd);
+  Row row_n = row_take(a, rl_n, p + kWaves, re);
+  {
+    int slot = 0;
+#pragma unroll
+    for (int tid = 1; tid <= 3; ++tid) {
+      const int g = tier_g(tid), gp = L::cb_pad(g), rows = (DH / g) * tier_C(tid);
+      const int nf4 = rows * g / 4;
+      float* dst = cb_s + L::cb_off(tid);
+      const int kk = tid == 1 ? k1 : (tid == 2 ? k2 : k3);
+#pragma unroll
+      for (int k = 0; k < kk; ++k) {
+        const int i = threadIdx.x + k * kT;
+        if (i < nf4) *reinterpret_cast<floatx4*>(dst + ((4 * i) / g) * gp + (4 * i) % g) = cbv[slot];
+        ++slot;
+      }
     }
   }
   if (threadIdx.x < NJ)
     ftab[threadIdx.x] = exp2(-(2.0 * threadIdx.x / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
   __syncthreads();
-  for (int i = threadIdx.x; i < kDelta * NJ; i += kWaves * 64)
-    dtab[i / NJ][i % NJ] = turn_phasor((double)(i / NJ) * ftab[i % NJ]);
-  {
-    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
-    for (int i = threadIdx.x; i < 16 * DH / 8; i += kWaves * 64) {
-      const int r = i / (DH / 8), c8 = i % (DH / 8);
-      half8 v;
-      if (r < GQA) v = *reinterpret_cast<const half8*>(qh + r * DH + 8 * c8);
-      else for (int s = 0; s < 8; ++s) v[s] = (_Float16)0.f;
-      *reinterpret_cast<half8*>(&q_s[r][8 * c8]) = v;
-    }
+  for (int i = threadIdx.x; i < kDelta * NJ; i += kT) {
+    const int d = i / NJ, j = i % NJ;
+    const float2 z = turn_phasor((double)d * ftab[j]);
+    float* row = reinterpret_cast<float*>(const_cast<uint8_t*>(dtab) + d * L::drow) + (j >> 2) * 8;
+    row[j & 3] = z.x;
+    row[4 + (j & 3)] = z.y;
   }
   const double f_lane = ftab[lane % NJ];
   __syncthreads();
@@ -318,24 +439,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   // no wait inside the loop has to account for it
   __builtin_amdgcn_s_waitcnt(0);
 
-  // ---- pipeline prologue: rows of the first two pages, data of the first --
-  Row row_c = row_take(a, row_issue(a, p, re, lane), p, re);
-  RowLd rl_n = row_issue(a, p + kWaves, re, lane);
-  uint4 stg_c = load_stage(a, row_c, lane);
-  int pos_c = load_pos(a, row_c, p, t);
-  half4 vreg[NM];
-  load_v<DH>(a, row_c, t, u, vreg);
-  Row row_n = row_take(a, rl_n, p + kWaves, re);
-
-  // online-softmax state of head hl = lane % 16 (replicated over the 4 rows)
+  // online-softmax state of head hl = lane % 16 (replicated over the 4 rows;
+  // lanes hl >= GQA shadow head hl % GQA and are never written out)
   const int hl = lane & 15;
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NM];
 #pragma unroll
   for (int mm = 0; mm < NM; ++mm) acc[mm] = (floatx4){0.f, 0.f, 0.f, 0.f};
-
-  uint8_t* st = stage[wave];
-  float2* bb = bbuf[wave];
 
   for (; p < re; p += kWaves) {
     // Lane-derived addresses are recomputed each iteration (a few VALU ops)
@@ -345,8 +455,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     asm volatile("" : "+v"(lane_v));
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
-    // ---- issue: row two pages ahead, stage/positions one page ahead -------
-    const RowLd rl_nn = row_issue(a, p + 2 * kWaves, re, lane);
+    // ---- issue: row three pages ahead, stage/positions one page ahead -----
+    const RowLd rl_3 = row_issue(a, p + 3 * kWaves, re, lane);
     const uint4 stg_n = load_stage(a, row_n, lane);
     const int pos_n = load_pos(a, row_n, p + kWaves, t);
 
@@ -354,59 +464,66 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     const int rel = (int)(row_c.page_off & 15);
     uint32_t hw = rel == 0 ? stg_c.x : (rel == 4 ? stg_c.y : (rel == 8 ? stg_c.z : stg_c.w));
     hw = (uint32_t)__builtin_amdgcn_readfirstlane((int)hw);
-    const int tid = row_c.ok ? (int)(hw & 0xFF) : 0;
-    const int n = min((int)((hw >> 8) & 0xFF), kTile);
+    int tid = row_c.ok ? (int)(hw & 0xFF) : 0;
+    // a dense page whose rows were not prefetched (not 16-byte aligned) is skipped
+    if (tid == kDenseTier && !row_looks_dense<DH>(row_c)) tid = 0;
+    const int n = (tid == 0) ? 0 : min((int)((hw >> 8) & 0xFF), kTile);
     if (!row_c.ok) pos_c = -1;
     const bool valid = (t < n) && (pos_c >= 0);
 
-    // ---- page base phasors e^{i 2pi f_j t_mid} (one per lane) -------------
+    // ---- page centre t_mid; query rows rotated by -t_mid into LDS ---------
+    //      <q, R(pos) k> = <R(-t_mid) q, R(pos - t_mid) k>
     int t_lo = __builtin_amdgcn_readlane(pos_c, 0);
     int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
     const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
-    if (lane < NJ) bb[lane] = turn_phasor((double)t_mid * f_lane);
+    if (lane < NJ) {
+      const float2 z = turn_phasor((double)t_mid * f_lane);
+#pragma unroll
+      for (int hh = 0; hh < GQA; ++hh) {
+        const float r0 = qv0[hh] * z.x + qv1[hh] * z.y;
+        const float r1 = qv1[hh] * z.x - qv0[hh] * z.y;
+        const uint32_t hp = pk_rtz(r0, r1);
+        const half2v hi = __builtin_bit_cast(half2v, hp);
+        const half2v lo = __builtin_bit_cast(half2v, pk_rest(r0, r1, hp));
+        _Float16* qh = qr + hh * L::qrow;
+        _Float16* ql = qr + (GQA + hh) * L::qrow;
+        qh[lane] = hi[0];
+        qh[lane + NJ] = hi[1];
+        ql[lane] = lo[0];
+        ql[lane + NJ] = lo[1];
+      }
+    }
 
-    // ---- locate this page's keys: dense rows, or centroid offsets + radii --
+    // ---- locate this page's keys: centroid offsets + radii (compressed) ---
     const bool dense = tid == kDenseTier;
-    uint4 kd[NC];
-    int cofs[NC];
-    float rh[NC];
-    if (dense) {
-      const bool ok = (row_c.th_off & 15) == 0;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int64_t src = row_c.th_off + ((int64_t)t * DH + 32 * c + 8 * u) * 2;
-        kd[c] = (ok && t < n && src + 16 <= a.pages_bytes) ? *reinterpret_cast<const uint4*>(a.pages + src)
-                                                            : uint4{0u, 0u, 0u, 0u};
-        cofs[c] = 0;
-        rh[c] = 0.f;
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) { cofs[c] = 0; rh[c] = 0.f; kd[c] = uint4{0u, 0u, 0u, 0u}; }
-      if (tid >= 1 && tid <= 3) {
-        if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
-        wave_lds_sync();
-        const int64_t base = row_c.page_off & ~(int64_t)15;
-        const int64_t thr64 = row_c.th_off - base, rdr64 = row_c.rad_off - base;
-        const int g = tier_g(tid), b = tier_b(tid);
-        const int G = DH / g;
-        const bool ok = thr64 >= 0 && rdr64 >= 0 && rdr64 + n * G <= 512 && thr64 + (n * G * b + 7) / 8 + 2 < 512;
-        const int thr = ok ? (int)thr64 : 0, rdr = ok ? (int)rdr64 : 0;
-        if (tid == 1) locate_k<DH, 1>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
-        else if (tid == 2) locate_k<DH, 2>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
-        else locate_k<DH, 3>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
-      }
+    int cofs[2] = {0, 0};
+    float rh[2] = {0.f, 0.f};
+    if (tid >= 1 && tid <= 3) {
+      if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
+      wave_lds_sync();
+      const int64_t base = row_c.page_off & ~(int64_t)15;
+      const int64_t thr64 = row_c.th_off - base, rdr64 = row_c.rad_off - base;
+      const int g = tier_g(tid), b = tier_b(tid);
+      const int G = DH / g;
+      const bool ok = thr64 >= 0 && rdr64 >= 0 && rdr64 + n * G <= 512 && thr64 + (n * G * b + 7) / 8 + 2 < 512;
+      const int thr = ok ? (int)thr64 : 0, rdr = ok ? (int)rdr64 : 0;
+      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
     }
     wave_lds_sync();
 
-    // ---- RoPE per chunk pair (c, c + NP): k_rot = R(pos) k_hat, phasor =
-    //      base(t_mid) * delta(pos - t_mid) -> fp16 MFMA operand -------------
-    half8 kb[NC];
+    // ---- k_rot = R(pos - t_mid) k_hat per chunk pair (c, c + NP), fp32,
+    //      split hi + lo fp16.  Phasors from the delta table (sine negated
+    //      for pos < t_mid), or formed directly when |pos - t_mid| >= kDelta.
+    half8 kh[NC], kl[NC];
     {
-      const int dl = pos_c - t_mid;
+      const int dl = valid ? pos_c - t_mid : 0;
       const int ad = dl < 0 ? -dl : dl;
+      const bool near = ad < kDelta;
       const float sg = dl < 0 ? -1.f : 1.f;
-      const bool near = valid && ad < kDelta;
+      const bool any_far = __ballot(!near) != 0;
+      const float* drw = reinterpret_cast<const float*>(dtab + (near ? ad : 0) * L::drow) + 2 * (DH / 8) * u;
 #pragma unroll
       for (int c = 0; c < NP; ++c) {
         float k0[8], k1[8];                      // chunks c and c + NP
@@ -415,47 +532,57 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
 #pragma unroll
           for (int s = 0; s < 8; ++s) { k0[s] = (float)h0[s]; k1[s] = (float)h1[s]; }
         } else {
-          const float4* c0 = reinterpret_cast<const float4*>(cb_s + cofs[c]);
-          const float4* c1 = reinterpret_cast<const float4*>(cb_s + cofs[c + NP]);
+          const float4* c0 = reinterpret_cast<const float4*>(cb_s + cofs[0] + 8 * c);
+          const float4* c1 = reinterpret_cast<const float4*>(cb_s + cofs[1] + 8 * c);
           const float4 a0 = c0[0], a1 = c0[1], b0 = c1[0], b1 = c1[1];
-          const float r0 = rh[c], r1 = rh[c + NP];
+          const float r0 = rh[0], r1 = rh[1];
           k0[0] = r0 * a0.x; k0[1] = r0 * a0.y; k0[2] = r0 * a0.z; k0[3] = r0 * a0.w;
           k0[4] = r0 * a1.x; k0[5] = r0 * a1.y; k0[6] = r0 * a1.z; k0[7] = r0 * a1.w;
           k1[0] = r1 * b0.x; k1[1] = r1 * b0.y; k1[2] = r1 * b0.z; k1[3] = r1 * b0.w;
           k1[4] = r1 * b1.x; k1[5] = r1 * b1.y; k1[6] = r1 * b1.z; k1[7] = r1 * b1.w;
         }
-        const float4* bq = reinterpret_cast<const float4*>(bb + 32 * c + 8 * u);
-        const float4* dq = reinterpret_cast<const float4*>(&dtab[near ? ad : 0][32 * c + 8 * u]);
+        float C[8], S[8];
+        {
+          const float4* dq = reinterpret_cast<const float4*>(drw + 16 * c);
+          const float4 c03 = dq[0], s03 = dq[1], c47 = dq[2], s47 = dq[3];
+          C[0] = c03.x; C[1] = c03.y; C[2] = c03.z; C[3] = c03.w;
+          C[4] = c47.x; C[5] = c47.y; C[6] = c47.z; C[7] = c47.w;
+          S[0] = sg * s03.x; S[1] = sg * s03.y; S[2] = sg * s03.z; S[3] = sg * s03.w;
+          S[4] = sg * s47.x; S[5] = sg * s47.y; S[6] = sg * s47.z; S[7] = sg * s47.w;
+        }
+        if (any_far && !near) {
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-          const float4 b2 = bq[s2];              // two base phasors (j, j+1)
-          float zr[2], zi[2];
-          if (near) {
-            const float4 d2 = dq[s2];
-            const float di0 = sg * d2.y, di1 = sg * d2.w;
-            zr[0] = b2.x * d2.x - b2.y * di0; zi[0] = b2.x * di0 + b2.y * d2.x;
-            zr[1] = b2.z * d2.z - b2.w * di1; zi[1] = b2.z * di1 + b2.w * d2.z;
-          } else {
-            const double pd = (double)(valid ? pos_c : 0);
-            const float2 z0 = turn_phasor(pd * ftab[32 * c + 8 * u + 2 * s2]);
-            const float2 z1 = turn_phasor(pd * ftab[32 * c + 8 * u + 2 * s2 + 1]);
-            zr[0] = z0.x; zi[0] = z0.y; zr[1] = z1.x; zi[1] = z1.y;
-          }
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int s = 2 * s2 + e;
-            kb[c][s] = (_Float16)(k0[s] * zr[e] - k1[s] * zi[e]);
-            kb[c + NP][s] = (_Float16)(k1[s] * zr[e] + k0[s] * zi[e]);
+          for (int s = 0; s < 8; ++s) {
+            const float2 z = turn_phasor((double)dl * ftab[chunk_dim<DH>(c, 0) + (DH / 8) * u + s]);
+            C[s] = z.x;
+            S[s] = z.y;
           }
         }
+        float x0[8], x1[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          x0[s] = k0[s] * C[s] - k1[s] * S[s];
+          x1[s] = k1[s] * C[s] + k0[s] * S[s];
+        }
+        split_f16(x0, kh[c], kl[c]);
+        split_f16(x1, kh[c + NP], kl[c + NP]);
       }
     }
-    // ---- S^T = K_rot q^T on MFMA: lane (u, hl) gets head hl, tokens 4u..4u+3
+    // ---- S^T = K_rot q_rot^T on MFMA (hi*hi + lo*hi + hi*lo): lane (u, hl)
+    //      gets head hl, tokens 4u..4u+3
     floatx4 S = {0.f, 0.f, 0.f, 0.f};
+    {
+      const _Float16* qh = qr + (hl % GQA) * L::qrow;
+      const _Float16* ql = qh + GQA * L::qrow;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const half8 qa = *reinterpret_cast<const half8*>(&q_s[lane & 15][32 * c + 8 * u]);
-      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[c], qa, S, 0, 0, 0);
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u;
+        const half8 qa = *reinterpret_cast<const half8*>(qh + d0);
+        const half8 qb = *reinterpret_cast<const half8*>(ql + d0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qa, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[c], qa, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qb, S, 0, 0, 0);
+      }
     }
 
     // ---- online softmax over the page, per head, in the log2 domain -------
@@ -484,21 +611,28 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     }
 
     // ---- O^T += V^T P^T on MFMA: A[i = dim 16mm + t][k = token 4u + i'] ----
+    // slots without a token get V = 0 (their p is already 0; this keeps
+    // whatever bytes an unused slot holds out of the sum)
+    if (vmask != 0xFFFFu) {
+      const uint32_t keep = (vmask >> (4 * u)) & 0xFu;
 #pragma unroll
-    for (int mm = 0; mm < NM; ++mm) {
-      half4 av = vreg[mm];
-      if (vmask != 0xFFFFu)
+      for (int mm = 0; mm < NM; ++mm)
+#pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (!((vmask >> (4 * u + i)) & 1u)) av[i] = (_Float16)0.f;
-      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pa, acc[mm], 0, 0, 0);
+          vreg[mm][i] = ((keep >> i) & 1u) ? vreg[mm][i] : (_Float16)0.f;
     }
+#pragma unroll
+    for (int mm = 0; mm < NM; ++mm)
+      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(vreg[mm], pa, acc[mm], 0, 0, 0);
 
     // ---- issue V / dense K of the next page into the freed registers ------
     load_v<DH>(a, row_n, t, u, vreg);
+    load_dense<DH>(a, row_n, t, u, kd);
     wave_lds_sync();
 
     row_c = row_n;
-    row_n = row_take(a, rl_nn, p + 2 * kWaves, re);
+    row_n = row_take(a, rl_2, p + 2 * kWaves, re);
+    rl_2 = rl_3;
     stg_c = stg_n;
     pos_c = pos_n;
   }
@@ -506,7 +640,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   // ---- merge the waves' states in LDS, write this item's partial ----------
   constexpr int PS = partial_stride<DH, GQA>();
   __syncthreads();
-  float* mrg = cb_s;                                  // reuse codebook space: [kWaves][GQA][DH]
+  float* mrg = reinterpret_cast<float*>(smem);        // [kWaves][GQA][DH]
   float* mrg_ml = mrg + kWaves * GQA * DH;            // [kWaves][GQA][2]
   if (hl < GQA) {
 #pragma unroll
@@ -516,28 +650,37 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   }
   __syncthreads();
   float* part = a.partials + (int64_t)item * PS;
-  for (int i = threadIdx.x; i < GQA * DH; i += kWaves * 64) {
-    const int hh = i / DH, d = i % DH;
+  float* fw = mrg_ml + kWaves * GQA * 2;              // [GQA][kWaves] wave weights 2^(m_w - M)
+  if (threadIdx.x < GQA) {
+    const int hh = threadIdx.x;
     float M = -INFINITY;
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[(w * GQA + hh) * 2]);
-    float L = 0.f, A = 0.f;
-    if (M != -INFINITY)
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = mrg_ml[(w * GQA + hh) * 2];
-        if (mw == -INFINITY) continue;
-        const float f = __builtin_amdgcn_exp2f(mw - M);
-        L += f * mrg_ml[(w * GQA + hh) * 2 + 1];
-        A += f * mrg[(w * GQA + hh) * DH + d];
-      }
+    float Ls = 0.f;
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = mrg_ml[(w * GQA + hh) * 2];
+      const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      fw[hh * kWaves + w] = f;
+      Ls += f * mrg_ml[(w * GQA + hh) * 2 + 1];
+    }
+    part[hh] = M;
+    part[GQA + hh] = Ls;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < GQA * DH; i += kWaves * 64) {
+    const int hh = i / DH, d = i % DH;
+    float A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) A += fw[hh * kWaves + w] * mrg[(w * GQA + hh) * DH + d];
     part[16 + hh * DH + d] = A;
-    if (d == 0) { part[hh] = M; part[GQA + hh] = L; }
   }
 }
 
 // Log-sum-exp merge of the partials of each (sequence, kv head).  One
-// workgroup per (sequence, kv head, 128-float slice of its GQA*DH output);
-// all loads of a thread are independent (issued together) so the merge costs
-// about one memory round trip.
+// workgroup per (sequence, kv head, slice of up to 128 floats of its GQA*DH
+// output); thread = (item lane il, float4 column c).  Each thread keeps its
+// own running (max, sum, weighted acc) over its items, so all of a thread's
+// loads are independent and a merge over <= 32 items costs one memory round
+// trip after the work_start read; the 8 item lanes are combined in LDS.
 template <int DH, int GQA>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ partials,
                                                            const int32_t* __restrict__ work_start,
@@ -546,75 +689,62 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   constexpr int SL = GQA * DH < 128 ? GQA * DH : 128; // floats per output slice
   constexpr int NSL = (GQA * DH) / SL;                // slices per (seq, kv head)
   constexpr int IL = 8;                               // item lanes: 256 threads = 8 x 32 float4 columns
-  __shared__ float ml_s[GQA][2];
-  __shared__ float4 red[IL][32];
-  __shared__ float mred[256];
+  constexpr int UN = 4;                               // items per item lane per round trip
+  __shared__ float4 red_v[IL][32];
+  __shared__ float red_m[IL][32], red_l[IL][32];
   const int sh = blockIdx.x / NSL, slice = blockIdx.x % NSL;
   const int ib = work_start[sh], ni = work_start[sh + 1] - ib;
-  const int hh0 = (slice * SL) / DH;                  // first head of this slice
-  constexpr int HPS = SL / DH > 0 ? SL / DH : 1;      // heads per slice
-  // M and L of the slice's heads: 256 threads stride over (item, head)
-  for (int k = 0; k < HPS; ++k) {
-    const int hh = hh0 + k;
-    float mx = -INFINITY;
-    for (int it = threadIdx.x; it < ni; it += 256) mx = fmaxf(mx, partials[(int64_t)(ib + it) * PS + hh]);
-    mred[threadIdx.x] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if (threadIdx.x < o) mred[threadIdx.x] = fmaxf(mred[threadIdx.x], mred[threadIdx.x + o]);
-      __syncthreads();
-    }
-    const float M = mred[0];
-    __syncthreads();
-    float ls = 0.f;
-    for (int it = threadIdx.x; it < ni; it += 256) {
-      const float* pp = partials + (int64_t)(ib + it) * PS;
-      const float mi = pp[hh];
-      if (mi != -INFINITY) ls += __builtin_amdgcn_exp2f(mi - M) * pp[GQA + hh];
-    }
-    mred[threadIdx.x] = ls;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if (threadIdx.x < o) mred[threadIdx.x] += mred[threadIdx.x + o];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) { ml_s[hh][0] = M; ml_s[hh][1] = mred[0]; }
-    __syncthreads();
-  }
-  // weighted sum of the slice: thread = (item lane il, float4 column c)
   const int c = threadIdx.x & 31, il = threadIdx.x >> 5;
   const bool col_ok = 4 * c < SL;
   const int f0 = slice * SL + (col_ok ? 4 * c : 0);   // first float of this column in [GQA*DH]
   const int hh = f0 / DH;
-  const float M = ml_s[hh][0];
+  float M = -INFINITY, Ls = 0.f;
   float4 sum = {0.f, 0.f, 0.f, 0.f};
-  constexpr int UN = 8;
   for (int it0 = il; it0 < ni; it0 += IL * UN) {
     float4 v[UN];
-    float mi[UN];
+    float mi[UN], li[UN];
 #pragma unroll
     for (int k = 0; k < UN; ++k) {
       const int it = it0 + k * IL;
       const float* pp = partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
       mi[k] = it < ni ? pp[hh] : -INFINITY;
+      li[k] = pp[GQA + hh];
       v[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
     }
+    float Mn = M;
+#pragma unroll
+    for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, mi[k]);
+    if (Mn == -INFINITY) continue;
+    const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+    sum.x *= r; sum.y *= r; sum.z *= r; sum.w *= r;
+    Ls *= r;
 #pragma unroll
     for (int k = 0; k < UN; ++k) {
-      const float f = (mi[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mi[k] - M);
+      const float f = (mi[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mi[k] - Mn);
+      Ls += f * li[k];
       sum.x += f * v[k].x; sum.y += f * v[k].y; sum.z += f * v[k].z; sum.w += f * v[k].w;
     }
+    M = Mn;
   }
-  red[il][c] = sum;
+  red_v[il][c] = sum;
+  red_m[il][c] = M;
+  red_l[il][c] = Ls;
   __syncthreads();
   if (il == 0 && col_ok) {
-    float4 tot = red[0][c];
-    for (int k = 1; k < IL; ++k) {
-      const float4 x = red[k][c];
-      tot.x += x.x; tot.y += x.y; tot.z += x.z; tot.w += x.w;
-    }
-    const float L = ml_s[hh][1];
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float Mx = -INFINITY;
+    for (int k = 0; k < IL; ++k) Mx = fmaxf(Mx, red_m[k][c]);
+    float4 tot = {0.f, 0.f, 0.f, 0.f};
+    float Lt = 0.f;
+    if (Mx != -INFINITY)
+      for (int k = 0; k < IL; ++k) {
+        const float mk = red_m[k][c];
+        if (mk == -INFINITY) continue;
+        const float f = __builtin_amdgcn_exp2f(mk - Mx);
+        const float4 x = red_v[k][c];
+        tot.x += f * x.x; tot.y += f * x.y; tot.z += f * x.z; tot.w += f * x.w;
+        Lt += f * red_l[k][c];
+      }
+    const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
     half4 o;
     o[0] = (_Float16)(tot.x * inv); o[1] = (_Float16)(tot.y * inv);
     o[2] = (_Float16)(tot.z * inv); o[3] = (_Float16)(tot.w * inv);
@@ -624,7 +754,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 }
 
 template <int DH, int GQA>
-static int launch_decode_t(const DecodeLaunch& L, hipStream_t stream) {
+static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream) {
   DecodeArgs a;
   a.pages = L.pages; a.pages_bytes = L.pages_bytes; a.ptable = L.ptable; a.vslot = L.vslot;
   a.positions = L.positions; a.v_pool = reinterpret_cast<const _Float16*>(L.v_pool);
@@ -635,16 +765,19 @@ static int launch_decode_t(const DecodeLaunch& L, hipStream_t stream) {
   a.scale_log2 = L.sm_scale * 1.4426950408889634f;
   a.log2_theta = __builtin_log2(L.rope_theta);
   if (L.num_items > 0) {
-    hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(kWaves * 64), 0, stream, a);
+    if (phases & kPhasePartials)
+      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(kWaves * 64), 0, stream, a);
     const int nsh = L.num_seqs * L.num_kv;
-    hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))), dim3(256), 0, stream,
-                       L.partials, L.work_start, L.num_kv, reinterpret_cast<_Float16*>(L.out));
+    if ((phases & kPhaseMerge) && nsh > 0)
+      hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
+                         dim3(256), 0, stream, L.partials, L.work_start, L.num_kv,
+                         reinterpret_cast<_Float16*>(L.out));
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_decode(const DecodeLaunch& L, hipStream_t stream) {
-#define SPHKV_DISPATCH(D, Q) if (L.dh == D && L.gqa == Q) return launch_decode_t<D, Q>(L, stream);
+int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream) {
+#define SPHKV_DISPATCH(D, Q) if (L.dh == D && L.gqa == Q) return launch_decode_t<D, Q>(L, phases, stream);
   SPHKV_DISPATCH(128, 1) SPHKV_DISPATCH(128, 2) SPHKV_DISPATCH(128, 4) SPHKV_DISPATCH(128, 8)
   SPHKV_DISPATCH(64, 1) SPHKV_DISPATCH(64, 2) SPHKV_DISPATCH(64, 4) SPHKV_DISPATCH(64, 8)
 #undef SPHKV_DISPATCH

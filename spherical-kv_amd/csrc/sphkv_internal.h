@@ -37,7 +37,11 @@ struct RaggedLaunch {
 };
 
 int launch_encode(const EncodeLaunch& L, hipStream_t stream);
-int launch_decode(const DecodeLaunch& L, hipStream_t stream);
+// Decode phases: the split kernel writing one (m, l, acc) partial per work
+// item, and the log-sum-exp merge of each (sequence, kv head)'s partials.
+constexpr int kPhasePartials = 1;
+constexpr int kPhaseMerge = 2;
+int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream);
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream);
 
 // fp32 elements of one work item's partial: 16 (m, l, padding) + gqa * dh

@@ -206,26 +206,37 @@ def encode_pages(pool: PagedPool, k: torch.Tensor, v: torch.Tensor, src_rows: to
     check(rc, "sphkv_encode_pages")
 
 
+def _decode_workspace(pool: PagedPool, gqa: int, workspace: Optional[torch.Tensor]) -> torch.Tensor:
+    wsb = pool.workspace_bytes(gqa)
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=pool.device)
+    _need(workspace, torch.uint8, "workspace", pool.device)
+    if workspace.numel() < wsb:
+        raise ValueError(f"workspace needs {wsb} bytes, got {workspace.numel()}")
+    return workspace
+
+
+def _check_q(pool: PagedPool, q: torch.Tensor, gqa: int) -> None:
+    plan = pool.plan
+    _need(q, torch.float16, "q", pool.device)
+    want = (plan.num_seqs, plan.num_kv * gqa, plan.dh)
+    if tuple(q.shape) != want:
+        raise ValueError(f"q must be {want}, got {tuple(q.shape)}")
+
+
 def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Angle-domain paged attention decode.  q fp16 [num_seqs, num_kv*gqa, dh]
     -> out fp16 of the same shape."""
     plan = pool.plan
-    dev = pool.device
-    _need(q, torch.float16, "q", dev)
-    want = (plan.num_seqs, plan.num_kv * gqa, plan.dh)
-    if tuple(q.shape) != want:
-        raise ValueError(f"q must be {want}, got {tuple(q.shape)}")
+    _check_q(pool, q, gqa)
     if out is None:
         out = torch.empty_like(q)
-    _need(out, torch.float16, "out", dev)
+    _need(out, torch.float16, "out", pool.device)
     if out.shape != q.shape:
         raise ValueError("out must match q")
-    wsb = pool.workspace_bytes(gqa)
-    if workspace is None:
-        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
-    _need(workspace, torch.uint8, "workspace", dev)
+    workspace = _decode_workspace(pool, gqa, workspace)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(plan.dh)
     c1, c2, c3 = pool.cb_ptrs()
@@ -236,6 +247,44 @@ def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
         plan.num_seqs, plan.num_kv, gqa, q.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         workspace.numel(), plan.dh, plan.page_size, float(sm_scale), float(rope_theta), _stream())
     check(rc, "sphkv_decode_paged")
+    return out
+
+
+def decode_paged_partials(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
+                          workspace: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
+    """First phase of decode_paged: one (m, l, acc) partial per work item into
+    `workspace` (fp32 [num_items, 16 + gqa*dh] viewed as bytes); returns the
+    fp32 view of the partials."""
+    plan = pool.plan
+    _check_q(pool, q, gqa)
+    workspace = _decode_workspace(pool, gqa, workspace)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(plan.dh)
+    c1, c2, c3 = pool.cb_ptrs()
+    rc = load().sphkv_decode_paged_partials(
+        pool.pages.data_ptr(), plan.pages_bytes, pool.ptable.data_ptr(), pool.vslot.data_ptr(),
+        pool.positions.data_ptr(), plan.num_rows, pool.v_pool.data_ptr(), plan.num_vpages,
+        c1, c2, c3, pool.work.data_ptr(), pool.num_items, pool.work_start.data_ptr(),
+        plan.num_seqs, plan.num_kv, gqa, q.data_ptr(), workspace.data_ptr(),
+        workspace.numel(), plan.dh, plan.page_size, float(sm_scale), float(rope_theta), _stream())
+    check(rc, "sphkv_decode_paged_partials")
+    n = pool.num_items * (16 + gqa * plan.dh)
+    return workspace[:4 * n].view(torch.float32).view(pool.num_items, 16 + gqa * plan.dh)
+
+
+def merge_partials(pool: PagedPool, workspace: torch.Tensor, gqa: int,
+                   out: torch.Tensor) -> torch.Tensor:
+    """Second phase of decode_paged: log-sum-exp merge of the partials in
+    `workspace` into out fp16 [num_seqs, num_kv*gqa, dh]."""
+    plan = pool.plan
+    _need(out, torch.float16, "out", pool.device)
+    if tuple(out.shape) != (plan.num_seqs, plan.num_kv * gqa, plan.dh):
+        raise ValueError("out has the wrong shape")
+    workspace = _decode_workspace(pool, gqa, workspace)
+    rc = load().sphkv_decode_merge_partials(
+        workspace.data_ptr(), workspace.numel(), pool.num_items, pool.work_start.data_ptr(),
+        plan.num_seqs, plan.num_kv, gqa, plan.dh, out.data_ptr(), _stream())
+    check(rc, "sphkv_decode_merge_partials")
     return out
 
 

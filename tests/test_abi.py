@@ -1,0 +1,124 @@
+"""CPU tests of the C-ABI boundary (no GPU, no kernel launches).
+
+libsphkv.so must load, export every function include/sphkv.h declares, and the
+ctypes table must agree with the header on argument counts.  The argument
+checks run on the host before any HIP call, so their error behaviour is tested
+here: a bad call returns a negative status and leaves a message.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import sphkv_lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "sphkv.h")
+
+
+def header_functions():
+    """name -> number of parameters of every function declared in sphkv.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(sphkv_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        out[name] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_header_parses():
+    fns = header_functions()
+    assert "sphkv_decode_paged" in fns and "sphkv_encode_pages" in fns
+    assert len(fns) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    lib = sphkv_lib.load()
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in sphkv.h but not exported"
+
+
+def test_ctypes_table_matches_header():
+    fns = header_functions()
+    assert set(sphkv_lib.SIGNATURES) == set(fns)
+    for name, nargs in fns.items():
+        assert len(sphkv_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_version_string():
+    assert sphkv_lib.version().startswith("sphkv")
+
+
+def test_workspace_bytes():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_paged_workspace_bytes(256, 4, 128) == 256 * (16 + 4 * 128) * 4
+    assert lib.sphkv_decode_paged_workspace_bytes(0, 8, 64) == 0
+    assert lib.sphkv_decode_paged_workspace_bytes(4, 3, 128) == -1      # gqa not supported
+    assert lib.sphkv_decode_paged_workspace_bytes(4, 4, 96) == -1       # dh not supported
+    assert lib.sphkv_decode_paged_workspace_bytes(-1, 4, 128) == -1
+
+
+def _decode_args(**kw):
+    a = dict(pages=None, pages_bytes=0, ptable=None, vslot=None, positions=None, num_rows=0,
+             v_pool=None, num_vpages=0, cb1=None, cb2=None, cb3=None, work=None, num_items=0,
+             work_start=None, num_seqs=1, num_kv=8, gqa=4, q=None, out=None, workspace=None,
+             workspace_bytes=0, dh=128, page_size=16, sm_scale=0.088, rope_theta=5e5, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dh=96), "dh must be 64 or 128"),
+    (dict(gqa=3), "gqa must be"),
+    (dict(page_size=32), "page_size must be 16"),
+    (dict(rope_theta=1.0), "rope_theta"),
+    (dict(num_items=8), "workspace too small"),
+    (dict(num_items=4, workspace_bytes=10 ** 9), "at least one work item"),
+    (dict(num_items=16, workspace_bytes=10 ** 9, work_start=None), "null pointer"),
+])
+def test_decode_argument_errors(kw, msg):
+    lib = sphkv_lib.load()
+    rc = lib.sphkv_decode_paged(*_decode_args(**kw))
+    assert rc == -1
+    assert msg in lib.sphkv_last_error().decode()
+
+
+def test_decode_zero_sequences_is_a_no_op():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_paged(*_decode_args(num_seqs=0)) == 0
+    assert lib.sphkv_last_error().decode() == ""
+
+
+def test_merge_argument_errors():
+    lib = sphkv_lib.load()
+    rc = lib.sphkv_decode_merge_partials(None, 0, 8, None, 1, 8, 4, 128, None, None)
+    assert rc == -1 and "workspace too small" in lib.sphkv_last_error().decode()
+    buf = ctypes.create_string_buffer(8)
+    rc = lib.sphkv_decode_merge_partials(buf, 10 ** 9, 8, buf, 1, 8, 4, 128, None, None)
+    assert rc == -1 and "null output" in lib.sphkv_last_error().decode()
+
+
+def test_encode_argument_errors():
+    lib = sphkv_lib.load()
+    args = [None, 0, None, 0, None, None, None, None, None, None, 4, 8, None, None, None,
+            None, 0, None, 0, None, None, 128, 16, None]
+    args[21] = 80
+    assert lib.sphkv_encode_pages(*args) == -1
+    assert "dh must be 64 or 128" in lib.sphkv_last_error().decode()
+    args[21] = 128
+    assert lib.sphkv_encode_pages(*args) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+
+
+def test_ragged_argument_errors():
+    lib = sphkv_lib.load()
+    args = [None, 0, None, None, None, 4, None, None, 100, None, 4, 8, None,
+            128, 8, 16, 6, 16, None, None]
+    args[14] = 7                                   # group_size * groups != dh
+    assert lib.sphkv_fused_decode_ragged(*args) == -1
+    assert "groups*group_size" in lib.sphkv_last_error().decode()
+    args[14] = 8
+    args[16] = 9                                   # b_theta
+    assert lib.sphkv_fused_decode_ragged(*args) == -1
+    assert "b_theta" in lib.sphkv_last_error().decode()

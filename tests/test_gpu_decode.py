@@ -154,3 +154,28 @@ def test_ragged_logits_matches_oracle(gpu):
         fin = np.isfinite(want)
         assert (np.isneginf(got) == ~fin).all()
         assert max_err(got[fin], want[fin]) < 2e-4
+
+
+def test_decode_split_phases_equal_fused_call(gpu):
+    # partials + merge as two calls give exactly the one-call result, and the
+    # partials merge (fp64, on the host) to the same output
+    wl = synth.make_decode_workload(2, ctx_override=3000)
+    pool, _ = pool_from_oracle(wl, gpu, rows_per_item=24)
+    q = torch.as_tensor(wl.q, device=gpu)
+    ref = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta)
+    ws = torch.empty(pool.workspace_bytes(wl.gqa), dtype=torch.uint8, device=gpu)
+    part = ops.decode_paged_partials(pool, q, wl.gqa, wl.rope_theta, ws)
+    out = ops.merge_partials(pool, ws, wl.gqa, torch.empty_like(q))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    P = part.double().cpu().numpy()
+    ws_h = pool.work_start.cpu().numpy()
+    G, DH = wl.gqa, wl.dh
+    host = np.zeros((wl.num_kv * G, DH))
+    for sh in range(wl.num_kv):
+        rows = P[ws_h[sh]:ws_h[sh + 1]]
+        m, l, acc = rows[:, :G], rows[:, G:2 * G], rows[:, 16:].reshape(-1, G, DH)
+        M = m.max(0)
+        f = np.where(np.isfinite(m), np.exp2(m - M), 0.0)
+        host[sh * G:(sh + 1) * G] = (f[:, :, None] * acc).sum(0) / (f * l).sum(0)[:, None]
+    assert max_err(out[0].float().cpu().numpy(), host) < 1e-3
