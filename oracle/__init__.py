@@ -148,13 +148,12 @@ def unpack_page(pages: np.ndarray, row: np.ndarray, tier_id: int, n: int, dh: in
 
 @functools.lru_cache(maxsize=None)
 def v_page_index(dh: int) -> np.ndarray:
-    """Position of element (token k, dim d) inside a V page of the decode pool:
-    d = 16*mm + t, k = 4*u + i  ->  ((t*4 + u) * (dh/16) + mm) * 4 + i."""
+    """Position of element (token k, dim d) inside a V page of the decode pool
+    (dim-major: the 16 tokens of one dim are contiguous): d * 16 + k."""
     out = np.zeros((16, dh), np.int64)
     for k in range(16):
         for d in range(dh):
-            mm, t, u, i = d // 16, d % 16, k // 4, k % 4
-            out[k, d] = ((t * 4 + u) * (dh // 16) + mm) * 4 + i
+            out[k, d] = d * 16 + k
     return out
 
 

@@ -131,20 +131,20 @@ __device__ __forceinline__ int load_pos(const DecodeArgs& a, const Row& r, int p
   return __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * t, 0, 0);
 }
 
-// V page layout ("MFMA order"): element (token 4u+i, dim 16mm+t) at half offset
-// ((t*4 + u) * (DH/16) + mm) * 4 + i, so lane (u, t) reads its PV B operands
-// for all mm as DH/2 contiguous bytes.
+// V page layout, dim-major: element (token k, dim d) at half d * 16 + k.  Lane
+// l loads dims l + 64 hf (hf < DH/64), 16 tokens = 32 bytes each: vreg[2hf]
+// holds tokens 0..7, vreg[2hf + 1] tokens 8..15 -- the B operands of the
+// 4x4x4 PV MFMA.
 template <int DH>
-__device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int t, int u, half4 (&vreg)[DH / 16]) {
+__device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int lane, half8 (&vreg)[DH / 32]) {
   const rsrc_t rs = make_rsrc(a.v_pool + r.vs * DH * kTile, r.ok ? DH * kTile * 2 : 0);
-  const int base = (t * 4 + u) * (DH / 16) * 8;     // bytes
 #pragma unroll
-  for (int m2 = 0; m2 < DH / 32; ++m2) {
-    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * m2, 0, 0);
-    const uint2 lo = {(uint32_t)w[0], (uint32_t)w[1]}, hi = {(uint32_t)w[2], (uint32_t)w[3]};
-    vreg[2 * m2] = __builtin_bit_cast(half4, lo);
-    vreg[2 * m2 + 1] = __builtin_bit_cast(half4, hi);
-  }
+  for (int hf = 0; hf < DH / 64; ++hf)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, ((lane + 64 * hf) * kTile + 8 * k) * 2, 0, 0);
+      vreg[2 * hf + k] = __builtin_bit_cast(half8, uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]});
+    }
 }
 
 // Dimension of element s of chunk c for lane quarter u.  A lane's chunks
@@ -188,8 +188,10 @@ __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 //    RoPE frequencies j, 4 x cos(2 pi f_j d) then 4 x sin(2 pi f_j d), fp32,
 //    rows padded by 16 bytes;
 //  * f_j in turns per token (fp64);
-//  * per wave: the 512-byte staging window of its page, and the query rows
-//    rotated to the page centre split as hi + lo fp16 ([2][GQA][DH + 8]).
+//  * per wave: the 512-byte staging window of its page, the query rows
+//    rotated to the page centre split as hi + lo fp16 ([2][GQA][DH + 8]), and
+//    the page's softmax weights P as fp16 [max(GQA, 4)][16 tokens] (rows >=
+//    GQA stay zero), read back as the PV MFMA's A operand.
 template <int DH, int GQA>
 struct DecodeLds {
   static constexpr int NJ = DH / 2;
@@ -208,7 +210,9 @@ struct DecodeLds {
   static constexpr int o_stage = o_ftab + NJ * 8;
   static constexpr int o_qr = o_stage + kWaves * 512;
   static constexpr int qr_wave = 2 * GQA * qrow;                 // halves per wave
-  static constexpr int total = o_qr + kWaves * qr_wave * 2;
+  static constexpr int PR = GQA < 4 ? 4 : GQA;                   // P rows (heads padded to 4)
+  static constexpr int o_pt = o_qr + kWaves * qr_wave * 2;
+  static constexpr int total = o_pt + kWaves * PR * 32;
   // the end-of-item wave merge reuses the space: [kWaves][GQA][DH] acc,
   // [kWaves][GQA][2] (m, l), [GQA][kWaves] weights
   static constexpr int merge_bytes = kWaves * GQA * (DH + 3) * 4;
@@ -315,17 +319,24 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
 }
 
 // x = hi + lo with hi, lo fp16: hi = x rounded toward zero (v_cvt_pkrtz), lo =
-// fp16(x - hi) formed by one mixed-precision FMA (fp32 x, fp16 hi) that
-// writes one half of the packed result.  The pair carries x to about 2^-22
-// relative, so products on the fp16 MFMA lose nothing that matters against
-// the 2e-3 tolerance.
+// fp16(x - hi) formed by one mixed-precision FMA per half (fp32 x, fp16 hi)
+// that writes that half of the packed result.  The pair carries x to about
+// 2^-22 relative, so products on the fp16 MFMA lose nothing that matters
+// against the 2e-3 tolerance.  The FMAs are inline asm (the compiler forms
+// them only when fp32 denormals are flushed); the s_nop after each covers the
+// forwarding hazard of a partial (one-half) VGPR write, which the compiler's
+// hazard recognizer does not track through inline asm.  Inputs are never the
+// direct result of a transcendental instruction.
 __device__ __forceinline__ uint32_t pk_rtz(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
 __device__ __forceinline__ uint32_t pk_rest(float a, float b, uint32_t hi) {
-  uint32_t d = 0;
-  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "+v"(d) : "v"(a), "v"(hi));
-  asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(d) : "v"(b), "v"(hi));
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "s_nop 0\n\t"
+      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "s_nop 0"
+      : "=&v"(d) : "v"(a), "v"(b), "v"(hi));
   return d;
 }
 __device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8& lo) {
@@ -341,7 +352,6 @@ template <int DH, int GQA>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeArgs a) {
   constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
   constexpr int NP = NC / 2;         // chunks holding the first RoPE half
-  constexpr int NM = DH / 16;        // PV MFMA blocks
   constexpr int NJ = DH / 2;         // RoPE frequencies
   using L = DecodeLds<DH, GQA>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::total];
@@ -387,23 +397,30 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
       }
     }
   }
-  // this lane's query pair (j, j + NJ) of every head of the item, fp32
-  float qv0[GQA], qv1[GQA];
+  // this lane's query pair (j, j + NJ) of every head of the item, packed fp16
+  uint32_t qv[GQA];
   {
     const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
     const int j = lane % NJ;
 #pragma unroll
     for (int hh = 0; hh < GQA; ++hh) {
-      qv0[hh] = (float)qh[hh * DH + j];
-      qv1[hh] = (float)qh[hh * DH + j + NJ];
+      half2v v;
+      v[0] = qh[hh * DH + j];
+      v[1] = qh[hh * DH + j + NJ];
+      qv[hh] = __builtin_bit_cast(uint32_t, v);
     }
+  }
+  if (GQA < 4 && lane < (4 - GQA) * 2) {              // zero P rows GQA..3 of this wave
+    half8 z;
+    for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.f;
+    *reinterpret_cast<half8*>(reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile + GQA * kTile + 8 * lane) = z;
   }
   // first page's data and the next page's row
   Row row_c = row_take(a, rl_c, p, re);
   uint4 stg_c = load_stage(a, row_c, lane);
   int pos_c = load_pos(a, row_c, p, t);
-  half4 vreg[NM];
-  load_v<DH>(a, row_c, t, u, vreg);
+  half8 vreg[DH / 32];
+  load_v<DH>(a, row_c, lane, vreg);
   uint4 kd[NC];
   load_dense<DH>(a, row_c, t, u, kd);
   Row row_n = row_take(a, rl_n, p + kWaves, re);
@@ -433,7 +450,6 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     row[j & 3] = z.x;
     row[4 + (j & 3)] = z.y;
   }
-  const double f_lane = ftab[lane % NJ];
   __syncthreads();
   // everything loaded so far is complete before the page pipeline starts, so
   // no wait inside the loop has to account for it
@@ -443,11 +459,23 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   // lanes hl >= GQA shadow head hl % GQA and are never written out)
   const int hl = lane & 15;
   float m_run = -INFINITY, l_run = 0.f;
-  floatx4 acc[NM];
+  // PV accumulators of the 4x4x4 MFMA: acc[hs][hf] lane l, element i =
+  // O[head 4 hs + i][dim 64 hf + l]
+  constexpr int NHS = L::PR / 4, NHF = DH / 64;
+  floatx4 acc[NHS][NHF];
 #pragma unroll
-  for (int mm = 0; mm < NM; ++mm) acc[mm] = (floatx4){0.f, 0.f, 0.f, 0.f};
+  for (int hs = 0; hs < NHS; ++hs)
+#pragma unroll
+    for (int hf = 0; hf < NHF; ++hf) acc[hs][hf] = (floatx4){0.f, 0.f, 0.f, 0.f};
+  _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
 
-  for (; p < re; p += kWaves) {
+  // One page of the pipeline.  The staging window and positions of the next
+  // page are loaded into the other register set of a pair, and the pointer-
+  // table rows into the other slot of a pair, so the loop (unrolled by two)
+  // never copies a register that a load is still filling: such a copy would
+  // wait for that load.
+  auto step = [&](const int p, uint4& stg_c, int& pos_c, uint4& stg_n, int& pos_n, RowLd& rl_issue,
+                  RowLd& rl_take) __attribute__((always_inline)) {
     // Lane-derived addresses are recomputed each iteration (a few VALU ops)
     // instead of being hoisted out of the loop, where they would not fit in
     // the register budget of 3 waves per SIMD and would be spilled.
@@ -456,9 +484,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
     // ---- issue: row three pages ahead, stage/positions one page ahead -----
-    const RowLd rl_3 = row_issue(a, p + 3 * kWaves, re, lane);
-    const uint4 stg_n = load_stage(a, row_n, lane);
-    const int pos_n = load_pos(a, row_n, p + kWaves, t);
+    rl_issue = row_issue(a, p + 3 * kWaves, re, lane);
+    stg_n = load_stage(a, row_n, lane);
+    pos_n = load_pos(a, row_n, p + kWaves, t);
 
     // ---- this page's header (lane 0's 16 bytes of the stage) --------------
     const int rel = (int)(row_c.page_off & 15);
@@ -477,11 +505,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
     const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
     if (lane < NJ) {
-      const float2 z = turn_phasor((double)t_mid * f_lane);
+      const float2 z = turn_phasor((double)t_mid * ftab[lane_v % NJ]);
 #pragma unroll
       for (int hh = 0; hh < GQA; ++hh) {
-        const float r0 = qv0[hh] * z.x + qv1[hh] * z.y;
-        const float r1 = qv1[hh] * z.x - qv0[hh] * z.y;
+        const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
+        const float q0 = (float)qp[0], q1 = (float)qp[1];
+        const float r0 = q0 * z.x + q1 * z.y;
+        const float r1 = q1 * z.x - q0 * z.y;
         const uint32_t hp = pk_rtz(r0, r1);
         const half2v hi = __builtin_bit_cast(half2v, hp);
         const half2v lo = __builtin_bit_cast(half2v, pk_rest(r0, r1, hp));
@@ -516,8 +546,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     // ---- k_rot = R(pos - t_mid) k_hat per chunk pair (c, c + NP), fp32,
     //      split hi + lo fp16.  Phasors from the delta table (sine negated
     //      for pos < t_mid), or formed directly when |pos - t_mid| >= kDelta.
-    half8 kh[NC], kl[NC];
+    //      Each chunk pair feeds the QK MFMA (S^T = K_rot q_rot^T as hi*hi +
+    //      lo*hi + hi*lo; lane (u, hl) gets head hl, tokens 4u..4u+3) as soon
+    //      as it is split, so few operand registers are live at a time.
+    floatx4 S = {0.f, 0.f, 0.f, 0.f};
     {
+      const _Float16* qh = qr + (hl % GQA) * L::qrow;
+      const _Float16* ql = qh + GQA * L::qrow;
       const int dl = valid ? pos_c - t_mid : 0;
       const int ad = dl < 0 ? -dl : dl;
       const bool near = ad < kDelta;
@@ -541,47 +576,43 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
           k1[0] = r1 * b0.x; k1[1] = r1 * b0.y; k1[2] = r1 * b0.z; k1[3] = r1 * b0.w;
           k1[4] = r1 * b1.x; k1[5] = r1 * b1.y; k1[6] = r1 * b1.z; k1[7] = r1 * b1.w;
         }
-        float C[8], S[8];
+        float pc[8], ps[8];                     // phasor cos / sin
         {
           const float4* dq = reinterpret_cast<const float4*>(drw + 16 * c);
           const float4 c03 = dq[0], s03 = dq[1], c47 = dq[2], s47 = dq[3];
-          C[0] = c03.x; C[1] = c03.y; C[2] = c03.z; C[3] = c03.w;
-          C[4] = c47.x; C[5] = c47.y; C[6] = c47.z; C[7] = c47.w;
-          S[0] = sg * s03.x; S[1] = sg * s03.y; S[2] = sg * s03.z; S[3] = sg * s03.w;
-          S[4] = sg * s47.x; S[5] = sg * s47.y; S[6] = sg * s47.z; S[7] = sg * s47.w;
+          pc[0] = c03.x; pc[1] = c03.y; pc[2] = c03.z; pc[3] = c03.w;
+          pc[4] = c47.x; pc[5] = c47.y; pc[6] = c47.z; pc[7] = c47.w;
+          ps[0] = sg * s03.x; ps[1] = sg * s03.y; ps[2] = sg * s03.z; ps[3] = sg * s03.w;
+          ps[4] = sg * s47.x; ps[5] = sg * s47.y; ps[6] = sg * s47.z; ps[7] = sg * s47.w;
         }
         if (any_far && !near) {
 #pragma unroll
           for (int s = 0; s < 8; ++s) {
             const float2 z = turn_phasor((double)dl * ftab[chunk_dim<DH>(c, 0) + (DH / 8) * u + s]);
-            C[s] = z.x;
-            S[s] = z.y;
+            pc[s] = z.x;
+            ps[s] = z.y;
           }
         }
         float x0[8], x1[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          x0[s] = k0[s] * C[s] - k1[s] * S[s];
-          x1[s] = k1[s] * C[s] + k0[s] * S[s];
+          x0[s] = k0[s] * pc[s] - k1[s] * ps[s];
+          x1[s] = k1[s] * pc[s] + k0[s] * ps[s];
         }
-        split_f16(x0, kh[c], kl[c]);
-        split_f16(x1, kh[c + NP], kl[c + NP]);
-      }
-    }
-    // ---- S^T = K_rot q_rot^T on MFMA (hi*hi + lo*hi + hi*lo): lane (u, hl)
-    //      gets head hl, tokens 4u..4u+3
-    floatx4 S = {0.f, 0.f, 0.f, 0.f};
-    {
-      const _Float16* qh = qr + (hl % GQA) * L::qrow;
-      const _Float16* ql = qh + GQA * L::qrow;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u;
-        const half8 qa = *reinterpret_cast<const half8*>(qh + d0);
-        const half8 qb = *reinterpret_cast<const half8*>(ql + d0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qa, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[c], qa, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qb, S, 0, 0, 0);
+        half8 kh0, kl0, kh1, kl1;
+        split_f16(x0, kh0, kl0);
+        split_f16(x1, kh1, kl1);
+        const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u, d1 = chunk_dim<DH>(c + NP, 0) + (DH / 8) * u;
+        const half8 qa0 = *reinterpret_cast<const half8*>(qh + d0);
+        const half8 qb0 = *reinterpret_cast<const half8*>(ql + d0);
+        const half8 qa1 = *reinterpret_cast<const half8*>(qh + d1);
+        const half8 qb1 = *reinterpret_cast<const half8*>(ql + d1);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qa0, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qa0, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qb0, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qa1, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qa1, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qb1, S, 0, 0, 0);
       }
     }
 
@@ -606,35 +637,64 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     l_run = alpha * l_run + rows_sum(es);
     m_run = m_new;
     if (__ballot(upd) != 0) {
+      // head h's factor lives in lane h (row u = 0); accumulators hold heads
+      // 4 hs + i in element i
 #pragma unroll
-      for (int mm = 0; mm < NM; ++mm) acc[mm] *= alpha;
+      for (int hs = 0; hs < NHS; ++hs)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 * hs + i));
+#pragma unroll
+          for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
+        }
     }
 
-    // ---- O^T += V^T P^T on MFMA: A[i = dim 16mm + t][k = token 4u + i'] ----
+    // ---- O += P V on the 4x4x4 MFMA (16 blocks = 16 groups of 4 dims):
+    //      A = P[4 heads][4 tokens] (same for every block, from LDS),
+    //      B = V[4 tokens][dim 64 hf + l] (lane l's own dim) -----------------
+    if (hl < GQA) *reinterpret_cast<half4*>(pt + hl * kTile + 4 * u) = pa;
     // slots without a token get V = 0 (their p is already 0; this keeps
     // whatever bytes an unused slot holds out of the sum)
     if (vmask != 0xFFFFu) {
-      const uint32_t keep = (vmask >> (4 * u)) & 0xFu;
 #pragma unroll
-      for (int mm = 0; mm < NM; ++mm)
+      for (int v = 0; v < DH / 32; ++v)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          vreg[mm][i] = ((keep >> i) & 1u) ? vreg[mm][i] : (_Float16)0.f;
+        for (int e = 0; e < 8; ++e)
+          vreg[v][e] = ((vmask >> (8 * (v & 1) + e)) & 1u) ? vreg[v][e] : (_Float16)0.f;
     }
+    wave_lds_sync();
 #pragma unroll
-    for (int mm = 0; mm < NM; ++mm)
-      acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(vreg[mm], pa, acc[mm], 0, 0, 0);
+    for (int hs = 0; hs < NHS; ++hs) {
+      const half8* prow = reinterpret_cast<const half8*>(pt + (4 * hs + (lane_v & 3)) * kTile);
+      const half8 p0 = prow[0], p1 = prow[1];
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) {
+        const half8 pp = tg < 2 ? p0 : p1;
+        const half4 pa4 = (tg & 1) ? half4{pp[4], pp[5], pp[6], pp[7]} : half4{pp[0], pp[1], pp[2], pp[3]};
+#pragma unroll
+        for (int hf = 0; hf < NHF; ++hf) {
+          const half8 vv = vreg[2 * hf + (tg >> 1)];
+          const half4 vb = (tg & 1) ? half4{vv[4], vv[5], vv[6], vv[7]} : half4{vv[0], vv[1], vv[2], vv[3]};
+          acc[hs][hf] = __builtin_amdgcn_mfma_f32_4x4x4f16(pa4, vb, acc[hs][hf], 0, 0, 0);
+        }
+      }
+    }
 
     // ---- issue V / dense K of the next page into the freed registers ------
-    load_v<DH>(a, row_n, t, u, vreg);
+    load_v<DH>(a, row_n, lane_v, vreg);
     load_dense<DH>(a, row_n, t, u, kd);
     wave_lds_sync();
 
     row_c = row_n;
-    row_n = row_take(a, rl_2, p + 2 * kWaves, re);
-    rl_2 = rl_3;
-    stg_c = stg_n;
-    pos_c = pos_n;
+    row_n = row_take(a, rl_take, p + 2 * kWaves, re);
+  };
+  uint4 stg_b;
+  int pos_b;
+  RowLd rl_3;
+  for (; p < re; p += 2 * kWaves) {
+    step(p, stg_c, pos_c, stg_b, pos_b, rl_3, rl_2);
+    if (p + kWaves >= re) break;
+    step(p + kWaves, stg_b, pos_b, stg_c, pos_c, rl_2, rl_3);
   }
 
   // ---- merge the waves' states in LDS, write this item's partial ----------
@@ -642,12 +702,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   __syncthreads();
   float* mrg = reinterpret_cast<float*>(smem);        // [kWaves][GQA][DH]
   float* mrg_ml = mrg + kWaves * GQA * DH;            // [kWaves][GQA][2]
-  if (hl < GQA) {
 #pragma unroll
-    for (int mm = 0; mm < NM; ++mm)
-      *reinterpret_cast<floatx4*>(mrg + (wave * GQA + hl) * DH + 16 * mm + 4 * u) = acc[mm];
-    if (u == 0) { mrg_ml[(wave * GQA + hl) * 2] = m_run; mrg_ml[(wave * GQA + hl) * 2 + 1] = l_run; }
-  }
+  for (int hs = 0; hs < NHS; ++hs)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * hs + i < GQA)
+#pragma unroll
+        for (int hf = 0; hf < NHF; ++hf) mrg[(wave * GQA + 4 * hs + i) * DH + 64 * hf + lane] = acc[hs][hf][i];
+  if (hl < GQA && u == 0) { mrg_ml[(wave * GQA + hl) * 2] = m_run; mrg_ml[(wave * GQA + hl) * 2 + 1] = l_run; }
   __syncthreads();
   float* part = a.partials + (int64_t)item * PS;
   float* fw = mrg_ml + kWaves * GQA * 2;              // [GQA][kWaves] wave weights 2^(m_w - M)

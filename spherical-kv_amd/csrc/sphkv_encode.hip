@@ -88,28 +88,26 @@ __global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
   int64_t row = tok_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
   if (row >= a.num_src_rows) row = -1;
 
-  // ---- V placement in the decode kernel's MFMA order: element (token 4u+i,
-  //      dim 16mm+tt) of page vs at half ((tt*4 + u) * DH/16 + mm) * 4 + i ----
+  // ---- V placement, dim-major: element (token k, dim d) of page vs at half
+  //      d * 16 + k, so one dim's 16 tokens are 32 contiguous bytes ---------
   if (vs >= 0 && vs < a.num_vpages) {
     constexpr int DPL = DH / 64;  // dims per lane
     for (int dd = 0; dd < DPL; ++dd) {
-      const int d = lane * DPL + dd;
-      const int mm = d / 16, tt = d % 16;
-      for (int uu = 0; uu < 4; ++uu) {
-        half4 q4;
-        for (int i = 0; i < 4; ++i) {
-          const int tok = 4 * uu + i;
-          int64_t rr = -1;
-          if (tok < n) rr = a.src_rows[(int64_t)p * kTile + tok];
-          _Float16 val = (_Float16)0.f;
-          if (rr >= 0 && rr < a.num_src_rows) {
-            __half hv = a.v[rr * DH + d];
-            val = *reinterpret_cast<_Float16*>(&hv);
-          }
-          q4[i] = val;
+      const int d = lane + 64 * dd;
+      half8 h[2];
+      for (int tok = 0; tok < kTile; ++tok) {
+        int64_t rr = -1;
+        if (tok < n) rr = a.src_rows[(int64_t)p * kTile + tok];
+        _Float16 val = (_Float16)0.f;
+        if (rr >= 0 && rr < a.num_src_rows) {
+          __half hv = a.v[rr * DH + d];
+          val = *reinterpret_cast<_Float16*>(&hv);
         }
-        *reinterpret_cast<half4*>(a.v_pool + vs * DH * kTile + ((tt * 4 + uu) * (DH / 16) + mm) * 4) = q4;
+        h[tok >> 3][tok & 7] = val;
       }
+      half8* dst = reinterpret_cast<half8*>(a.v_pool + vs * DH * kTile + d * kTile);
+      dst[0] = h[0];
+      dst[1] = h[1];
     }
   }
 

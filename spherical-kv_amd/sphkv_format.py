@@ -23,10 +23,10 @@ Two additions, both encoded without changing the header layout:
   pointer table stores absolute offsets, so placement is free.
 
 V is kept beside the pages in a pool of fp16 V pages, [num_vpages,
-page_size * dh], each page in the decode kernel's MFMA operand order: element
-(token k, dim d) with d = 16*mm + t and k = 4*u + i lives at
-((t*4 + u) * (dh/16) + mm) * 4 + i within its page (see v_page_index).  Row p
-of the pointer table uses V page vslot[p].
+page_size * dh], each page dim-major: element (token k, dim d) lives at
+d * 16 + k within its page (see v_page_index), so the 16 tokens of one dim are
+32 contiguous bytes, the decode kernel's PV operand.  Row p of the pointer
+table uses V page vslot[p].
 """
 from __future__ import annotations
 
@@ -198,9 +198,7 @@ def v_page_index(dh: int) -> np.ndarray:
     """[16, dh] int: position of element (token k, dim d) inside a V page."""
     k = np.arange(16)[:, None]
     d = np.arange(dh)[None, :]
-    mm, t = d // 16, d % 16
-    u, i = k // 4, k % 4
-    return ((t * 4 + u) * (dh // 16) + mm) * 4 + i
+    return d * 16 + k
 
 
 def rope_inv_freq(dh: int, theta: float) -> np.ndarray:

@@ -109,14 +109,14 @@ def validate_plan(plan: fmt.PagePlan) -> None:
 @dataclass
 class PagedPool:
     """Device-resident paged KV of one layer: byte pool, pointer table,
-    positions, token-minor V pages, per-tier codebooks and the decode work
+    positions, dim-major V pages, per-tier codebooks and the decode work
     list."""
     plan: fmt.PagePlan
     pages: torch.Tensor        # uint8 [pages_bytes]
     ptable: torch.Tensor       # int32 [P, 3]
     vslot: torch.Tensor        # int32 [P]
     positions: torch.Tensor    # int32 [P, 16]
-    v_pool: torch.Tensor       # fp16 [num_vpages, 16 * dh] (MFMA operand order)
+    v_pool: torch.Tensor       # fp16 [num_vpages, 16 * dh] (dim-major pages: [dh][16])
     codebooks: Dict[int, torch.Tensor]   # tier -> fp32 [num_kv, G, C, g]
     work: torch.Tensor         # int32 [n_items, 3]
     work_start: torch.Tensor   # int32 [num_seqs*num_kv + 1]
