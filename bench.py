@@ -50,8 +50,9 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # (FETCH_SIZE * 2 + WRITE_SIZE) KiB per dispatch.  On this part FETCH_SIZE
 # reads exactly half of a plain device copy's bytes (256 MiB copy -> 131083
 # KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
-# with `bench.py --calibrate`; re-measured whenever the kernel changes.
-TRAFFIC_BYTES = {}
+# with `bench.py --calibrate` under rocprofv3 --pmc (summary and commands in
+# profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
+TRAFFIC_BYTES = {(2, "default"): 85747275}
 
 
 def measured_traffic(config, layout):

@@ -87,6 +87,9 @@ int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_
     return fail(SPHKV_EINVAL, "%s: negative size", fn);
   if ((phases & sphkv::kPhasePartials) && !(rope_theta > 1.0))
     return fail(SPHKV_EINVAL, "%s: rope_theta must be > 1", fn);
+  if ((phases & sphkv::kPhasePartials) &&
+      (pages_bytes < 0 || pages_bytes > 0x7FFFFF00LL || (int64_t)num_rows * 64 > 0x7FFFFF00LL))
+    return fail(SPHKV_EINVAL, "%s: byte pool and pointer table must stay below 2 GiB", fn);
   const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
   if (workspace_bytes < need)
     return fail(SPHKV_EINVAL, "%s: workspace too small (%lld < %lld bytes)", fn,

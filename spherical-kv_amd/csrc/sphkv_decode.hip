@@ -80,21 +80,36 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
 }
 
+// Buffer resources of the kernel-wide arrays, built once per wave (scalar
+// registers).  Loads of absent data use an offset beyond every resource
+// (kOOB) and return zeros.  The byte pool, pointer table and positions are
+// below 2 GiB (checked by the host), so 32-bit offsets address them.
+struct Res {
+  rsrc_t pages, ptab, vslot, pos;
+};
+
+__device__ __forceinline__ Res make_res(const DecodeArgs& a) {
+  Res r;
+  r.pages = make_rsrc(a.pages, a.pages_bytes);
+  r.ptab = make_rsrc(a.ptable, (int64_t)a.num_rows * 12);
+  r.vslot = make_rsrc(a.vslot, (int64_t)a.num_rows * 4);
+  r.pos = make_rsrc(a.positions, (int64_t)a.num_rows * 4 * kTile);
+  return r;
+}
+
 // Pointer-table row of one page (wave-uniform): lanes 0..2 fetch the row,
 // lane 3 the V slot; the values are read out (readlane) only when needed.
 struct RowLd { int x, y; };
 struct Row {
-  int64_t page_off, th_off, rad_off, vs;
+  int page_off, th_off, rad_off, vs;
   bool ok;
 };
 
-__device__ __forceinline__ RowLd row_issue(const DecodeArgs& a, int p, int re, int lane) {
+__device__ __forceinline__ RowLd row_issue(const Res& rs, int p, int re, int lane) {
   const bool ok = p < re;
-  const rsrc_t rp = make_rsrc(a.ptable + 3 * (int64_t)(ok ? p : 0), ok ? 12 : 0);
-  const rsrc_t rv = make_rsrc(a.vslot + (ok ? p : 0), ok ? 4 : 0);
   RowLd l;
-  l.x = __builtin_amdgcn_raw_buffer_load_b32(rp, lane < 3 ? 4 * lane : kOOB, 0, 0);
-  l.y = __builtin_amdgcn_raw_buffer_load_b32(rv, lane == 3 ? 0 : kOOB, 0, 0);
+  l.x = __builtin_amdgcn_raw_buffer_load_b32(rs.ptab, (ok && lane < 3) ? 12 * p + 4 * lane : kOOB, 0, 0);
+  l.y = __builtin_amdgcn_raw_buffer_load_b32(rs.vslot, (ok && lane == 3) ? 4 * p : kOOB, 0, 0);
   return l;
 }
 
@@ -104,7 +119,7 @@ __device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int
   r.th_off = __builtin_amdgcn_readlane(l.x, 1);
   r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
   r.vs = __builtin_amdgcn_readlane(l.y, 3);
-  r.ok = p < re && r.page_off >= 0 && r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
+  r.ok = p < re && r.page_off >= 0 && (int64_t)r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
          r.vs >= 0 && r.vs < a.num_vpages;
   if (!r.ok) { r.page_off = 0; r.th_off = 0; r.rad_off = 0; r.vs = 0; }
   return r;
@@ -115,20 +130,19 @@ __device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int
 // decides how the page is processed.
 template <int DH>
 __device__ __forceinline__ bool row_looks_dense(const Row& r) {
-  return r.ok && (r.rad_off - r.th_off) >= 2 * DH && (r.th_off & 15) == 0;
+  return r.ok && (r.rad_off - r.th_off) >= 2 * DH && (r.th_off & 15) == 0 && r.th_off >= 0;
 }
 
-// 512-byte staging window [page_off & ~15, +512) of a page: lanes < 32 hold 16 bytes each.
-__device__ __forceinline__ uint4 load_stage(const DecodeArgs& a, const Row& r, int lane) {
-  const int64_t base = r.page_off & ~(int64_t)15;
-  const rsrc_t rs = make_rsrc(a.pages + base, r.ok ? (a.pages_bytes - base < 512 ? a.pages_bytes - base : 512) : 0);
-  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane < 32 ? 16 * lane : kOOB, 0, 0);
+// 512-byte staging window [page_off & ~15, +512) of a page: lanes < 32 hold
+// 16 bytes each (bytes past the end of the pool read as zero).
+__device__ __forceinline__ uint4 load_stage(const Res& rs, const Row& r, int lane) {
+  const int off = (r.ok && lane < 32) ? (r.page_off & ~15) + 16 * lane : kOOB;
+  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, off, 0, 0);
   return uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
 }
 
-__device__ __forceinline__ int load_pos(const DecodeArgs& a, const Row& r, int p, int t) {
-  const rsrc_t rs = make_rsrc(a.positions + (int64_t)(r.ok ? p : 0) * kTile, r.ok ? 4 * kTile : 0);
-  return __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * t, 0, 0);
+__device__ __forceinline__ int load_pos(const Res& rs, const Row& r, int p, int t) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rs.pos, r.ok ? (p * kTile + t) * 4 : kOOB, 0, 0);
 }
 
 // V page layout, dim-major: element (token k, dim d) at half d * 16 + k.  Lane
@@ -163,20 +177,20 @@ __host__ __device__ constexpr int chunk_dim(int c, int u) {
 // resource covers the page's theta section only when the pointer-table row
 // describes a dense page, so compressed pages cost no traffic here.
 template <int DH>
-__device__ __forceinline__ void load_dense(const DecodeArgs& a, const Row& r, int t, int u, uint4 (&kd)[DH / 32]) {
-  const bool dense = row_looks_dense<DH>(r);
-  const int64_t room = a.pages_bytes - r.th_off;
-  const int64_t len = r.rad_off - r.th_off;
-  const int64_t nb = dense ? (len < room ? len : room) : 0;
-  const rsrc_t rs = make_rsrc(a.pages + (dense ? r.th_off : 0), nb);
+__device__ __forceinline__ void load_dense(const Res& rs, const Row& r, int t, int u, uint4 (&kd)[DH / 32]) {
+  const bool dense = row_looks_dense<DH>(r) && (int64_t)r.th_off + (int64_t)(t + 1) * DH * 2 <= r.rad_off;
 #pragma unroll
   for (int c = 0; c < DH / 32; ++c) {
-    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, (t * DH + chunk_dim<DH>(c, u)) * 2, 0, 0);
+    const int off = dense ? r.th_off + (t * DH + chunk_dim<DH>(c, u)) * 2 : kOOB;
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, off, 0, 0);
     kd[c] = uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
   }
 }
 
-constexpr int kWaves = 12;             // waves per decode workgroup (3 per SIMD)
+// Waves per decode workgroup: 16 (4 per SIMD) where the register and LDS
+// budgets allow it (GQA <= 4), else 12 (3 per SIMD).
+template <int GQA>
+__host__ __device__ constexpr int decode_waves() { return GQA <= 4 ? 16 : 12; }
 constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| < kDelta
 
 __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
@@ -194,6 +208,7 @@ __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 //    GQA stay zero), read back as the PV MFMA's A operand.
 template <int DH, int GQA>
 struct DecodeLds {
+  static constexpr int kWaves = decode_waves<GQA>();
   static constexpr int NJ = DH / 2;
   __host__ __device__ static constexpr int cb_pad(int g) { return g + 4; }
   static constexpr int cb_n1 = (DH / 16) * 64 * 20;
@@ -349,7 +364,9 @@ __device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8&
 }
 
 template <int DH, int GQA>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(decode_waves<GQA>() * 64)
+__attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() / 4))) void decode_kernel(DecodeArgs a) {
+  constexpr int kWaves = decode_waves<GQA>();
   constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
   constexpr int NP = NC / 2;         // chunks holding the first RoPE half
   constexpr int NJ = DH / 2;         // RoPE frequencies
@@ -373,10 +390,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   _Float16* qr = reinterpret_cast<_Float16*>(smem + L::o_qr) + wave * L::qr_wave;   // [hi, lo][GQA][qrow]
 
   int p = rb + wave;
+  const Res rs = make_res(a);
   // ---- first pages' pointer-table rows, then the shared tables' loads ----
-  RowLd rl_c = row_issue(a, p, re, lane);
-  RowLd rl_n = row_issue(a, p + kWaves, re, lane);
-  RowLd rl_2 = row_issue(a, p + 2 * kWaves, re, lane);
+  RowLd rl_c = row_issue(rs, p, re, lane);
+  RowLd rl_n = row_issue(rs, p + kWaves, re, lane);
+  RowLd rl_2 = row_issue(rs, p + 2 * kWaves, re, lane);
   // codebooks: every load of a thread is issued before its first LDS store
   constexpr int kT = kWaves * 64;
   constexpr int n4_1 = L::cb_n1 / 20 * 4, n4_2 = L::cb_n2 / 20 * 4, n4_3 = L::cb_n3 / 36 * 8;  // float4s
@@ -417,12 +435,12 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
   }
   // first page's data and the next page's row
   Row row_c = row_take(a, rl_c, p, re);
-  uint4 stg_c = load_stage(a, row_c, lane);
-  int pos_c = load_pos(a, row_c, p, t);
+  uint4 stg_c = load_stage(rs, row_c, lane);
+  int pos_c = load_pos(rs, row_c, p, t);
   half8 vreg[DH / 32];
   load_v<DH>(a, row_c, lane, vreg);
   uint4 kd[NC];
-  load_dense<DH>(a, row_c, t, u, kd);
+  load_dense<DH>(rs, row_c, t, u, kd);
   Row row_n = row_take(a, rl_n, p + kWaves, re);
   {
     int slot = 0;
@@ -484,9 +502,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
     // ---- issue: row three pages ahead, stage/positions one page ahead -----
-    rl_issue = row_issue(a, p + 3 * kWaves, re, lane);
-    stg_n = load_stage(a, row_n, lane);
-    pos_n = load_pos(a, row_n, p + kWaves, t);
+    rl_issue = row_issue(rs, p + 3 * kWaves, re, lane);
+    stg_n = load_stage(rs, row_n, lane);
+    pos_n = load_pos(rs, row_n, p + kWaves, t);
 
     // ---- this page's header (lane 0's 16 bytes of the stage) --------------
     const int rel = (int)(row_c.page_off & 15);
@@ -531,12 +549,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
     if (tid >= 1 && tid <= 3) {
       if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
       wave_lds_sync();
-      const int64_t base = row_c.page_off & ~(int64_t)15;
-      const int64_t thr64 = row_c.th_off - base, rdr64 = row_c.rad_off - base;
+      const int base = row_c.page_off & ~15;
+      const int thr0 = row_c.th_off - base, rdr0 = row_c.rad_off - base;   // offsets are < 2^31
       const int g = tier_g(tid), b = tier_b(tid);
       const int G = DH / g;
-      const bool ok = thr64 >= 0 && rdr64 >= 0 && rdr64 + n * G <= 512 && thr64 + (n * G * b + 7) / 8 + 2 < 512;
-      const int thr = ok ? (int)thr64 : 0, rdr = ok ? (int)rdr64 : 0;
+      const bool ok = row_c.th_off >= base && row_c.rad_off >= base && thr0 <= 512 && rdr0 <= 512 &&
+                      rdr0 + n * G <= 512 && thr0 + (n * G * b + 7) / 8 + 2 < 512;
+      const int thr = ok ? thr0 : 0, rdr = ok ? rdr0 : 0;
       if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
       else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
       else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
@@ -682,7 +701,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 
 
     // ---- issue V / dense K of the next page into the freed registers ------
     load_v<DH>(a, row_n, lane_v, vreg);
-    load_dense<DH>(a, row_n, t, u, kd);
+    load_dense<DH>(rs, row_n, t, u, kd);
     wave_lds_sync();
 
     row_c = row_n;
@@ -828,7 +847,7 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.log2_theta = __builtin_log2(L.rope_theta);
   if (L.num_items > 0) {
     if (phases & kPhasePartials)
-      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(kWaves * 64), 0, stream, a);
+      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream, a);
     const int nsh = L.num_seqs * L.num_kv;
     if ((phases & kPhaseMerge) && nsh > 0)
       hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
