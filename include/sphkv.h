@@ -166,6 +166,83 @@ int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const i
                               int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
                               int32_t page_size, float* logits_out, void* stream);
 
+/*
+ * ---- Mode-A (LayerPool) path -------------------------------------------
+ * Unpacked pools as sphkv_lut.py:71-80 builds them:
+ *   theta_codes, radius_codes  uint8 [num_pages, page_size, G_max]
+ *   r_scales                   fp32  [num_pages, G_max]
+ *   v_pool                     fp16  [num_pages, page_size, dh] (token-major)
+ *   block_table, bits_table    int32 [num_kv, max_blocks]: pool page (-1 =
+ *                              none) and tier index of each logical page
+ *   cb_flat                    fp32  [num_kv, num_tiers, G_max, cb_max, g_max]
+ *   tier_G, tier_g             int32 [num_tiers]
+ * Radius r_hat = r_scale * code / 255.  No RoPE: q and the encoded keys are
+ * post-RoPE.
+ */
+
+/*
+ * Decode-time single-token encode + append (decode_kernel.cu:10-84, called by
+ * fused_decode.py:28-35 from sphkv_lut.py:176-183).  For every kv head h:
+ * v_pool[pids[h], slot] = fp16(v_new[h]); per group the first-max argmax of
+ * <k_g / (|k_g| + 1e-8), centroid> over decode_cb [num_kv, G, C, g], its code
+ * into theta_codes, and the radius against the page's running-max scale
+ * (is_new_page: scale = |k_g|; else a larger |k_g| rescales the page's
+ * earlier radius codes).  Bit-exact with the reference arithmetic (nvcc's
+ * contraction of a*b + c to fmaf, IEEE sqrt / divide, roundf).
+ * k_post, v_new fp32 [num_kv, dh]; pids int64 [num_kv] (pool pages; a pid
+ * outside [0, num_pages) is skipped).  dh <= 256, G * g <= dh, G * C <= 4096.
+ */
+int sphkv_encode_append(const float* k_post, const float* v_new, const float* decode_cb,
+                        uint8_t* theta_codes, uint8_t* radius_codes, float* r_scales, uint16_t* v_pool,
+                        const int64_t* pids, int32_t num_kv, int64_t num_pages, int32_t slot, int32_t G,
+                        int32_t g, int32_t C, int32_t G_max, int32_t dh, int32_t page_size,
+                        int32_t is_new_page, void* stream);
+
+/*
+ * Mode-A decode (fused_decode.py:12-26 -> decode_kernel.cu:108-289).
+ * q_all fp32 [num_q, dh] (num_q = num_kv * kv_groups); out fp32 [num_q, dh];
+ * partial_scratch fp32 [num_q, max_blocks, dh + 2].  Per q head and logical
+ * page, partial_scratch[hq, p, 0:2] = the page's (m, l): m = max logit, l =
+ * sum exp(logit - m), logit = sm_scale * sum_g r_hat_g <q_g, centroid_g[code]>
+ * (-1e9 where that sum is exactly 0, as the reference masks unwritten slots);
+ * (-inf, 0) for absent pages.  out = softmax-weighted V over all pages,
+ * acc / (l + 1e-8).  The rest of partial_scratch is scratch.  ctx_lens and
+ * max_ctx are accepted for the reference signature and unused, as there.
+ * dh in {64, 128}; kv_groups 1..8; page_size a multiple of 16 up to 128.
+ */
+int sphkv_decode_modea(const float* q_all, const float* cb_flat, const int32_t* tier_G, const int32_t* tier_g,
+                       const uint8_t* theta_codes, const uint8_t* radius_codes, const float* r_scales,
+                       const uint16_t* v_pool, int64_t num_pages, const int32_t* block_table,
+                       const int32_t* bits_table, const int32_t* ctx_lens, float* out, float* partial_scratch,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers,
+                       int32_t max_blocks, int32_t page_size, int32_t dh, int32_t G_max, int32_t cb_max,
+                       int32_t g_max, float sm_scale, int32_t max_ctx, void* stream);
+
+/*
+ * Per-query q.centroid table (the q_lut that new_fused_decode.py:22-43
+ * consumes): q_lut fp32 [num_q, num_tiers, G_max, cb_max],
+ * q_lut[hq, t, g, c] = sum_{d < tier_g[t]} q[hq, g*tier_g[t] + d] *
+ * cb_flat[hq / kv_groups, t, g, c, d] for g < tier_G[t], else 0.
+ * No reference counterpart (the reference never builds the table).
+ */
+int sphkv_q_lut(const float* q_all, const float* cb_flat, const int32_t* tier_G, const int32_t* tier_g,
+                int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers, int32_t dh,
+                int32_t G_max, int32_t cb_max, int32_t g_max, float* q_lut, void* stream);
+
+/*
+ * Logits from a q_lut (new_fused_decode.py:22-43): logits_out fp32
+ * [num_q, max_ctx]; token n of kv head hkv = hq / kv_groups is slot
+ * n % page_size of logical page n / page_size; logit = sm_scale *
+ * sum_{g < G_max} r_hat_g * q_lut[hq, tier, g, code_g]; -inf for
+ * n >= ctx_lens[hkv] or an absent page.
+ */
+int sphkv_logits_lut(const float* q_lut, const uint8_t* theta_codes, const uint8_t* radius_codes,
+                     const float* r_scales, int64_t num_pages, const int32_t* block_table,
+                     const int32_t* bits_table, const int32_t* ctx_lens, float* logits_out,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers,
+                     int32_t max_blocks, int32_t page_size, int32_t G_max, int32_t cb_size_max,
+                     float sm_scale, int32_t max_ctx, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

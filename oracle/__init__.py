@@ -25,6 +25,15 @@ Contents and the reference lines each part restates (reference repo paths):
                               (call sites spherical_kv_pipeline.py:1102-1125,
                               1865-1870) evaluated with the caller's cos/sin
                               tables.
+* Mode-A (LayerPool) path:
+  encode_append (C)           decode_kernel.cu:10-84, nvcc's FP contraction
+                              written out (bit-exact target)
+  decode_mode_a               decode_kernel.cu:108-246 in fp64: per (q head,
+                              page) logits sum_g r_hat_g <q_g, c> * sm_scale
+                              (-1e9 where the sum is 0, :183), page (m, l, acc),
+                              merge out = acc / (l + 1e-8) (:244)
+  q_lut, lut_logits           the per-query table and the logits of
+                              new_fused_decode.py:22-43 (fp64)
 
 Pins (see tests/test_oracle.py): hand-written known answers for pack_bits and
 the header, brute-force fp64 argmax on unambiguous groups, committed golden
@@ -74,6 +83,8 @@ def _load():
         lib.orc_page_bytes.restype = ctypes.c_int64
         lib.orc_build_page.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
         lib.orc_build_page.restype = ctypes.c_int64
+        lib.orc_encode_append.argtypes = [P, P, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         _lib = lib
     return _lib
 
@@ -301,4 +312,103 @@ def ragged_logits(pages, ptable, head_ids, positions, cos_tbl, sin_tbl, q, grp, 
                            cw[valid], r_hat[valid], None, G, g)
         for j, i in enumerate(valid):
             out[:, p * page_size + i] = lg[:, j]
+    return out
+
+
+# ------------------------------------------------------------- Mode A --
+def encode_append(k_post: np.ndarray, v_new: np.ndarray, decode_cb: np.ndarray, theta: np.ndarray,
+                  radius: np.ndarray, r_scales: np.ndarray, v_pool: np.ndarray, pids: np.ndarray,
+                  slot: int, is_new_page: bool) -> None:
+    """decode_kernel.cu:10-84 on numpy pools, in place.  k_post / v_new fp32
+    [num_kv, dh]; decode_cb fp32 [num_kv, G, C, g]; theta / radius uint8
+    [n_pages, page_size, G_max]; r_scales fp32 [n_pages, G_max]; v_pool fp16
+    [n_pages, page_size, dh]; pids int64 [num_kv]."""
+    lib = _load()
+    num_kv, dh = k_post.shape
+    _, G, C, g = decode_cb.shape
+    n_pages, page_size, G_max = theta.shape
+    for a in (theta, radius, r_scales, v_pool):
+        assert a.flags.c_contiguous
+    for h in range(num_kv):
+        pid = int(pids[h])
+        if pid < 0 or pid >= n_pages:
+            continue
+        v_pool[pid, slot] = v_new[h].astype(np.float16)
+        k = np.ascontiguousarray(k_post[h], np.float32)
+        cb = np.ascontiguousarray(decode_cb[h], np.float32)
+        lib.orc_encode_append(_ptr(k), _ptr(cb), _ptr(theta), _ptr(radius), _ptr(r_scales), pid, int(slot), G, g, C,
+                              G_max, page_size, 1 if is_new_page else 0)
+
+
+def q_lut(q_all: np.ndarray, cb_flat: np.ndarray, tier_G, tier_g, kv_groups: int) -> np.ndarray:
+    """[num_q, num_tiers, G_max, cb_max] fp64: <q_g, centroid> per tier, group, code."""
+    num_q, dh = q_all.shape
+    _, T, G_max, cb_max, g_max = cb_flat.shape
+    out = np.zeros((num_q, T, G_max, cb_max))
+    for hq in range(num_q):
+        hkv = hq // kv_groups
+        for t in range(T):
+            Gt, gt = int(tier_G[t]), int(tier_g[t])
+            for gi in range(Gt):
+                qg = q_all[hq, gi * gt:(gi + 1) * gt].astype(np.float64)
+                out[hq, t, gi] = cb_flat[hkv, t, gi, :, :gt].astype(np.float64) @ qg
+    return out
+
+
+def decode_mode_a(q_all, cb_flat, tier_G, tier_g, theta, radius, r_scales, v_pool, block_table, bits_table,
+                  kv_groups: int, sm_scale: float):
+    """decode_kernel.cu:108-246 in fp64.  Returns (out [num_q, dh], m [num_q,
+    max_blocks], l [num_q, max_blocks]) with m = -inf, l = 0 for absent pages."""
+    num_q, dh = q_all.shape
+    num_kv, max_blocks = block_table.shape
+    page_size = theta.shape[1]
+    lut = q_lut(q_all, cb_flat, tier_G, tier_g, kv_groups)
+    out = np.zeros((num_q, dh))
+    M = np.full((num_q, max_blocks), -np.inf)
+    Lp = np.zeros((num_q, max_blocks))
+    for hq in range(num_q):
+        hkv = hq // kv_groups
+        accs, ms, ls = [], [], []
+        for p in range(max_blocks):
+            phys, t = int(block_table[hkv, p]), int(bits_table[hkv, p])
+            if phys < 0 or phys >= theta.shape[0] or t < 0 or t >= cb_flat.shape[1]:
+                continue
+            Gt = int(tier_G[t])
+            rh = r_scales[phys, :Gt].astype(np.float64)[None, :] * radius[phys, :, :Gt].astype(np.float64) / 255.0
+            vals = lut[hq, t, np.arange(Gt)[None, :], theta[phys, :, :Gt].astype(np.int64)]
+            s = (rh * vals).sum(axis=1)
+            lg = np.where(s == 0.0, -1e9, s * sm_scale)
+            m = lg.max()
+            e = np.exp(lg - m)
+            M[hq, p], Lp[hq, p] = m, e.sum()
+            ms.append(m)
+            ls.append(e.sum())
+            accs.append(e @ v_pool[phys].astype(np.float64))
+        if ms:
+            Mx = max(ms)
+            f = np.exp(np.array(ms) - Mx)
+            out[hq] = (f[:, None] * np.array(accs)).sum(0) / ((f * np.array(ls)).sum() + 1e-8)
+    return out, M, Lp
+
+
+def lut_logits(lut, theta, radius, r_scales, block_table, bits_table, ctx_lens, kv_groups: int,
+               sm_scale: float, max_ctx: int) -> np.ndarray:
+    """new_fused_decode.py:22-43 contract in fp64: [num_q, max_ctx]."""
+    num_q, T, G_max, cb_max = lut.shape
+    num_kv, max_blocks = block_table.shape
+    page_size = theta.shape[1]
+    out = np.full((num_q, max_ctx), -np.inf)
+    for hq in range(num_q):
+        hkv = hq // kv_groups
+        for n in range(min(max_ctx, int(ctx_lens[hkv]))):
+            lb, s = divmod(n, page_size)
+            if lb >= max_blocks:
+                break
+            phys, t = int(block_table[hkv, lb]), int(bits_table[hkv, lb])
+            if phys < 0 or phys >= theta.shape[0] or t < 0 or t >= T:
+                continue
+            rh = r_scales[phys].astype(np.float64) * radius[phys, s].astype(np.float64) / 255.0
+            codes = theta[phys, s].astype(np.int64)
+            vals = np.where(codes < cb_max, lut[hq, t, np.arange(G_max), np.minimum(codes, cb_max - 1)], 0.0)
+            out[hq, n] = (rh * vals).sum() * sm_scale
     return out

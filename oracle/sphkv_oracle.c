@@ -14,6 +14,8 @@
  *   orc_radius_codes       pagebuilder.py:17-21        int8 radius codes
  *   orc_build_page         pagebuilder.py:8-33 + paging.py:20-31
  *   orc_page_bytes         spherical_kv_pipeline.py:1202-1205 (section sizes)
+ *   orc_encode_append      decode_kernel.cu:10-84 (Mode-A single-token encode +
+ *                          append with the running-max radius scale)
  *
  * Floating-point order.  The reference runs these ops on torch CPU in fp32.
  * Bit-exact parity needs the exact operation order torch uses, which was
@@ -31,6 +33,12 @@
  *   - argmax returns the first index of the maximum (strict '>').
  * Compile without -ffast-math and with -ffp-contract=off so that every
  * fmaf / '*' / '+' / '/' below is exactly one IEEE operation.
+ *
+ * orc_encode_append restates CUDA device code instead: nvcc (default
+ * -fmad=true) contracts each `acc += a * b` and `acc += (a * b) * c` into one
+ * fmaf with the last product, keeps IEEE sqrtf and '/' (-prec-sqrt,
+ * -prec-div), and roundf rounds half away from zero.  Those contractions are
+ * written out as fmaf below.
  */
 #include <math.h>
 #include <stdint.h>
@@ -168,4 +176,56 @@ int64_t orc_build_page(const float* r, const int32_t* codes, int N, int G,
     int64_t tb = ((int64_t)N * G * b_theta + 7) / 8;
     memcpy(th + tb, rc, (size_t)N * G);
     return ORC_HEADER_BYTES + 4 * (int64_t)G + tb + (int64_t)N * G;
+}
+
+/*
+ * decode_kernel.cu:10-84 for one kv head h.  Pools: theta / radius uint8
+ * [n_pages, page_size, G_max], r_scales fp32 [n_pages, G_max], v_pool fp16
+ * bits (uint16) [n_pages, page_size, dh].  k, v fp32 [dh]; cb fp32 [G, C, g]
+ * (this head's decode codebook).  v is rounded to fp16 by the caller (the
+ * kernel writes __float2half, round to nearest even).
+ */
+void orc_encode_append(const float* k, const float* cb, uint8_t* theta, uint8_t* radius, float* r_scales,
+                       int64_t pid, int slot, int G, int g, int C, int G_max, int page_size, int is_new_page)
+{
+    const int64_t code_base = (pid * page_size + slot) * G_max;
+    for (int grp = 0; grp < G; ++grp) {
+        const float* kg = k + grp * g;
+        float norm_sq = 0.f;
+        for (int d = 0; d < g; ++d) norm_sq = fmaf(kg[d], kg[d], norm_sq);          /* :47-48 */
+        const float norm = sqrtf(norm_sq + 1e-16f);                                 /* :49 */
+        const float inv_norm = 1.0f / (norm + 1e-8f);                               /* :50 */
+        const float* cbg = cb + (int64_t)grp * C * g;
+        float best_sim = -1e30f;
+        int best_code = 0;
+        for (int c = 0; c < C; ++c) {                                               /* :52-61 */
+            float sim = 0.f;
+            for (int d = 0; d < g; ++d) sim = fmaf(kg[d] * inv_norm, cbg[c * g + d], sim);
+            if (sim > best_sim) { best_sim = sim; best_code = c; }
+        }
+        theta[code_base + grp] = (uint8_t)best_code;
+        float r_scale;                                                              /* :66-82 */
+        if (is_new_page) {
+            r_scales[pid * G_max + grp] = norm;
+            r_scale = norm;
+        } else {
+            const float prev = r_scales[pid * G_max + grp];
+            if (norm > prev) {
+                const float ratio = prev / (norm + 1e-8f);
+                for (int t = 0; t < slot; ++t) {
+                    uint8_t* rc = radius + (pid * page_size + t) * G_max + grp;
+                    float x = (float)(*rc) * ratio;
+                    x = fminf(fmaxf(roundf(x), 0.f), 255.f);
+                    *rc = (uint8_t)x;
+                }
+                r_scales[pid * G_max + grp] = norm;
+                r_scale = norm;
+            } else {
+                r_scale = prev;
+            }
+        }
+        float r_q = roundf(norm / (r_scale + 1e-8f) * 255.0f);                      /* :83-85 */
+        r_q = fminf(fmaxf(r_q, 0.f), 255.f);
+        radius[code_base + grp] = (uint8_t)r_q;
+    }
 }

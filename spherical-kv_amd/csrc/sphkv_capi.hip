@@ -175,3 +175,127 @@ int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const i
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Mode-A (LayerPool) path
+// ---------------------------------------------------------------------------
+namespace {
+
+bool modea_geometry(const char* fn, int32_t num_q, int32_t num_kv, int32_t kv_groups, int32_t num_tiers,
+                    int32_t dh, int32_t G_max, int32_t cb_max, int32_t g_max, int* rc) {
+  if (num_kv < 0 || kv_groups < 1 || kv_groups > 8 || num_q != num_kv * kv_groups) {
+    *rc = fail(SPHKV_EINVAL, "%s: need num_q_heads == num_kv_heads * kv_groups, kv_groups 1..8", fn);
+    return false;
+  }
+  if (num_tiers < 1 || num_tiers > sphkv::kModeAMaxTiers) {
+    *rc = fail(SPHKV_EINVAL, "%s: num_tiers must be 1..%d", fn, sphkv::kModeAMaxTiers);
+    return false;
+  }
+  if (G_max < 1 || cb_max < 1 || cb_max > 256 || g_max < 1 || G_max * g_max < 1 || dh < 1) {
+    *rc = fail(SPHKV_EINVAL, "%s: bad table geometry (G_max %d, cb_max %d, g_max %d)", fn, G_max, cb_max, g_max);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sphkv_encode_append(const float* k_post, const float* v_new, const float* decode_cb,
+                        uint8_t* theta_codes, uint8_t* radius_codes, float* r_scales, uint16_t* v_pool,
+                        const int64_t* pids, int32_t num_kv, int64_t num_pages, int32_t slot, int32_t G,
+                        int32_t g, int32_t C, int32_t G_max, int32_t dh, int32_t page_size,
+                        int32_t is_new_page, void* stream) {
+  const char* fn = "sphkv_encode_append";
+  if (dh < 1 || dh > 256) return fail(SPHKV_EINVAL, "%s: dh must be 1..256 (got %d)", fn, dh);
+  if (G < 1 || g < 1 || G * g > dh || G > G_max)
+    return fail(SPHKV_EINVAL, "%s: need 1 <= G <= G_max and G * g <= dh", fn);
+  if (C < 1 || C > 256 || G * C > 4096) return fail(SPHKV_EINVAL, "%s: need C <= 256 and G * C <= 4096", fn);
+  if (page_size < 1 || slot < 0 || slot >= page_size)
+    return fail(SPHKV_EINVAL, "%s: slot must be in [0, page_size)", fn);
+  if (num_kv < 0 || num_pages < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (num_kv == 0) return ok();
+  if (!k_post || !v_new || !decode_cb || !theta_codes || !radius_codes || !r_scales || !v_pool || !pids)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::AppendLaunch L{k_post, v_new, decode_cb, theta_codes, radius_codes, r_scales,
+                        reinterpret_cast<_Float16*>(v_pool), pids, num_pages, num_kv, slot, G, g, C,
+                        G_max, dh, page_size, is_new_page ? 1 : 0};
+  return launch_status(sphkv::launch_append(L, (hipStream_t)stream), fn);
+}
+
+int sphkv_decode_modea(const float* q_all, const float* cb_flat, const int32_t* tier_G, const int32_t* tier_g,
+                       const uint8_t* theta_codes, const uint8_t* radius_codes, const float* r_scales,
+                       const uint16_t* v_pool, int64_t num_pages, const int32_t* block_table,
+                       const int32_t* bits_table, const int32_t* ctx_lens, float* out, float* partial_scratch,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers,
+                       int32_t max_blocks, int32_t page_size, int32_t dh, int32_t G_max, int32_t cb_max,
+                       int32_t g_max, float sm_scale, int32_t max_ctx, void* stream) {
+  const char* fn = "sphkv_decode_modea";
+  (void)ctx_lens;
+  (void)max_ctx;
+  int rc = 0;
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (!modea_geometry(fn, num_q_heads, num_kv_heads, kv_groups, num_tiers, dh, G_max, cb_max, g_max, &rc))
+    return rc;
+  if (page_size < 16 || page_size > 128 || page_size % 16 != 0)
+    return fail(SPHKV_EINVAL, "%s: page_size must be a multiple of 16 in 16..128 (got %d)", fn, page_size);
+  if (max_blocks < 0 || num_pages < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  const int nhp = kv_groups <= 4 ? 1 : 2;
+  const int64_t lds = sphkv::modea_split_lds_bytes(dh, nhp, num_tiers, G_max, cb_max, page_size);
+  if (lds > 160 * 1024)
+    return fail(SPHKV_EINVAL, "%s: per-query tables need %lld bytes of LDS (> 160 KiB)", fn, (long long)lds);
+  if (num_kv_heads == 0 || max_blocks == 0) return ok();
+  if (!q_all || !cb_flat || !tier_G || !tier_g || !theta_codes || !radius_codes || !r_scales || !v_pool ||
+      !block_table || !bits_table || !out || !partial_scratch)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  // ranges of logical pages: about two workgroups per CU, each range >= 2 pages
+  int nsplit = (512 + num_kv_heads - 1) / num_kv_heads;
+  if (nsplit > max_blocks / 2) nsplit = max_blocks / 2;
+  if (nsplit < 1) nsplit = 1;
+  const int ppw = max_blocks / nsplit;
+  sphkv::ModeALaunch L{q_all, cb_flat, tier_G, tier_g, theta_codes, radius_codes, r_scales,
+                       reinterpret_cast<const _Float16*>(v_pool), block_table, bits_table, out, partial_scratch,
+                       num_q_heads, num_kv_heads, kv_groups, num_tiers, max_blocks, page_size, dh, G_max,
+                       cb_max, g_max, num_pages, sm_scale, nsplit, ppw};
+  return launch_status(sphkv::launch_modea(L, (hipStream_t)stream), fn);
+}
+
+int sphkv_q_lut(const float* q_all, const float* cb_flat, const int32_t* tier_G, const int32_t* tier_g,
+                int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers, int32_t dh,
+                int32_t G_max, int32_t cb_max, int32_t g_max, float* q_lut, void* stream) {
+  const char* fn = "sphkv_q_lut";
+  int rc = 0;
+  if (!modea_geometry(fn, num_q_heads, num_kv_heads, kv_groups, num_tiers, dh, G_max, cb_max, g_max, &rc))
+    return rc;
+  if (num_q_heads == 0) return ok();
+  if (!q_all || !cb_flat || !tier_G || !tier_g || !q_lut) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::ModeALaunch L{q_all, cb_flat, tier_G, tier_g, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, num_q_heads, num_kv_heads, kv_groups, num_tiers, 0, 16, dh, G_max,
+                       cb_max, g_max, 0, 1.f, 1, 1};
+  return launch_status(sphkv::launch_qlut(L, q_lut, (hipStream_t)stream), fn);
+}
+
+int sphkv_logits_lut(const float* q_lut, const uint8_t* theta_codes, const uint8_t* radius_codes,
+                     const float* r_scales, int64_t num_pages, const int32_t* block_table,
+                     const int32_t* bits_table, const int32_t* ctx_lens, float* logits_out,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t kv_groups, int32_t num_tiers,
+                     int32_t max_blocks, int32_t page_size, int32_t G_max, int32_t cb_size_max,
+                     float sm_scale, int32_t max_ctx, void* stream) {
+  const char* fn = "sphkv_logits_lut";
+  if (num_kv_heads < 0 || kv_groups < 1 || num_q_heads != num_kv_heads * kv_groups)
+    return fail(SPHKV_EINVAL, "%s: need num_q_heads == num_kv_heads * kv_groups", fn);
+  if (num_tiers < 1 || G_max < 1 || cb_size_max < 1 || cb_size_max > 256 || page_size < 1)
+    return fail(SPHKV_EINVAL, "%s: bad table geometry", fn);
+  if (max_blocks < 0 || max_ctx < 0 || num_pages < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (num_q_heads == 0 || max_ctx == 0) return ok();
+  if (!q_lut || !theta_codes || !radius_codes || !r_scales || !block_table || !bits_table || !ctx_lens ||
+      !logits_out)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::LutLogitsLaunch L{q_lut, theta_codes, radius_codes, r_scales, block_table, bits_table, ctx_lens,
+                           logits_out, num_q_heads, num_kv_heads, kv_groups, num_tiers, max_blocks, page_size,
+                           G_max, cb_size_max, max_ctx, num_pages, sm_scale};
+  return launch_status(sphkv::launch_lut_logits(L, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"

@@ -36,6 +36,39 @@ struct RaggedLaunch {
   float* logits_out;
 };
 
+// Mode-A (LayerPool) path
+constexpr int kModeAMaxTiers = 8;
+
+struct AppendLaunch {
+  const float* k_post; const float* v_new; const float* decode_cb;
+  uint8_t* theta_codes; uint8_t* radius_codes; float* r_scales; _Float16* v_pool;
+  const int64_t* pids; int64_t num_pages;
+  int32_t num_kv, slot, G, g, C, G_max, dh, page_size, is_new_page;
+};
+
+struct ModeALaunch {
+  const float* q; const float* cb_flat; const int32_t* tier_G; const int32_t* tier_g;
+  const uint8_t* theta_codes; const uint8_t* radius_codes; const float* r_scales; const _Float16* v_pool;
+  const int32_t* block_table; const int32_t* bits_table;
+  float* out; float* partial;
+  int32_t num_q, num_kv, kv_groups, num_tiers, max_blocks, page_size, dh, G_max, cb_max, g_max;
+  int64_t num_pages; float sm_scale;
+  int32_t nsplit, ppw;       // logical-page ranges: nsplit ranges of ppw pages, the last takes the rest
+};
+
+struct LutLogitsLaunch {
+  const float* q_lut; const uint8_t* theta_codes; const uint8_t* radius_codes; const float* r_scales;
+  const int32_t* block_table; const int32_t* bits_table; const int32_t* ctx_lens; float* logits_out;
+  int32_t num_q, num_kv, kv_groups, num_tiers, max_blocks, page_size, G_max, cb_size_max, max_ctx;
+  int64_t num_pages; float sm_scale;
+};
+
+int launch_append(const AppendLaunch& L, hipStream_t stream);
+int launch_modea(const ModeALaunch& L, hipStream_t stream);
+int launch_qlut(const ModeALaunch& L, float* lut, hipStream_t stream);
+int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream);
+int64_t modea_split_lds_bytes(int dh, int nhp, int num_tiers, int G_max, int cb_max, int page_size);
+
 int launch_encode(const EncodeLaunch& L, hipStream_t stream);
 // Decode phases: the split kernel writing one (m, l, acc) partial per work
 // item, and the log-sum-exp merge of each (sequence, kv head)'s partials.

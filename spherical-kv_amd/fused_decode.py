@@ -9,7 +9,9 @@ the reference's availability probe (`from fused_decode import fused_decode`,
 spherical_kv_pipeline.py:1053-1086) sees the failure.
 
 Every call launches on torch.cuda.current_stream() (the reference used the
-legacy default stream) and raises RuntimeError on a non-zero status.
+legacy default stream) and raises RuntimeError on a non-zero status.  Outputs
+the reference writes through (out, partial_scratch, the pools) must be
+contiguous tensors of the reference's dtype.
 """
 from __future__ import annotations
 
@@ -77,18 +79,94 @@ def fused_decode_ragged(pages, ptable, head_ids, positions, cos_tbl, sin_tbl, q,
     return out
 
 
+def _inplace(t: torch.Tensor, name: str, dtype) -> torch.Tensor:
+    """A tensor the kernel writes through: must already be a contiguous CUDA
+    tensor of the right dtype (a converted copy would drop the writes)."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA (HIP) tensor")
+    if t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor (written in place)")
+    return t
+
+
 def sphkv_decode(q_all, cb_flat, tier_G, tier_g, theta_codes, radius_codes, r_scales, v_pool,
                  block_table, bits_table, ctx_lens, out, partial_scratch,
                  num_q_heads, num_kv_heads, kv_groups, num_tiers, max_blocks, page_size, dh,
                  G_max, cb_max, g_max, sm_scale, max_ctx):
-    """Mode-A decode over LayerPool tables (fused_decode.py:12-26)."""
-    raise NotImplementedError("sphkv_decode (Mode-A LayerPool decode) is not built yet")
+    """Mode-A decode over LayerPool tables (fused_decode.py:12-26); writes and
+    returns `out` fp32 [num_q_heads, dh].
+
+    partial_scratch fp32 [num_q_heads, max_blocks, dh + 2] receives each (q
+    head, logical page)'s (m, l) in [..., 0:2] (read by the omega-EMA update,
+    spherical_kv_pipeline.py:1690-1701); its other entries are scratch.
+    ctx_lens and max_ctx are unused, as in the reference kernel.
+    """
+    q_all = _dev(q_all, "q_all", torch.float32)
+    cb_flat = _dev(cb_flat, "cb_flat", torch.float32)
+    tier_G = _dev(tier_G, "tier_G", torch.int32)
+    tier_g = _dev(tier_g, "tier_g", torch.int32)
+    theta_codes = _dev(theta_codes, "theta_codes", torch.uint8)
+    radius_codes = _dev(radius_codes, "radius_codes", torch.uint8)
+    r_scales = _dev(r_scales, "r_scales", torch.float32)
+    v_pool = _dev(v_pool, "v_pool", torch.float16)
+    block_table = _dev(block_table, "block_table", torch.int32)
+    bits_table = _dev(bits_table, "bits_table", torch.int32)
+    out = _inplace(out, "out", torch.float32)
+    partial_scratch = _inplace(partial_scratch, "partial_scratch", torch.float32)
+    nq, nkv, mb, ps = int(num_q_heads), int(num_kv_heads), int(max_blocks), int(page_size)
+    n_pages = int(theta_codes.shape[0])
+    if tuple(theta_codes.shape) != (n_pages, ps, int(G_max)) or theta_codes.shape != radius_codes.shape:
+        raise ValueError("theta_codes / radius_codes must be [n_pages, page_size, G_max]")
+    if tuple(r_scales.shape) != (n_pages, int(G_max)) or tuple(v_pool.shape) != (n_pages, ps, int(dh)):
+        raise ValueError("r_scales must be [n_pages, G_max] and v_pool [n_pages, page_size, dh]")
+    if block_table.numel() != nkv * mb or bits_table.numel() != nkv * mb:
+        raise ValueError("block_table / bits_table must be [num_kv_heads, max_blocks]")
+    if cb_flat.numel() != nkv * int(num_tiers) * int(G_max) * int(cb_max) * int(g_max):
+        raise ValueError("cb_flat must be [num_kv, num_tiers, G_max, cb_max, g_max]")
+    if tier_G.numel() < int(num_tiers) or tier_g.numel() < int(num_tiers):
+        raise ValueError("tier_G / tier_g need num_tiers entries")
+    if q_all.numel() != nq * int(dh) or out.numel() != nq * int(dh):
+        raise ValueError("q_all and out must be [num_q_heads, dh]")
+    if partial_scratch.numel() < nq * mb * (int(dh) + 2):
+        raise ValueError("partial_scratch must be [num_q_heads, max_blocks, dh + 2]")
+    rc = _lib.sphkv_decode_modea(
+        q_all.data_ptr(), cb_flat.data_ptr(), tier_G.data_ptr(), tier_g.data_ptr(), theta_codes.data_ptr(),
+        radius_codes.data_ptr(), r_scales.data_ptr(), v_pool.data_ptr(), n_pages, block_table.data_ptr(),
+        bits_table.data_ptr(), 0, out.data_ptr(), partial_scratch.data_ptr(), nq, nkv, int(kv_groups),
+        int(num_tiers), mb, ps, int(dh), int(G_max), int(cb_max), int(g_max), float(sm_scale),
+        int(max_ctx), _stream())
+    check(rc, "sphkv_decode")
+    return out
 
 
 def sphkv_encode_append(k_post, v_new, decode_cb, theta_codes, radius_codes, r_scales, v_pool,
                         pids, slot, G, g, C, G_max, dh, page_size, is_new_page):
-    """Decode-time single-token encode + append (fused_decode.py:28-35)."""
-    raise NotImplementedError("sphkv_encode_append is not built yet")
+    """Decode-time single-token encode + append (fused_decode.py:28-35): writes
+    slot `slot` of pool page pids[h] for every kv head h, in place."""
+    k_post = _dev(k_post, "k_post", torch.float32)
+    v_new = _dev(v_new, "v_new", torch.float32)
+    decode_cb = _dev(decode_cb, "decode_cb", torch.float32)
+    pids = _dev(pids, "pids", torch.int64)
+    theta_codes = _inplace(theta_codes, "theta_codes", torch.uint8)
+    radius_codes = _inplace(radius_codes, "radius_codes", torch.uint8)
+    r_scales = _inplace(r_scales, "r_scales", torch.float32)
+    v_pool = _inplace(v_pool, "v_pool", torch.float16)
+    num_kv = int(k_post.shape[0])
+    n_pages = int(theta_codes.shape[0])
+    if k_post.numel() != num_kv * int(dh) or v_new.numel() != num_kv * int(dh) or pids.numel() != num_kv:
+        raise ValueError("k_post / v_new must be [num_kv, dh] and pids [num_kv]")
+    if decode_cb.numel() != num_kv * int(G) * int(C) * int(g):
+        raise ValueError("decode_cb must be [num_kv, G, C, g]")
+    if theta_codes.numel() != n_pages * int(page_size) * int(G_max) or radius_codes.shape != theta_codes.shape:
+        raise ValueError("theta_codes / radius_codes must be [n_pages, page_size, G_max]")
+    if r_scales.numel() != n_pages * int(G_max) or v_pool.numel() != n_pages * int(page_size) * int(dh):
+        raise ValueError("r_scales must be [n_pages, G_max] and v_pool [n_pages, page_size, dh]")
+    rc = _lib.sphkv_encode_append(
+        k_post.data_ptr(), v_new.data_ptr(), decode_cb.data_ptr(), theta_codes.data_ptr(),
+        radius_codes.data_ptr(), r_scales.data_ptr(), v_pool.data_ptr(), pids.data_ptr(), num_kv, n_pages,
+        int(slot), int(G), int(g), int(C), int(G_max), int(dh), int(page_size), 1 if is_new_page else 0,
+        _stream())
+    check(rc, "sphkv_encode_append")
 
 
 # Backwards-compatible aliases (fused_decode.py:37-41)

@@ -34,6 +34,13 @@ SIGNATURES = {
     "sphkv_decode_merge_partials": (ctypes.c_int, [P, I64, I32, P, I32, I32, I32, I32, P, P]),
     "sphkv_fused_decode_ragged": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
                                                  I32, I32, I32, I32, I32, P, P]),
+    "sphkv_encode_append": (ctypes.c_int, [P, P, P, P, P, P, P, P, I32, I64, I32, I32, I32, I32, I32,
+                                           I32, I32, I32, P]),
+    "sphkv_decode_modea": (ctypes.c_int, [P, P, P, P, P, P, P, P, I64, P, P, P, P, P, I32, I32, I32, I32,
+                                          I32, I32, I32, I32, I32, I32, F32, I32, P]),
+    "sphkv_q_lut": (ctypes.c_int, [P, P, P, P, I32, I32, I32, I32, I32, I32, I32, I32, P, P]),
+    "sphkv_logits_lut": (ctypes.c_int, [P, P, P, P, I64, P, P, P, P, I32, I32, I32, I32, I32, I32, I32,
+                                        I32, F32, I32, P]),
 }
 
 

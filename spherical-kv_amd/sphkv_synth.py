@@ -158,3 +158,61 @@ def make_encode_workload(seed: int = 3, tokens: int = 8192, num_kv: int = 8, dh:
     plan = fmt.plan_pages(tier_of, None, 1, num_kv, dh, 16, rng=None)
     return Workload(name="config3", dh=dh, num_kv=num_kv, gqa=1, num_seqs=1, lengths=[tokens],
                     rope_theta=500000.0, codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan)
+
+
+# Mode-A tier geometry (tiers.py:35-41): tier id -> (g, b); G = dh / g, C = 2^b.
+MODEA_TIERS = {1: (16, 6), 2: (16, 4), 3: (32, 3)}
+
+
+def make_modea_workload(seed: int = 11, num_kv: int = 8, kv_groups: int = 4, dh: int = 128,
+                        page_size: int = 16, ctx: int = 4096, tiers=(1, 2), fracs=None,
+                        holes: float = 0.0, spare_pages: int = 0) -> Dict[str, object]:
+    """LayerPool-shaped Mode-A tables (sphkv_lut.py:71-127) from a seeded draw.
+
+    Every kv head holds ctx tokens in ceil(ctx / page_size) logical pages placed
+    at random pool pages; each logical page has one tier (drawn with weights `fracs`, equal if None),
+    uniform theta codes below that tier's C, uniform uint8 radius codes,
+    lognormal radius scales; slots past ctx stay zero (codes 0, radius 0), the
+    state sphkv_encode_append leaves them in.  `holes` is the fraction of
+    logical pages marked absent (-1).  cb_flat rows are normalize(N(0,1)),
+    zero padded to [G_max, cb_max, g_max]; V ~ N(0,1) fp16; q ~ N(0,1) fp32.
+    """
+    rng = np.random.default_rng(seed)
+    T = len(tiers)
+    fracs = np.ones(T) if fracs is None else np.asarray(fracs, np.float64)
+    geo = [(dh // MODEA_TIERS[t][0], MODEA_TIERS[t][0], 1 << MODEA_TIERS[t][1]) for t in tiers]   # (G, g, C)
+    G_max = max(G for G, _, _ in geo)
+    g_max = max(g for _, g, _ in geo)
+    cb_max = max(C for _, _, C in geo)
+    cb_flat = np.zeros((num_kv, T, G_max, cb_max, g_max), np.float32)
+    for h in range(num_kv):
+        for ti, (G, g, C) in enumerate(geo):
+            x = rng.standard_normal((G, C, g))
+            cb_flat[h, ti, :G, :C, :g] = (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
+    nlog = -(-ctx // page_size)
+    n_pages = num_kv * nlog + spare_pages
+    perm = rng.permutation(n_pages)[:num_kv * nlog].reshape(num_kv, nlog).astype(np.int32)
+    tier_idx = rng.choice(T, size=(num_kv, nlog), p=fracs / fracs.sum()).astype(np.int32)
+    if holes > 0:
+        perm = np.where(rng.random((num_kv, nlog)) < holes, -1, perm).astype(np.int32)
+    theta = np.zeros((n_pages, page_size, G_max), np.uint8)
+    radius = np.zeros((n_pages, page_size, G_max), np.uint8)
+    r_scales = np.zeros((n_pages, G_max), np.float32)
+    v_pool = rng.standard_normal((n_pages, page_size, dh)).astype(np.float16)
+    for h in range(num_kv):
+        for lb in range(nlog):
+            ph = int(perm[h, lb])
+            if ph < 0:
+                continue
+            G, g, C = geo[int(tier_idx[h, lb])]
+            n = min(page_size, ctx - lb * page_size)
+            theta[ph, :n, :G] = rng.integers(0, C, size=(n, G))
+            radius[ph, :n, :G] = rng.integers(1, 256, size=(n, G))
+            r_scales[ph, :G] = np.exp(rng.normal(1.0, 0.3, size=G)).astype(np.float32)
+    q = rng.standard_normal((num_kv * kv_groups, dh)).astype(np.float32)
+    return dict(q=q, cb_flat=cb_flat, tier_G=np.array([G for G, _, _ in geo], np.int32),
+                tier_g=np.array([g for _, g, _ in geo], np.int32), theta=theta, radius=radius,
+                r_scales=r_scales, v_pool=v_pool, block_table=perm, bits_table=tier_idx,
+                ctx_lens=np.full(num_kv, ctx, np.int32), num_kv=num_kv, kv_groups=kv_groups, dh=dh,
+                page_size=page_size, num_tiers=T, G_max=G_max, cb_max=cb_max, g_max=g_max, max_blocks=nlog,
+                sm_scale=float(1.0 / np.sqrt(dh)), max_ctx=ctx, tiers=tuple(tiers))

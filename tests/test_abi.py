@@ -122,3 +122,63 @@ def test_ragged_argument_errors():
     args[16] = 9                                   # b_theta
     assert lib.sphkv_fused_decode_ragged(*args) == -1
     assert "b_theta" in lib.sphkv_last_error().decode()
+
+
+def _modea_args(**kw):
+    a = dict(q=None, cb=None, tG=None, tg=None, th=None, rd=None, rs=None, vp=None, num_pages=0, bt=None,
+             bits=None, ctx=None, out=None, part=None, num_q=32, num_kv=8, kv_groups=4, num_tiers=2,
+             max_blocks=64, page_size=16, dh=128, G_max=8, cb_max=64, g_max=16, sm_scale=0.088, max_ctx=1024,
+             stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dh=96), "dh must be 64 or 128"),
+    (dict(num_q=30), "num_q_heads == num_kv_heads * kv_groups"),
+    (dict(kv_groups=16, num_q=128), "kv_groups 1..8"),
+    (dict(num_tiers=9), "num_tiers must be"),
+    (dict(cb_max=512), "bad table geometry"),
+    (dict(page_size=24), "page_size must be a multiple of 16"),
+    (dict(num_tiers=8, G_max=64, cb_max=256), "LDS"),
+    (dict(), "null pointer"),
+])
+def test_modea_decode_argument_errors(kw, msg):
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_modea(*_modea_args(**kw)) == -1
+    assert msg in lib.sphkv_last_error().decode()
+
+
+def test_modea_decode_empty_is_a_no_op():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_modea(*_modea_args(max_blocks=0)) == 0
+    assert lib.sphkv_decode_modea(*_modea_args(num_kv=0, num_q=0)) == 0
+
+
+def test_encode_append_argument_errors():
+    lib = sphkv_lib.load()
+    base = [None] * 8 + [8, 100, 0, 8, 16, 64, 8, 128, 16, 1, None]
+    for idx, val, msg in [(15, 300, "dh must be"), (11, 9, "G <= G_max"), (12, 17, "G * g <= dh"),
+                          (13, 512, "C <= 256"), (10, 16, "slot must be"), (10, -1, "slot must be"),
+                          (9, -5, "negative size"), (10, 0, "null pointer")]:
+        args = list(base)
+        args[idx] = val
+        assert lib.sphkv_encode_append(*args) == -1, msg
+        assert msg in lib.sphkv_last_error().decode()
+    args = list(base)
+    args[8] = 0                                    # no kv heads: nothing to do
+    assert lib.sphkv_encode_append(*args) == 0
+
+
+def test_q_lut_and_logits_argument_errors():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_q_lut(None, None, None, None, 32, 8, 4, 2, 128, 8, 64, 16, None, None) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_q_lut(None, None, None, None, 33, 8, 4, 2, 128, 8, 64, 16, None, None) == -1
+    assert "kv_groups" in lib.sphkv_last_error().decode()
+    lg = [None, None, None, None, 10, None, None, None, None, 32, 8, 4, 2, 64, 16, 8, 64, 0.1, 1024, None]
+    assert lib.sphkv_logits_lut(*lg) == -1 and "null pointer" in lib.sphkv_last_error().decode()
+    lg[16] = 300
+    assert lib.sphkv_logits_lut(*lg) == -1 and "bad table geometry" in lib.sphkv_last_error().decode()
+    lg[16], lg[18] = 64, 0
+    assert lib.sphkv_logits_lut(*lg) == 0

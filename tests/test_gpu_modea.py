@@ -1,0 +1,141 @@
+"""GPU parity of the Mode-A (LayerPool) path through the reference-named
+Python entry points (fused_decode.sphkv_decode / sphkv_encode_append,
+new_fused_decode.sphkv_logits / build_q_lut) and the C ABI behind them.
+
+Bars: encode_append bit-exact with the oracle's restatement of
+decode_kernel.cu:10-84 (codes, radius codes, radius scales, fp16 V) over a
+sequence of appends that opens pages and rescales earlier radius codes;
+decode output within max-abs 2e-3 of the fp64 oracle, per-page (m, l) within
+1e-4 abs / 1e-4 relative; LUT and logits within 1e-4 (fp32 sums of at most
+G_max terms), -inf exactly where the oracle has it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import fused_decode
+import new_fused_decode
+import oracle
+import sphkv_synth as synth
+from gpu_helpers import log, max_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("page_size", [16, 128])
+def test_encode_append_bitexact_over_a_sequence(gpu, page_size):
+    rng = np.random.default_rng(21 + page_size)
+    num_kv, dh, G, g, C, G_max = 8, 128, 8, 16, 64, 8
+    x = rng.standard_normal((num_kv, G, C, g))
+    cb = (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
+    n_pages = 3 * num_kv
+    th = np.zeros((n_pages, page_size, G_max), np.uint8)
+    rd = np.zeros_like(th)
+    rs = np.zeros((n_pages, G_max), np.float32)
+    vp = np.zeros((n_pages, page_size, dh), np.float16)
+    d_th, d_rd, d_rs, d_vp, d_cb = _t(th, gpu), _t(rd, gpu), _t(rs, gpu), _t(vp, gpu), _t(cb, gpu)
+    steps = page_size + 5                               # opens a second page per head
+    scale = np.exp(rng.normal(0, 0.7, size=(steps, num_kv, dh)))
+    for step in range(steps):
+        slot = step % page_size
+        pg = step // page_size
+        pids = np.arange(num_kv, dtype=np.int64) + pg * num_kv
+        k = (rng.standard_normal((num_kv, dh)) * scale[step]).astype(np.float32)
+        v = rng.standard_normal((num_kv, dh)).astype(np.float32)
+        oracle.encode_append(k, v, cb, th, rd, rs, vp, pids, slot, slot == 0)
+        fused_decode.sphkv_encode_append(_t(k, gpu), _t(v, gpu), d_cb, d_th, d_rd, d_rs, d_vp, _t(pids, gpu),
+                                         slot, G, g, C, G_max, dh, page_size, slot == 0)
+    torch.cuda.synchronize()
+    log(f"append page_size={page_size} steps={steps}")
+    assert (d_th.cpu().numpy() == th).all()
+    assert (d_rd.cpu().numpy() == rd).all()
+    assert (d_rs.cpu().numpy().view(np.uint32) == rs.view(np.uint32)).all()
+    assert (d_vp.cpu().numpy().view(np.uint16) == vp.view(np.uint16)).all()
+
+
+CASES = [
+    dict(dh=128, kv_groups=4, page_size=16, ctx=2000, tiers=(1, 2), holes=0.0),
+    dict(dh=128, kv_groups=4, page_size=128, ctx=3001, tiers=(1, 2, 3), holes=0.1),
+    dict(dh=64, kv_groups=8, page_size=32, ctx=777, tiers=(1, 3), holes=0.05),
+    dict(dh=128, kv_groups=1, page_size=16, ctx=17, tiers=(2,), holes=0.0),
+    dict(dh=64, kv_groups=2, page_size=64, ctx=5000, tiers=(1, 2), holes=0.3),
+]
+
+
+def _modea_call(w, gpu):
+    dev = {k: _t(w[k], gpu) for k in ("q", "cb_flat", "tier_G", "tier_g", "theta", "radius", "r_scales",
+                                       "v_pool", "block_table", "bits_table", "ctx_lens")}
+    nq = w["q"].shape[0]
+    out = torch.empty((nq, w["dh"]), dtype=torch.float32, device=gpu)
+    part = torch.zeros((nq, w["max_blocks"], w["dh"] + 2), dtype=torch.float32, device=gpu)
+    r = fused_decode.sphkv_decode(dev["q"], dev["cb_flat"], dev["tier_G"], dev["tier_g"], dev["theta"],
+                                  dev["radius"], dev["r_scales"], dev["v_pool"], dev["block_table"],
+                                  dev["bits_table"], dev["ctx_lens"], out, part, nq, w["num_kv"], w["kv_groups"],
+                                  w["num_tiers"], w["max_blocks"], w["page_size"], w["dh"], w["G_max"],
+                                  w["cb_max"], w["g_max"], w["sm_scale"], w["max_ctx"])
+    assert r is out
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), part.cpu().numpy(), dev
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"dh{c['dh']}-g{c['kv_groups']}-p{c['page_size']}" for c in CASES])
+def test_decode_modea_matches_oracle(gpu, case):
+    w = synth.make_modea_workload(seed=31, num_kv=4, **case)
+    log(f"modea {case} max_blocks={w['max_blocks']}")
+    got, part, _ = _modea_call(w, gpu)
+    want, M, L = oracle.decode_mode_a(w["q"], w["cb_flat"], w["tier_G"], w["tier_g"], w["theta"], w["radius"],
+                                      w["r_scales"], w["v_pool"], w["block_table"], w["bits_table"],
+                                      w["kv_groups"], w["sm_scale"])
+    err = max_err(got, want)
+    log(f"  out max abs err {err:.3e}")
+    assert err <= TOL
+    gm, gl = part[:, :, 0], part[:, :, 1]
+    absent = np.isinf(M)
+    assert (np.isinf(gm) == absent).all() and (gl[absent] == 0).all()
+    np.testing.assert_allclose(gm[~absent], M[~absent], atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(gl[~absent], L[~absent], rtol=1e-4)
+
+
+def test_lut_and_logits_match_oracle(gpu):
+    w = synth.make_modea_workload(seed=41, num_kv=4, kv_groups=4, dh=128, page_size=16, ctx=1000,
+                                  tiers=(1, 2, 3), fracs=(1, 1, 1), holes=0.1)
+    dev = {k: _t(w[k], gpu) for k in ("q", "cb_flat", "tier_G", "tier_g", "theta", "radius", "r_scales",
+                                       "block_table", "bits_table")}
+    lut = new_fused_decode.build_q_lut(dev["q"], dev["cb_flat"], dev["tier_G"], dev["tier_g"], w["num_kv"],
+                                       w["kv_groups"], w["num_tiers"], w["G_max"], w["cb_max"], w["g_max"])
+    want_lut = oracle.q_lut(w["q"], w["cb_flat"], w["tier_G"], w["tier_g"], w["kv_groups"])
+    assert max_err(lut.cpu().numpy(), want_lut) <= 1e-4
+    ctx = np.array([1000, 999, 600, 1], np.int32)
+    max_ctx = 1024
+    nq = w["q"].shape[0]
+    logits = torch.empty((nq, max_ctx), dtype=torch.float32, device=gpu)
+    r = new_fused_decode.sphkv_logits(lut, dev["theta"], dev["radius"], dev["r_scales"], dev["block_table"],
+                                      dev["bits_table"], _t(ctx, gpu), logits, nq, w["num_kv"], w["kv_groups"],
+                                      w["num_tiers"], w["max_blocks"], w["page_size"], w["G_max"], w["cb_max"],
+                                      w["sm_scale"], max_ctx)
+    assert r is logits
+    got = logits.cpu().numpy()
+    want = oracle.lut_logits(want_lut, w["theta"], w["radius"], w["r_scales"], w["block_table"],
+                             w["bits_table"], ctx, w["kv_groups"], w["sm_scale"], max_ctx)
+    inf = np.isinf(want)
+    assert (np.isinf(got) == inf).all()
+    err = max_err(got[~inf], want[~inf])
+    log(f"lut logits max abs err {err:.3e}")
+    assert err <= 1e-4
+
+
+def test_modea_single_range_and_empty_tables(gpu):
+    """max_blocks 1 (one range writes out directly) and a head whose pages are all absent."""
+    w = synth.make_modea_workload(seed=5, num_kv=2, kv_groups=4, dh=128, page_size=16, ctx=9, tiers=(1,), fracs=(1,))
+    w["block_table"] = w["block_table"].copy()
+    w["block_table"][1, :] = -1
+    got, part, _ = _modea_call(w, gpu)
+    want, M, L = oracle.decode_mode_a(w["q"], w["cb_flat"], w["tier_G"], w["tier_g"], w["theta"], w["radius"],
+                                      w["r_scales"], w["v_pool"], w["block_table"], w["bits_table"], 4, w["sm_scale"])
+    assert max_err(got, want) <= TOL
+    assert (got[4:] == 0).all()                       # acc 0 / (0 + 1e-8)
