@@ -11,6 +11,10 @@ copies of the KV pool (each ~80 MB).  Timing uses HIP events on the stream the
 kernels run on (torch's current stream), around exactly K steps.
 
 Prints one JSON line (see the "roofline" and "cpu_baseline" objects).
+
+`--path modea` measures the Mode-A (LayerPool) decode instead, on the same
+attention shape with unpacked uint8 pools (fused_decode.sphkv_decode); the
+default line is the angle-domain (Mode-B) decode above.
 """
 from __future__ import annotations
 
@@ -95,6 +99,98 @@ def cpu_baseline(wl, pool: ops.PagedPool, budget_s: float = 20.0):
                       f"restatement of spherical_kv_pipeline.py:2143-2177,2348,2367"}
 
 
+def modea_bytes(w) -> int:
+    """Algorithmic HBM bytes of one Mode-A decode: per present logical page
+    its theta and radius codes (page_size x G_tier bytes each), r_scales
+    (G_tier fp32), fp16 V (page_size x dh) and its two table entries, plus the
+    per-(q head, page) (m, l) written to partial_scratch."""
+    total = 0
+    ps, dh = w["page_size"], w["dh"]
+    for h in range(w["num_kv"]):
+        for p in range(w["max_blocks"]):
+            if w["block_table"][h, p] < 0:
+                continue
+            Gt = int(w["tier_G"][w["bits_table"][h, p]])
+            total += 2 * ps * Gt + 4 * Gt + 2 * ps * dh + 8
+    return total + w["q"].shape[0] * w["max_blocks"] * 8
+
+
+def cpu_baseline_modea(w, budget_s: float = 20.0):
+    """The fp64 numpy restatement of decode_kernel.cu:108-246, one kv head at a
+    time on one host core, as many heads as fit the budget."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    kvg = w["kv_groups"]
+    times, done = [], 0
+    t_start = time.perf_counter()
+    for h in range(w["num_kv"]):
+        t0 = time.perf_counter()
+        oracle.decode_mode_a(w["q"][h * kvg:(h + 1) * kvg], w["cb_flat"][h:h + 1], w["tier_G"], w["tier_g"],
+                             w["theta"], w["radius"], w["r_scales"], w["v_pool"], w["block_table"][h:h + 1],
+                             w["bits_table"][h:h + 1], kvg, w["sm_scale"])
+        times.append(time.perf_counter() - t0)
+        done += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    step_us = float(np.median(times)) * w["num_kv"] * 1e6
+    return {"value": round(step_us, 1), "unit": "µs/decode step (extrapolated from per-head time)", "cores": 1,
+            "kind": "port", "sample": f"{done} of {w['num_kv']} kv heads, median per-head time x {w['num_kv']}; "
+                                      f"numpy fp64 restatement of decode_kernel.cu:108-246"}
+
+
+def bench_modea(args, dev):
+    import fused_decode
+    log(f"[bench] building Mode-A workload (page_size {args.page_size})")
+    w = synth.make_modea_workload(seed=2, num_kv=8, kv_groups=4, dh=128, page_size=args.page_size, ctx=32768,
+                                  tiers=(1, 2), fracs=(0.6, 0.4))
+    names = ("q", "cb_flat", "tier_G", "tier_g", "theta", "radius", "r_scales", "v_pool", "block_table",
+             "bits_table", "ctx_lens")
+    d = {k: torch.from_numpy(np.ascontiguousarray(w[k])).to(dev) for k in names}
+    pools = [(d["theta"], d["radius"], d["r_scales"], d["v_pool"])]
+    for _ in range(args.rotate - 1):
+        pools.append(tuple(t.clone() for t in pools[0]))
+    nq, mb = w["q"].shape[0], w["max_blocks"]
+    out = torch.empty((nq, w["dh"]), dtype=torch.float32, device=dev)
+    part = torch.zeros((nq, mb, w["dh"] + 2), dtype=torch.float32, device=dev)
+    nbytes = modea_bytes(w)
+
+    def step(i):
+        th, rd, rs, vp = pools[i % len(pools)]
+        fused_decode.sphkv_decode(d["q"], d["cb_flat"], d["tier_G"], d["tier_g"], th, rd, rs, vp,
+                                  d["block_table"], d["bits_table"], d["ctx_lens"], out, part, nq, w["num_kv"],
+                                  w["kv_groups"], w["num_tiers"], mb, w["page_size"], w["dh"], w["G_max"],
+                                  w["cb_max"], w["g_max"], w["sm_scale"], w["max_ctx"])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] Mode-A {ms * 1e3:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+    cpu = None if args.no_cpu_baseline else cpu_baseline_modea(w)
+    line = {
+        "metric": "µs/decode step + achieved HBM GB/s (Mode-A LayerPool decode), 8B shape, 32K ctx, 1 GPU",
+        "value": round(ms * 1e3, 3), "unit": "µs/decode step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8 codes, fp16 V, fp32 math",
+        "data": "synthetic (sphkv_synth.make_modea_workload seed 2)", "achieved_hbm_gbps": round(gbps, 1),
+        "config": {"workload": f"Mode A: 32 q / 8 kv heads, dh 128, 32768 ctx, {w['page_size']}-token pages, "
+                               f"60/40 tier 1/2, random page placement", "pages": int(w["num_kv"] * mb),
+                   "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "modea_split_kernel + modea_merge_kernel", "kernel_us": round(ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,6 +201,9 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
                     help="page placement: the config's own (random for configs 2-5) or sequential")
+    ap.add_argument("--path", default="modeb", choices=["modeb", "modea"],
+                    help="modeb: the angle-domain paged decode (the headline); modea: LayerPool decode")
+    ap.add_argument("--page-size", type=int, default=16, help="Mode-A page size (16..128, multiple of 16)")
     ap.add_argument("--calibrate", action="store_true",
                     help="after timing, run plain device copies of COPY_BYTES (torch copy_), the "
                          "reference kernel of known traffic for FETCH_SIZE / WRITE_SIZE counters")
@@ -119,6 +218,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.path == "modea":
+        bench_modea(args, dev)
+        return
 
     log(f"[bench] building config{args.config} workload")
     wl = synth.make_decode_workload(args.config, layout=args.layout)

@@ -241,23 +241,17 @@ int sphkv_decode_modea(const float* q_all, const float* cb_flat, const int32_t* 
   if (page_size < 16 || page_size > 128 || page_size % 16 != 0)
     return fail(SPHKV_EINVAL, "%s: page_size must be a multiple of 16 in 16..128 (got %d)", fn, page_size);
   if (max_blocks < 0 || num_pages < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
-  const int nhp = kv_groups <= 4 ? 1 : 2;
-  const int64_t lds = sphkv::modea_split_lds_bytes(dh, nhp, num_tiers, G_max, cb_max, page_size);
+  sphkv::ModeALaunch L{q_all, cb_flat, tier_G, tier_g, theta_codes, radius_codes, r_scales,
+                       reinterpret_cast<const _Float16*>(v_pool), block_table, bits_table, out, partial_scratch,
+                       num_q_heads, num_kv_heads, kv_groups, num_tiers, max_blocks, page_size, dh, G_max,
+                       cb_max, g_max, num_pages, sm_scale, 1, 0};
+  const int64_t lds = sphkv::modea_configure(L);
   if (lds > 160 * 1024)
     return fail(SPHKV_EINVAL, "%s: per-query tables need %lld bytes of LDS (> 160 KiB)", fn, (long long)lds);
   if (num_kv_heads == 0 || max_blocks == 0) return ok();
   if (!q_all || !cb_flat || !tier_G || !tier_g || !theta_codes || !radius_codes || !r_scales || !v_pool ||
       !block_table || !bits_table || !out || !partial_scratch)
     return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
-  // ranges of logical pages: about two workgroups per CU, each range >= 2 pages
-  int nsplit = (512 + num_kv_heads - 1) / num_kv_heads;
-  if (nsplit > max_blocks / 2) nsplit = max_blocks / 2;
-  if (nsplit < 1) nsplit = 1;
-  const int ppw = max_blocks / nsplit;
-  sphkv::ModeALaunch L{q_all, cb_flat, tier_G, tier_g, theta_codes, radius_codes, r_scales,
-                       reinterpret_cast<const _Float16*>(v_pool), block_table, bits_table, out, partial_scratch,
-                       num_q_heads, num_kv_heads, kv_groups, num_tiers, max_blocks, page_size, dh, G_max,
-                       cb_max, g_max, num_pages, sm_scale, nsplit, ppw};
   return launch_status(sphkv::launch_modea(L, (hipStream_t)stream), fn);
 }
 
@@ -272,7 +266,7 @@ int sphkv_q_lut(const float* q_all, const float* cb_flat, const int32_t* tier_G,
   if (!q_all || !cb_flat || !tier_G || !tier_g || !q_lut) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
   sphkv::ModeALaunch L{q_all, cb_flat, tier_G, tier_g, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                        nullptr, nullptr, num_q_heads, num_kv_heads, kv_groups, num_tiers, 0, 16, dh, G_max,
-                       cb_max, g_max, 0, 1.f, 1, 1};
+                       cb_max, g_max, 0, 1.f, 1, 0};
   return launch_status(sphkv::launch_qlut(L, q_lut, (hipStream_t)stream), fn);
 }
 

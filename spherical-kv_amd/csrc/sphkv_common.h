@@ -31,6 +31,20 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Every per-page load is a buffer load against a resource that covers exactly
+// the bytes that page may need; a resource of 0 bytes makes the load return
+// zeros without touching memory.  So each loop iteration issues the same
+// loads in the same order whatever the page holds, and the vmcnt waits the
+// compiler derives are exact (a branch around a load makes them conservative,
+// down to waiting for every prefetch in flight).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kOOB = 0x7FFFFF00;       // offset beyond any resource
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const uint32_t n = bytes <= 0 ? 0u : (bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // xor-shuffle within a wave (ds_bpermute / DPP chosen by the compiler).

@@ -66,20 +66,6 @@ struct DecodeArgs {
 
 constexpr float kRescaleLog2 = 8.0f;   // reference-max hysteresis (log2 units)
 
-// Every per-page load is a buffer load against a resource that covers exactly
-// the bytes that page may need; a resource of 0 bytes makes the load return
-// zeros without touching memory.  So each loop iteration issues the same
-// loads in the same order whatever the page holds, and the vmcnt waits the
-// compiler derives are exact (a branch around a load makes them conservative,
-// down to waiting for every prefetch in flight).
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kOOB = 0x7FFFFF00;       // offset beyond any resource
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const uint32_t n = bytes <= 0 ? 0u : (bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
-}
-
 // Buffer resources of the kernel-wide arrays, built once per wave (scalar
 // registers).  Loads of absent data use an offset beyond every resource
 // (kOOB) and return zeros.  The byte pool, pointer table and positions are

@@ -53,7 +53,10 @@ struct ModeALaunch {
   float* out; float* partial;
   int32_t num_q, num_kv, kv_groups, num_tiers, max_blocks, page_size, dh, G_max, cb_max, g_max;
   int64_t num_pages; float sm_scale;
-  int32_t nsplit, ppw;       // logical-page ranges: nsplit ranges of ppw pages, the last takes the rest
+  // set by modea_configure: nsplit ranges of logical pages per kv head (range s
+  // = [s * max_blocks / nsplit, (s + 1) * max_blocks / nsplit)); fast = 1 selects
+  // the vector-load kernel (G_max 4 or 8), 0 the general one
+  int32_t nsplit, fast;
 };
 
 struct LutLogitsLaunch {
@@ -67,7 +70,9 @@ int launch_append(const AppendLaunch& L, hipStream_t stream);
 int launch_modea(const ModeALaunch& L, hipStream_t stream);
 int launch_qlut(const ModeALaunch& L, float* lut, hipStream_t stream);
 int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream);
-int64_t modea_split_lds_bytes(int dh, int nhp, int num_tiers, int G_max, int cb_max, int page_size);
+// Chooses the kernel and the page split for a launch; returns the dynamic
+// LDS bytes the chosen split kernel needs (callers reject > 160 KiB).
+int64_t modea_configure(ModeALaunch& L);
 
 int launch_encode(const EncodeLaunch& L, hipStream_t stream);
 // Decode phases: the split kernel writing one (m, l, acc) partial per work

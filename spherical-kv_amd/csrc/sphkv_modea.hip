@@ -25,6 +25,8 @@
 //                      partial_scratch[..., 0:2] (read by the omega-EMA update,
 //                      spherical_kv_pipeline.py:1690-1701); per range one
 //                      online-softmax partial (m, l, acc[dh]).
+//   modea_fast_kernel  the same for G_max 4 or 8 with vector loads and a
+//                      two-deep tile prefetch ring (the common case).
 //   modea_merge_kernel log-sum-exp merge of the ranges (decode_kernel.cu:223-246):
 //                      out = acc / (l + 1e-8).
 //   qlut_kernel        the per-query LUT [num_q, num_tiers, G_max, cb_max].
@@ -186,6 +188,13 @@ __device__ __forceinline__ float rsum16(float x) {
 // hardware exp2.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
+// First logical page of range s of a kv head's block table (ranges split the
+// table as evenly as integers allow; every range holds >= 2 pages when
+// nsplit > 1, so a range's partial fits in the free part of two page entries).
+__device__ __forceinline__ int range_begin(const ModeALaunch& a, int s) {
+  return (int)((int64_t)s * a.max_blocks / a.nsplit);
+}
+
 template <int DH, int NHP>
 __global__ __launch_bounds__(256) void modea_split_kernel(ModeALaunch a) {
   constexpr int NH = 4 * NHP;              // q-head rows (padded)
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(256) void modea_split_kernel(ModeALaunch a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int hkv = blockIdx.x / a.nsplit, s = blockIdx.x % a.nsplit;
-  const int pb = s * a.ppw, pe = (s == a.nsplit - 1) ? a.max_blocks : pb + a.ppw;
+  const int pb = range_begin(a, s), pe = range_begin(a, s + 1);
   const int P = a.page_size, NT = P / 16;
   const int lut_n = NH * a.num_tiers * a.G_max * a.cb_max;
   float* lut = reinterpret_cast<float*>(smem);                           // [NH][tier][G_max][cb_max]
@@ -384,50 +393,502 @@ __global__ __launch_bounds__(256) void modea_split_kernel(ModeALaunch a) {
   }
 }
 
-// One workgroup per q head: log-sum-exp over the ranges' partials.
-__global__ __launch_bounds__(128) void modea_merge_kernel(ModeALaunch a) {
-  const int hq = blockIdx.x;
-  const int d = threadIdx.x;
-  if (d >= a.dh) return;
-  float Mx = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s)
-    Mx = fmaxf(Mx, a.partial[((int64_t)hq * a.max_blocks + s * a.ppw + 1) * (a.dh + 2) + 2]);
-  float Ls = 0.f, A = 0.f;
-  if (Mx != -INFINITY)
-    for (int s = 0; s < a.nsplit; ++s) {
-      const float* e0 = a.partial + ((int64_t)hq * a.max_blocks + s * a.ppw) * (a.dh + 2);
-      const float* e1 = e0 + (a.dh + 2);
-      if (e1[2] == -INFINITY) continue;
-      const float f = fast_exp(e1[2] - Mx);
-      Ls += f * e1[3];
-      A += f * e0[2 + d];
+// Log-sum-exp merge of the ranges' partials (decode_kernel.cu:223-246):
+// workgroup = (q head, 64-dim chunk); wave w folds ranges w, w + 8, ... into a
+// running (m, l, acc) with four ranges' loads in flight at a time, then wave 0
+// folds the eight waves and writes out = acc / (l + 1e-8).
+constexpr int kMergeWaves = 8;
+__global__ __launch_bounds__(64 * kMergeWaves) void modea_merge_kernel(ModeALaunch a) {
+  const int nch = (a.dh + 63) / 64;
+  const int hq = blockIdx.x / nch, ch = blockIdx.x - hq * nch;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = ch * 64 + lane;
+  const bool dv = d < a.dh;
+  const int64_t E = a.dh + 2;
+  const float* base = a.partial + (int64_t)hq * a.max_blocks * E;
+  float m = -INFINITY, L = 0.f, A = 0.f;
+  for (int s0 = wave; s0 < a.nsplit; s0 += 4 * kMergeWaves) {
+    float ms[4], ls[4], as[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = s0 + u * kMergeWaves;
+      const bool ok = s < a.nsplit;
+      const float* e0 = base + (int64_t)(ok ? range_begin(a, s) : 0) * E;
+      ms[u] = ok ? e0[E + 2] : -INFINITY;
+      ls[u] = ok ? e0[E + 3] : 0.f;
+      as[u] = ok && dv ? e0[2 + d] : 0.f;
     }
-  a.out[(int64_t)hq * a.dh + d] = A / (Ls + 1e-8f);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (ms[u] == -INFINITY) continue;
+      const float mn = fmaxf(m, ms[u]);
+      const float fo = m == -INFINITY ? 0.f : fast_exp(m - mn), fn = fast_exp(ms[u] - mn);
+      L = L * fo + ls[u] * fn;
+      A = A * fo + as[u] * fn;
+      m = mn;
+    }
+  }
+  __shared__ float sm[kMergeWaves][66];
+  sm[wave][2 + lane] = A;
+  if (lane == 0) { sm[wave][0] = m; sm[wave][1] = L; }
+  __syncthreads();
+  if (wave == 0 && dv) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; ++w) Mx = fmaxf(Mx, sm[w][0]);
+    float Ls = 0.f, As = 0.f;
+    if (Mx != -INFINITY)
+#pragma unroll
+      for (int w = 0; w < kMergeWaves; ++w) {
+        if (sm[w][0] == -INFINITY) continue;
+        const float f = fast_exp(sm[w][0] - Mx);
+        Ls += f * sm[w][1];
+        As += f * sm[w][2 + lane];
+      }
+    a.out[(int64_t)hq * a.dh + d] = As / (Ls + 1e-8f);
+  }
 }
 
-int64_t modea_split_lds_bytes(int dh, int nhp, int num_tiers, int G_max, int cb_max, int page_size) {
+// ---------------------------------------------------------------------------
+// Mode-A decode, vector-load kernel (G_max 4 or 8: a token's code row is one
+// 4- or 8-byte load).  Workgroup = kFastWaves waves on one kv head and one
+// range of logical pages; the range's 16-token tiles are split evenly over
+// the waves (a page of P tokens is P / 16 tiles, so pages of 16 and of 128
+// spread the same way).
+//
+// Per wave, tiles stream through a two-deep register ring: while tile k is
+// scored and accumulated, the loads of tile k + 2 are in flight.  Every load
+// is a buffer load against a resource covering exactly the tile's page (0
+// bytes for an absent page or a tile past the end), so each ring step issues
+// the same loads whatever the page holds and the compiler's vmcnt waits stay
+// exact.  The first two tiles are issued before the workgroup builds its
+// lookup table, so their HBM latency overlaps that work.
+//
+// Lanes score a tile as (token t16 = lane % 16, head row hr = lane / 16) and
+// accumulate P V as (dims [DPL dg, DPL dg + DPL), dg = lane % 16; tokens
+// tq + 4 j, tq = lane / 16).  The table holds <q_g, c> * sm_scale * log2(e) /
+// 255, so a logit in log2 units is sum_g r_scale_g * rcode_g * T[g][code_g]
+// and softmax runs on the hardware exp2.  Each tile's (max, sum) per q head
+// goes to LDS; after the loop the tiles of each page are combined into the
+// reference's per-page (m, l) (decode_kernel.cu:183-205, in natural units).
+// ---------------------------------------------------------------------------
+constexpr int kFastWaves = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegLogit2 = -1e9f * kLog2e;     // the reference's -1e9 logit (decode_kernel.cu:183), log2 units
+
+// LDS carve-up of the vector-load kernel (floats unless noted).
+struct FastLds {
+  int lut, q, p, ts, tbl, red, total;             // offsets in 4-byte words; total bytes
+};
+__host__ __device__ inline FastLds fast_lds(int dh, int nhp, int num_tiers, int G_max, int cb_max, int max_pages,
+                                            int page_size) {
+  const int NH = 4 * nhp;
+  FastLds f;
+  f.lut = 0;
+  f.q = f.lut + NH * num_tiers * G_max * (cb_max + 1);
+  f.p = f.q + NH * dh;
+  f.ts = f.p + kFastWaves * 128;                 // per wave a [16][16] fp16 MFMA operand
+  f.tbl = f.ts + 2 * NH * max_pages * (page_size / 16);
+  f.red = f.tbl + 2 * max_pages;
+  f.total = 4 * (f.red + kFastWaves * NH * (dh + 2));
+  return f;
+}
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int GV, int DPL>
+struct FastTile {
+  int live, tier, slot;                 // wave-uniform: page present, tier, workgroup-local tile index
+  uint32_t th[GV / 4], rd[GV / 4];      // this lane's token: theta and radius code bytes
+  uint32_t rs;                          // lane g < G_tier: r_scales[g]
+  uint32_t v[4][DPL / 2];               // fp16 V: 4 tokens x DPL dims
+};
+
+template <int DH, int NHP, int GV>
+__global__ __launch_bounds__(64 * kFastWaves) void modea_fast_kernel(ModeALaunch a) {
+  constexpr int NH = 4 * NHP;
+  constexpr int DPL = DH / 16;
+  constexpr int W = kFastWaves;
+  constexpr int NTH = 64 * W;
+  extern __shared__ __attribute__((aligned(16))) float fsm[];
+  __shared__ int tG[kModeAMaxTiers], tg[kModeAMaxTiers];
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+  const int hkv = blockIdx.x / a.nsplit, s = blockIdx.x % a.nsplit;
+  const int rb = range_begin(a, s), npg = range_begin(a, s + 1) - rb;
+  const int P = a.page_size, TPP = P / 16;
+  const int max_pages = (a.max_blocks + a.nsplit - 1) / a.nsplit;
+  const FastLds lay = fast_lds(DH, NHP, a.num_tiers, a.G_max, a.cb_max, max_pages, P);
+  float* lut = fsm + lay.lut;                     // [NH][tier][G_max][cb_max + 1], entry cb_max = 0
+  float* qs = fsm + lay.q;
+  _Float16* pa = reinterpret_cast<_Float16*>(fsm + lay.p) + wave * 256;   // P as the MFMA A operand, [16][16] fp16
+  float* ts = fsm + lay.ts;                       // [tile][NH] (max, sum), log2 units
+  int* tbl = reinterpret_cast<int*>(fsm + lay.tbl);   // [page] (phys, tier)
+  float* red = fsm + lay.red;
+  const int T = a.num_tiers, GM = a.G_max, CM = a.cb_max, CMP = CM + 1;
+  const int U = T * GM * CM;                      // lookup-table entries per head row
+
+  // ---- 1. this thread's first lookup-table entry (u = tid): its centroid row's
+  // first 16 coordinates, loaded before anything is staged
+  const bool vec = (a.g_max & 3) == 0;
+  floatx4 cv0[4];
+  {
+    const int tier = tid / (GM * CM), r = tid - tier * GM * CM, g = r / CM, c = r - g * CM;
+    const bool in = tid < U && vec;
+    const float* row = in ? a.cb_flat + ((((int64_t)hkv * T + tier) * GM + g) * CM + c) * a.g_max : a.cb_flat;
+    const int last = in ? a.g_max - 4 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cv0[i] = *reinterpret_cast<const floatx4*>(row + (4 * i < last ? 4 * i : last));
+  }
+
+  // ---- 2. stage: tier geometry, block table range, scaled q, tile stats = (-inf, 0), P rows = 0
+  if (tid < T) { tG[tid] = a.tier_G[tid]; tg[tid] = a.tier_g[tid]; }
+  for (int i = tid; i < npg; i += NTH) {
+    tbl[2 * i] = a.block_table[(int64_t)hkv * a.max_blocks + rb + i];
+    tbl[2 * i + 1] = a.bits_table[(int64_t)hkv * a.max_blocks + rb + i];
+  }
+  const float qscale = a.sm_scale * kLog2e / 255.0f;
+  for (int i = tid; i < NH * DH; i += NTH) {
+    const int h = i / DH;
+    qs[i] = h < a.kv_groups ? a.q[((int64_t)hkv * a.kv_groups + h) * DH + (i - h * DH)] * qscale : 0.f;
+  }
+  for (int i = tid; i < npg * TPP * NH; i += NTH) { ts[2 * i] = -INFINITY; ts[2 * i + 1] = 0.f; }
+  for (int i = tid; i < W * 128; i += NTH) reinterpret_cast<uint32_t*>(fsm + lay.p)[i] = 0u;
+  for (int i = tid; i < NH * T * GM; i += NTH) lut[i * CMP + CM] = 0.f;
+  __syncthreads();
+
+  const int t16 = lane & 15, hr = lane >> 4;
+  const int dg = lane & 15, tq = lane >> 4;
+  const int ntile = npg * TPP;
+  const int k_begin = (int)((int64_t)ntile * wave / W), k_end = (int)((int64_t)ntile * (wave + 1) / W);
+  const int nt = k_end - k_begin;
+  const int tsh = (TPP & (TPP - 1)) == 0 ? __builtin_ctz(TPP) : -1;   // tiles per page as a shift
+
+  // ---- 3. this wave's block-table entries, 64 pages at a time, one per lane
+  int cbase = uniform(k_begin / TPP);
+  int cph = cbase + lane < npg ? tbl[2 * (cbase + lane)] : -1;
+  int ctr = cbase + lane < npg ? tbl[2 * (cbase + lane) + 1] : -1;
+
+  // issue the loads of workgroup-local tile k (k >= k_end: nothing is read)
+  auto issue = [&](FastTile<GV, DPL>& b, int k) {
+    const bool in = k < k_end;
+    const int kc = in ? k : k_begin;
+    const int pl = uniform(tsh >= 0 ? kc >> tsh : kc / TPP), ti = kc - pl * TPP;
+    if (pl - cbase >= 64) {
+      cbase = pl;
+      cph = cbase + lane < npg ? tbl[2 * (cbase + lane)] : -1;
+      ctr = cbase + lane < npg ? tbl[2 * (cbase + lane) + 1] : -1;
+    }
+    const int phys = __builtin_amdgcn_readlane(cph, (pl - cbase) & 63), tier = __builtin_amdgcn_readlane(ctr, (pl - cbase) & 63);
+    const bool tok = tier >= 0 && tier < T && tG[tier] >= 1 && tG[tier] <= GM && tg[tier] >= 1 &&
+                     tg[tier] <= a.g_max && tG[tier] * tg[tier] <= DH;
+    const bool live = in && phys >= 0 && phys < a.num_pages && tok;
+    const int Gt = live ? tG[tier] : 0;
+    b.live = live;
+    b.tier = live ? tier : 0;
+    b.slot = kc;
+    const int64_t pg = live ? phys : 0;
+    const rsrc_t rth = make_rsrc(a.theta_codes + pg * P * GM, live ? (int64_t)P * GM : 0);
+    const rsrc_t rrd = make_rsrc(a.radius_codes + pg * P * GM, live ? (int64_t)P * GM : 0);
+    const rsrc_t rrs = make_rsrc(a.r_scales + pg * GM, live ? (int64_t)GM * 4 : 0);
+    const rsrc_t rv = make_rsrc(a.v_pool + pg * P * DH, live ? (int64_t)P * DH * 2 : 0);
+    const int row = (ti * 16 + t16) * GV;
+    if constexpr (GV == 8) {
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rth, row, 0, 0);
+      const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(rrd, row, 0, 0);
+      b.th[0] = x[0]; b.th[1] = x[1]; b.rd[0] = y[0]; b.rd[1] = y[1];
+    } else {
+      b.th[0] = __builtin_amdgcn_raw_buffer_load_b32(rth, row, 0, 0);
+      b.rd[0] = __builtin_amdgcn_raw_buffer_load_b32(rrd, row, 0, 0);
+    }
+    b.rs = __builtin_amdgcn_raw_buffer_load_b32(rrs, lane < Gt ? 4 * lane : kOOB, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int off = ((ti * 16 + tq + 4 * j) * DH + DPL * dg) * 2;
+      if constexpr (DPL == 8) {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+        b.v[j][0] = w[0]; b.v[j][1] = w[1]; b.v[j][2] = w[2]; b.v[j][3] = w[3];
+      } else {
+        const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
+        b.v[j][0] = w[0]; b.v[j][1] = w[1];
+      }
+    }
+  };
+
+  // ---- 4. the first two tiles
+  FastTile<GV, DPL> b0, b1;
+  issue(b0, k_begin);
+  issue(b1, k_begin + 1);
+
+  // ---- 5. lookup table: entry u = (tier, g, c) holds <q_h,g, centroid> for
+  // every head row h, one head row at a time
+  auto entry_finish = [&](int tier, int g, int c, const floatx4 (&first)[4]) {
+    const int gt = tg[tier];
+    const float* row = a.cb_flat + ((((int64_t)hkv * T + tier) * GM + g) * CM + c) * a.g_max;
+    const float* qg = qs + g * gt;
+    float* dst = lut + (tier * GM + g) * CMP + c;
+    for (int d0 = 0; d0 < gt; d0 += 16) {
+      floatx4 cv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (d0 == 0) cv[i] = first[i];
+        else cv[i] = *reinterpret_cast<const floatx4*>(row + (d0 + 4 * i < gt ? d0 + 4 * i : gt - 4));
+        if (d0 + 4 * i + 4 > gt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (d0 + 4 * i + e >= gt) cv[i][e] = 0.f;
+      }
+#pragma unroll 1
+      for (int h = 0; h < NH; ++h) {
+        float dot = d0 == 0 ? 0.f : dst[h * T * GM * CMP];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dq = d0 + 4 * i + 4 <= gt ? d0 + 4 * i : 0;
+          const floatx4 qv = *reinterpret_cast<const floatx4*>(qg + h * DH + dq);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dot = __builtin_fmaf(qv[e], cv[i][e], dot);
+        }
+        dst[h * T * GM * CMP] = dot;
+      }
+    }
+  };
+  auto do_entry = [&](int u, bool first_loaded) {
+    if (u >= U) return;
+    const int tier = u / (GM * CM), r = u - tier * GM * CM, g = r / CM, c = r - g * CM;
+    const bool ok = tier_ok(a, tier, tG, tg) && g < tG[tier];
+    if (ok && vec) {
+      if (first_loaded) {
+        entry_finish(tier, g, c, cv0);
+      } else {
+        const float* row = a.cb_flat + ((((int64_t)hkv * T + tier) * GM + g) * CM + c) * a.g_max;
+        floatx4 cv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cv[i] = *reinterpret_cast<const floatx4*>(row + (4 * i < a.g_max - 4 ? 4 * i : a.g_max - 4));
+        entry_finish(tier, g, c, cv);
+      }
+    } else if (ok) {
+      const int gt = tg[tier];
+      const float* row = a.cb_flat + ((((int64_t)hkv * T + tier) * GM + g) * CM + c) * a.g_max;
+      const float* qg = qs + g * gt;
+      for (int h = 0; h < NH; ++h) {
+        float dot = 0.f;
+        for (int d = 0; d < gt; ++d) dot = __builtin_fmaf(qg[h * DH + d], row[d], dot);
+        lut[((h * T + tier) * GM + g) * CMP + c] = dot;
+      }
+    } else {
+      for (int h = 0; h < NH; ++h) lut[((h * T + tier) * GM + g) * CMP + c] = 0.f;
+    }
+  };
+  do_entry(tid, true);
+  for (int u = tid + NTH; u < U; u += NTH) do_entry(u, false);
+  __syncthreads();
+
+  // running (max, sum) of this lane's head rows (log2 units); P V accumulators
+  // in the MFMA D layout: acc[j][i] = out[head 4 (lane / 16) + i][dim DPL (lane % 16) + j]
+  float Mw[NHP], Lw[NHP];
+  floatx4 acc[DPL];
+#pragma unroll
+  for (int hp = 0; hp < NHP; ++hp) { Mw[hp] = -INFINITY; Lw[hp] = 0.f; }
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto process = [&](const FastTile<GV, DPL>& b) {
+    if (!b.live) return;
+    // logits of (token t16, head row hr + 4 hp); a code >= cb_max reads the
+    // row's zero entry
+    float lg[NHP];
+#pragma unroll
+    for (int hp = 0; hp < NHP; ++hp) {
+      const float* lt = lut + ((hr + 4 * hp) * T + b.tier) * GM * CMP;
+      float sum = 0.f;
+#pragma unroll
+      for (int g = 0; g < GV; ++g) {
+        const uint32_t code = (b.th[g / 4] >> (8 * (g % 4))) & 0xFFu;
+        const float rc = (float)((b.rd[g / 4] >> (8 * (g % 4))) & 0xFFu);
+        const float rsg = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)b.rs, g));
+        const float v = lt[g * CMP + (code < (uint32_t)CM ? code : (uint32_t)CM)];
+        sum = __builtin_fmaf(rsg * rc, v, sum);
+      }
+      lg[hp] = sum == 0.f ? kNegLogit2 : sum;                               // decode_kernel.cu:183
+    }
+    bool grow = false;
+    float fo[NHP];
+#pragma unroll
+    for (int hp = 0; hp < NHP; ++hp) {
+      const float mt = rmax16(lg[hp]);
+      const float e = __builtin_amdgcn_exp2f(lg[hp] - mt);
+      const float ls = rsum16(e);
+      if (t16 == 0) { ts[2 * (b.slot * NH + hr + 4 * hp)] = mt; ts[2 * (b.slot * NH + hr + 4 * hp) + 1] = ls; }
+      const float mn = fmaxf(Mw[hp], mt);
+      const float fn = __builtin_amdgcn_exp2f(mt - mn);
+      fo[hp] = __builtin_amdgcn_exp2f(Mw[hp] - mn);
+      grow |= mn > Mw[hp];
+      Lw[hp] = Lw[hp] * fo[hp] + ls * fn;
+      Mw[hp] = mn;
+      // A operand row (head), k = 4 (t16 % 4) + t16 / 4 <-> token t16
+      pa[(hr + 4 * hp) * 16 + 4 * (t16 & 3) + (t16 >> 2)] = (_Float16)(e * fn);
+    }
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      float f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fo[0]), 16 * i));
+        if constexpr (NHP == 2) {
+          const float f2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fo[NHP - 1]), 16 * i));
+          if (lane >= 16) f[i] = f2;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] *= f[i];
+    }
+    wave_lds_sync();
+    // P (A: row = lane % 16, k = 4 (lane / 16) + i <-> token lane / 16 + 4 i)
+    const half4 pA = *reinterpret_cast<const half4*>(pa + (lane & 15) * 16 + 4 * (lane >> 4));
+    // V (B: column = lane % 16 <-> dim DPL (lane % 16) + j, k as above): this
+    // lane's four token rows tq + 4 i, one dim per MFMA
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t lo = __builtin_amdgcn_perm(b.v[1][j / 2], b.v[0][j / 2], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(b.v[3][j / 2], b.v[2][j / 2], sel);
+      const half4 vB = __builtin_bit_cast(half4, (u32x2){lo, hi});
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pA, vB, acc[j], 0, 0, 0);
+    }
+    wave_lds_sync();
+  };
+
+  for (int k = 0; k < nt; k += 2) {
+    process(b0);
+    issue(b0, k_begin + k + 2);
+    if (k + 1 < nt) process(b1);
+    issue(b1, k_begin + k + 3);
+  }
+
+  // ---- this wave's partial -> LDS
+  float* rw = red + wave * NH * (DH + 2);
+  if ((lane >> 4) < NHP)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rw[(4 * (lane >> 4) + i) * (DH + 2) + 2 + DPL * dg + j] = acc[j][i];
+  if (t16 == 0)
+#pragma unroll
+    for (int hp = 0; hp < NHP; ++hp) {
+      rw[(hr + 4 * hp) * (DH + 2)] = Mw[hp];
+      rw[(hr + 4 * hp) * (DH + 2) + 1] = Lw[hp];
+    }
+  __syncthreads();
+
+  // ---- per-page (m, l) of each q head from its tiles (decode_kernel.cu:199-205)
+  for (int i = tid; i < npg * a.kv_groups; i += 64 * W) {
+    const int pl = i / a.kv_groups, h = i - pl * a.kv_groups;
+    float m = -INFINITY;
+    for (int t = 0; t < TPP; ++t) m = fmaxf(m, ts[2 * ((pl * TPP + t) * NH + h)]);
+    float l = 0.f;
+    if (m != -INFINITY)
+      for (int t = 0; t < TPP; ++t) {
+        const float mt = ts[2 * ((pl * TPP + t) * NH + h)];
+        if (mt != -INFINITY) l += ts[2 * ((pl * TPP + t) * NH + h) + 1] * __builtin_amdgcn_exp2f(mt - m);
+      }
+    float* pt = a.partial + ((int64_t)(hkv * a.kv_groups + h) * a.max_blocks + rb + pl) * (DH + 2);
+    pt[0] = m * kLn2;
+    pt[1] = l;
+  }
+  // ---- merge the waves; write out (one range) or this range's partial
+  for (int i = tid; i < a.kv_groups * DH; i += 64 * W) {
+    const int h = i / DH, d = i - h * DH;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, red[(w * NH + h) * (DH + 2)]);
+    float Ls = 0.f, A = 0.f;
+    if (Mx != -INFINITY)
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = red[(w * NH + h) * (DH + 2)];
+        if (mw == -INFINITY) continue;
+        const float f = __builtin_amdgcn_exp2f(mw - Mx);
+        Ls += f * red[(w * NH + h) * (DH + 2) + 1];
+        A += f * red[(w * NH + h) * (DH + 2) + 2 + d];
+      }
+    const int hq = hkv * a.kv_groups + h;
+    if (a.nsplit == 1) {
+      a.out[(int64_t)hq * DH + d] = A / (Ls + 1e-8f);                    // decode_kernel.cu:244-245
+    } else {
+      float* e0 = a.partial + ((int64_t)hq * a.max_blocks + rb) * (DH + 2);
+      e0[2 + d] = A;
+      if (d == 0) {
+        e0[(DH + 2) + 2] = Mx * kLn2;
+        e0[(DH + 2) + 3] = Ls;
+      }
+    }
+  }
+}
+
+static int64_t general_lds_bytes(int dh, int nhp, int num_tiers, int G_max, int cb_max, int page_size) {
   const int NH = 4 * nhp;
   return 4LL * ((int64_t)NH * num_tiers * G_max * cb_max + 4LL * page_size * NH + 4LL * NH * (dh + 2));
 }
 
-template <int DH, int NHP>
-static int launch_modea_t(const ModeALaunch& L, hipStream_t stream) {
-  const int64_t lds = modea_split_lds_bytes(DH, NHP, L.num_tiers, L.G_max, L.cb_max, L.page_size);
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&modea_split_kernel<DH, NHP>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+int64_t modea_configure(ModeALaunch& L) {
+  const int nhp = L.kv_groups <= 4 ? 1 : 2;
+  const int mb = L.max_blocks > 0 ? L.max_blocks : 1;
+  L.fast = (L.G_max == 4 || L.G_max == 8) ? 1 : 0;
+  // one 16-wave workgroup (fast) or eight 4-wave workgroups (general) per CU
+  const int target = L.fast ? 256 : 2048;
+  int nsplit = L.num_kv > 0 ? (target + L.num_kv - 1) / L.num_kv : 1;
+  if (nsplit > mb / 2) nsplit = mb / 2;
+  if (nsplit < 1) nsplit = 1;
+  if (L.fast) {
+    // the range's block table and tile stats live in LDS: split finer until they fit
+    auto bytes = [&](int ns) {
+      return (int64_t)fast_lds(L.dh, nhp, L.num_tiers, L.G_max, L.cb_max, (mb + ns - 1) / ns, L.page_size).total;
+    };
+    while (bytes(nsplit) > 160 * 1024 && nsplit < mb / 2) nsplit = nsplit * 2 <= mb / 2 ? nsplit * 2 : mb / 2;
+    L.nsplit = nsplit;
+    const int64_t b = bytes(nsplit);
+    if (b <= 160 * 1024) return b;
+    L.fast = 0;
+  }
+  L.nsplit = nsplit;
+  return general_lds_bytes(L.dh, nhp, L.num_tiers, L.G_max, L.cb_max, L.page_size);
+}
+
+template <typename K>
+static int launch_split(K kernel, const ModeALaunch& L, int threads, int64_t lds, hipStream_t stream) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL((modea_split_kernel<DH, NHP>), dim3(L.num_kv * L.nsplit), dim3(256), (size_t)lds, stream, L);
-  if (L.nsplit > 1) hipLaunchKernelGGL(modea_merge_kernel, dim3(L.num_q), dim3(128), 0, stream, L);
+  hipLaunchKernelGGL(kernel, dim3(L.num_kv * L.nsplit), dim3(threads), (size_t)lds, stream, L);
+  if (L.nsplit > 1)
+    hipLaunchKernelGGL(modea_merge_kernel, dim3(L.num_q * ((L.dh + 63) / 64)), dim3(64 * kMergeWaves), 0, stream, L);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_modea(const ModeALaunch& L, hipStream_t stream) {
-  if (L.num_kv <= 0 || L.max_blocks <= 0) return 0;
+int launch_modea(const ModeALaunch& L0, hipStream_t stream) {
+  if (L0.num_kv <= 0 || L0.max_blocks <= 0) return 0;
+  ModeALaunch L = L0;
+  const int64_t lds = modea_configure(L);
+  if (lds > 160 * 1024) return -1;
   const int nhp = L.kv_groups <= 4 ? 1 : 2;
-  if (L.dh == 128 && nhp == 1) return launch_modea_t<128, 1>(L, stream);
-  if (L.dh == 128 && nhp == 2) return launch_modea_t<128, 2>(L, stream);
-  if (L.dh == 64 && nhp == 1) return launch_modea_t<64, 1>(L, stream);
-  if (L.dh == 64 && nhp == 2) return launch_modea_t<64, 2>(L, stream);
+  const int ft = 64 * kFastWaves;
+  if (L.fast) {
+    if (L.dh == 128 && nhp == 1) return L.G_max == 8 ? launch_split(&modea_fast_kernel<128, 1, 8>, L, ft, lds, stream)
+                                                     : launch_split(&modea_fast_kernel<128, 1, 4>, L, ft, lds, stream);
+    if (L.dh == 128 && nhp == 2) return L.G_max == 8 ? launch_split(&modea_fast_kernel<128, 2, 8>, L, ft, lds, stream)
+                                                     : launch_split(&modea_fast_kernel<128, 2, 4>, L, ft, lds, stream);
+    if (L.dh == 64 && nhp == 1) return L.G_max == 8 ? launch_split(&modea_fast_kernel<64, 1, 8>, L, ft, lds, stream)
+                                                    : launch_split(&modea_fast_kernel<64, 1, 4>, L, ft, lds, stream);
+    if (L.dh == 64 && nhp == 2) return L.G_max == 8 ? launch_split(&modea_fast_kernel<64, 2, 8>, L, ft, lds, stream)
+                                                    : launch_split(&modea_fast_kernel<64, 2, 4>, L, ft, lds, stream);
+    return -1;
+  }
+  if (L.dh == 128 && nhp == 1) return launch_split(&modea_split_kernel<128, 1>, L, 256, lds, stream);
+  if (L.dh == 128 && nhp == 2) return launch_split(&modea_split_kernel<128, 2>, L, 256, lds, stream);
+  if (L.dh == 64 && nhp == 1) return launch_split(&modea_split_kernel<64, 1>, L, 256, lds, stream);
+  if (L.dh == 64 && nhp == 2) return launch_split(&modea_split_kernel<64, 2>, L, 256, lds, stream);
   return -1;
 }
 

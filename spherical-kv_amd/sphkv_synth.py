@@ -166,7 +166,7 @@ MODEA_TIERS = {1: (16, 6), 2: (16, 4), 3: (32, 3)}
 
 def make_modea_workload(seed: int = 11, num_kv: int = 8, kv_groups: int = 4, dh: int = 128,
                         page_size: int = 16, ctx: int = 4096, tiers=(1, 2), fracs=None,
-                        holes: float = 0.0, spare_pages: int = 0) -> Dict[str, object]:
+                        holes: float = 0.0, spare_pages: int = 0, G_pad: int = 0) -> Dict[str, object]:
     """LayerPool-shaped Mode-A tables (sphkv_lut.py:71-127) from a seeded draw.
 
     Every kv head holds ctx tokens in ceil(ctx / page_size) logical pages placed
@@ -174,14 +174,15 @@ def make_modea_workload(seed: int = 11, num_kv: int = 8, kv_groups: int = 4, dh:
     uniform theta codes below that tier's C, uniform uint8 radius codes,
     lognormal radius scales; slots past ctx stay zero (codes 0, radius 0), the
     state sphkv_encode_append leaves them in.  `holes` is the fraction of
-    logical pages marked absent (-1).  cb_flat rows are normalize(N(0,1)),
+    logical pages marked absent (-1); G_pad widens G_max (code rows and tables)
+    beyond the tiers' largest group count.  cb_flat rows are normalize(N(0,1)),
     zero padded to [G_max, cb_max, g_max]; V ~ N(0,1) fp16; q ~ N(0,1) fp32.
     """
     rng = np.random.default_rng(seed)
     T = len(tiers)
     fracs = np.ones(T) if fracs is None else np.asarray(fracs, np.float64)
     geo = [(dh // MODEA_TIERS[t][0], MODEA_TIERS[t][0], 1 << MODEA_TIERS[t][1]) for t in tiers]   # (G, g, C)
-    G_max = max(G for G, _, _ in geo)
+    G_max = max(max(G for G, _, _ in geo), G_pad)
     g_max = max(g for _, g, _ in geo)
     cb_max = max(C for _, _, C in geo)
     cb_flat = np.zeros((num_kv, T, G_max, cb_max, g_max), np.float32)

@@ -64,6 +64,9 @@ CASES = [
     dict(dh=64, kv_groups=8, page_size=32, ctx=777, tiers=(1, 3), holes=0.05),
     dict(dh=128, kv_groups=1, page_size=16, ctx=17, tiers=(2,), holes=0.0),
     dict(dh=64, kv_groups=2, page_size=64, ctx=5000, tiers=(1, 2), holes=0.3),
+    # G_max outside {4, 8}: the general kernel
+    dict(dh=64, kv_groups=4, page_size=16, ctx=1500, tiers=(1, 3), holes=0.1, G_pad=6),
+    dict(dh=128, kv_groups=8, page_size=48, ctx=2000, tiers=(1, 2, 3), holes=0.0, G_pad=12),
 ]
 
 
@@ -83,7 +86,7 @@ def _modea_call(w, gpu):
     return out.cpu().numpy(), part.cpu().numpy(), dev
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"dh{c['dh']}-g{c['kv_groups']}-p{c['page_size']}" for c in CASES])
+@pytest.mark.parametrize("case", CASES, ids=[f"dh{c['dh']}-g{c['kv_groups']}-p{c['page_size']}-G{c.get('G_pad', 0)}" for c in CASES])
 def test_decode_modea_matches_oracle(gpu, case):
     w = synth.make_modea_workload(seed=31, num_kv=4, **case)
     log(f"modea {case} max_blocks={w['max_blocks']}")
