@@ -542,14 +542,23 @@ __global__ __launch_bounds__(64 * kFastWaves) void modea_fast_kernel(ModeALaunch
     for (int i = 0; i < 4; ++i) cv0[i] = *reinterpret_cast<const floatx4*>(row + (4 * i < last ? 4 * i : last));
   }
 
-  // ---- 2. stage: tier geometry, block table range, scaled q, tile stats = (-inf, 0), P rows = 0
-  if (tid < T) { tG[tid] = a.tier_G[tid]; tg[tid] = a.tier_g[tid]; }
-  for (int i = tid; i < npg; i += NTH) {
-    tbl[2 * i] = a.block_table[(int64_t)hkv * a.max_blocks + rb + i];
-    tbl[2 * i + 1] = a.bits_table[(int64_t)hkv * a.max_blocks + rb + i];
-  }
+  // ---- 2. stage: tier geometry, block table range, scaled q, tile stats = (-inf, 0), P rows = 0.
+  // The first slice of each staged array is loaded into registers before any
+  // is written, so the loads share one round trip.
+  const int64_t tb0 = (int64_t)hkv * a.max_blocks + rb;
+  const int tgv0 = tid < T ? a.tier_G[tid] : 0, tgv1 = tid < T ? a.tier_g[tid] : 0;
+  const int bt0 = tid < npg ? a.block_table[tb0 + tid] : 0, bb0 = tid < npg ? a.bits_table[tb0 + tid] : 0;
+  const int qh0 = tid / DH;
+  const float qv0 = tid < NH * DH && qh0 < a.kv_groups ? a.q[((int64_t)hkv * a.kv_groups + qh0) * DH + (tid - qh0 * DH)] : 0.f;
   const float qscale = a.sm_scale * kLog2e / 255.0f;
-  for (int i = tid; i < NH * DH; i += NTH) {
+  if (tid < T) { tG[tid] = tgv0; tg[tid] = tgv1; }
+  if (tid < npg) { tbl[2 * tid] = bt0; tbl[2 * tid + 1] = bb0; }
+  if (tid < NH * DH) qs[tid] = qv0 * qscale;
+  for (int i = tid + NTH; i < npg; i += NTH) {
+    tbl[2 * i] = a.block_table[tb0 + i];
+    tbl[2 * i + 1] = a.bits_table[tb0 + i];
+  }
+  for (int i = tid + NTH; i < NH * DH; i += NTH) {
     const int h = i / DH;
     qs[i] = h < a.kv_groups ? a.q[((int64_t)hkv * a.kv_groups + h) * DH + (i - h * DH)] * qscale : 0.f;
   }
