@@ -243,6 +243,22 @@ int sphkv_logits_lut(const float* q_lut, const uint8_t* theta_codes, const uint8
                      int32_t max_blocks, int32_t page_size, int32_t G_max, int32_t cb_size_max,
                      float sm_scale, int32_t max_ctx, void* stream);
 
+/*
+ * omega importance EMA from a decode's per-page statistics; replaces
+ * _omega_ema_eager / _omega_ema_compiled (spherical_kv_pipeline.py:952-987)
+ * as called by _update_omega_gpu (:1669-1701).  m_q, l_q: the (m, l) of
+ * (q head hq, logical page p) at m_q[hq * q_stride + p * page_stride] (the
+ * [..., 0] and [..., 1] views of partial_scratch: q_stride =
+ * max_blocks * (dh + 2), page_stride = dh + 2).  Per q head, pages with
+ * l > 0 get w = exp(max(m - max, -60)) * l, mass = w / max(sum w, 1e-12);
+ * omega_out[h, p] = omega_prev[h, p] * ema_beta + mean_{hq of h} mass *
+ * (1 - ema_beta).  omega_prev / omega_out fp32 [num_kv, max_blocks]; they
+ * may be the same buffer.  kv_groups 1..64.
+ */
+int sphkv_omega_ema(const float* m_q, const float* l_q, int64_t q_stride, int64_t page_stride,
+                    const float* omega_prev, float* omega_out, int32_t num_kv, int32_t kv_groups,
+                    int32_t max_blocks, float ema_beta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

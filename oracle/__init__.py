@@ -412,3 +412,17 @@ def lut_logits(lut, theta, radius, r_scales, block_table, bits_table, ctx_lens, 
             vals = np.where(codes < cb_max, lut[hq, t, np.arange(G_max), np.minimum(codes, cb_max - 1)], 0.0)
             out[hq, n] = (rh * vals).sum() * sm_scale
     return out
+
+
+def omega_ema(m_q, l_q, omega_prev, num_kv: int, kv_groups: int, ema_beta: float) -> np.ndarray:
+    """spherical_kv_pipeline.py:952-987 (_omega_ema_eager) in fp64: m_q, l_q
+    [num_q, max_blocks]; omega_prev [num_kv, max_blocks]."""
+    m = np.asarray(m_q, np.float64)
+    l = np.asarray(l_q, np.float64)
+    valid = l > 0
+    m_safe = np.where(valid, m, -1e30)
+    m_max = m_safe.max(axis=1, keepdims=True)
+    w = np.exp(np.maximum(m_safe - m_max, -60.0)) * l
+    z = np.maximum(w.sum(axis=1, keepdims=True), 1e-12)
+    mass_kv = (w / z).reshape(num_kv, kv_groups, -1).mean(axis=1)
+    return np.asarray(omega_prev, np.float64) * ema_beta + mass_kv * (1.0 - ema_beta)

@@ -292,4 +292,19 @@ int sphkv_logits_lut(const float* q_lut, const uint8_t* theta_codes, const uint8
   return launch_status(sphkv::launch_lut_logits(L, (hipStream_t)stream), fn);
 }
 
+int sphkv_omega_ema(const float* m_q, const float* l_q, int64_t q_stride, int64_t page_stride,
+                    const float* omega_prev, float* omega_out, int32_t num_kv, int32_t kv_groups,
+                    int32_t max_blocks, float ema_beta, void* stream) {
+  const char* fn = "sphkv_omega_ema";
+  if (num_kv < 0 || max_blocks < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (kv_groups < 1 || kv_groups > sphkv::kOmegaMaxGroups)
+    return fail(SPHKV_EINVAL, "%s: kv_groups must be 1..%d", fn, sphkv::kOmegaMaxGroups);
+  if (q_stride < 0 || page_stride < 0) return fail(SPHKV_EINVAL, "%s: negative stride", fn);
+  if (num_kv == 0 || max_blocks == 0) return ok();
+  if (!m_q || !l_q || !omega_prev || !omega_out) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::OmegaLaunch L{m_q, l_q, q_stride, page_stride, omega_prev, omega_out, num_kv, kv_groups, max_blocks,
+                       ema_beta};
+  return launch_status(sphkv::launch_omega(L, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

@@ -66,7 +66,15 @@ struct LutLogitsLaunch {
   int64_t num_pages; float sm_scale;
 };
 
+constexpr int kOmegaMaxGroups = 64;
+struct OmegaLaunch {
+  const float* m; const float* l; int64_t q_stride, page_stride;   // element strides of the (m, l) views
+  const float* omega_prev; float* omega_out;                        // [num_kv, max_blocks]; may alias
+  int32_t num_kv, kv_groups, max_blocks; float beta;
+};
+
 int launch_append(const AppendLaunch& L, hipStream_t stream);
+int launch_omega(const OmegaLaunch& L, hipStream_t stream);
 int launch_modea(const ModeALaunch& L, hipStream_t stream);
 int launch_qlut(const ModeALaunch& L, float* lut, hipStream_t stream);
 int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream);

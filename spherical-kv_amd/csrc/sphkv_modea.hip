@@ -956,3 +956,70 @@ int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream) {
 }
 
 }  // namespace sphkv
+
+namespace sphkv {
+
+// ---------------------------------------------------------------------------
+// omega EMA from the decode's per-page statistics (spherical_kv_pipeline.py:
+// 952-987): per q head, pages with l > 0 compete in a softmax of their (m, l)
+// -- w = exp(max(m - max_p m, -60)) * l, mass = w / max(sum w, 1e-12) -- the
+// masses are averaged over each kv head's q heads and blended into omega:
+// omega' = omega * beta + mass * (1 - beta).  One workgroup per kv head.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float x = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, x) : v + x;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+__global__ __launch_bounds__(256) void omega_ema_kernel(OmegaLaunch a) {
+  __shared__ float red[4];
+  __shared__ float mx_s[kOmegaMaxGroups], z_s[kOmegaMaxGroups];
+  const int h = blockIdx.x;
+  for (int r = 0; r < a.kv_groups; ++r) {
+    const int64_t qb = (int64_t)(h * a.kv_groups + r) * a.q_stride;
+    float mx = -1e30f;
+    for (int p = threadIdx.x; p < a.max_blocks; p += blockDim.x) {
+      const float l = a.l[qb + (int64_t)p * a.page_stride];
+      if (l > 0.f) mx = fmaxf(mx, a.m[qb + (int64_t)p * a.page_stride]);
+    }
+    mx = block_reduce(mx, true, red);
+    float z = 0.f;
+    for (int p = threadIdx.x; p < a.max_blocks; p += blockDim.x) {
+      const float l = a.l[qb + (int64_t)p * a.page_stride];
+      const float m = l > 0.f ? a.m[qb + (int64_t)p * a.page_stride] : -1e30f;
+      z += expf(fmaxf(m - mx, -60.f)) * l;
+    }
+    z = block_reduce(z, false, red);
+    if (threadIdx.x == 0) { mx_s[r] = mx; z_s[r] = fmaxf(z, 1e-12f); }
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < a.max_blocks; p += blockDim.x) {
+    float s = 0.f;
+    for (int r = 0; r < a.kv_groups; ++r) {
+      const int64_t qb = (int64_t)(h * a.kv_groups + r) * a.q_stride + (int64_t)p * a.page_stride;
+      const float l = a.l[qb];
+      const float m = l > 0.f ? a.m[qb] : -1e30f;
+      s += expf(fmaxf(m - mx_s[r], -60.f)) * l / z_s[r];
+    }
+    const float mass = s / (float)a.kv_groups;
+    const int64_t o = (int64_t)h * a.max_blocks + p;
+    a.omega_out[o] = a.omega_prev[o] * a.beta + mass * (1.f - a.beta);
+  }
+}
+
+int launch_omega(const OmegaLaunch& L, hipStream_t stream) {
+  if (L.num_kv > 0 && L.max_blocks > 0)
+    hipLaunchKernelGGL(omega_ema_kernel, dim3(L.num_kv), dim3(256), 0, stream, L);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace sphkv

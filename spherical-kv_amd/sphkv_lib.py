@@ -41,6 +41,7 @@ SIGNATURES = {
     "sphkv_q_lut": (ctypes.c_int, [P, P, P, P, I32, I32, I32, I32, I32, I32, I32, I32, P, P]),
     "sphkv_logits_lut": (ctypes.c_int, [P, P, P, P, I64, P, P, P, P, I32, I32, I32, I32, I32, I32, I32,
                                         I32, F32, I32, P]),
+    "sphkv_omega_ema": (ctypes.c_int, [P, P, I64, I64, P, P, I32, I32, I32, F32, P]),
 }
 
 

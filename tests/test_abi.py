@@ -182,3 +182,14 @@ def test_q_lut_and_logits_argument_errors():
     assert lib.sphkv_logits_lut(*lg) == -1 and "bad table geometry" in lib.sphkv_last_error().decode()
     lg[16], lg[18] = 64, 0
     assert lib.sphkv_logits_lut(*lg) == 0
+
+
+def test_omega_ema_argument_errors():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_omega_ema(None, None, 130, 2, None, None, 8, 0, 64, 0.9, None) == -1
+    assert "kv_groups" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_omega_ema(None, None, -1, 2, None, None, 8, 4, 64, 0.9, None) == -1
+    assert "negative stride" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_omega_ema(None, None, 130, 2, None, None, 8, 4, 64, 0.9, None) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_omega_ema(None, None, 130, 2, None, None, 8, 4, 0, 0.9, None) == 0

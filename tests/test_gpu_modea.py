@@ -142,3 +142,37 @@ def test_modea_single_range_and_empty_tables(gpu):
                                       w["r_scales"], w["v_pool"], w["block_table"], w["bits_table"], 4, w["sm_scale"])
     assert max_err(got, want) <= TOL
     assert (got[4:] == 0).all()                       # acc 0 / (0 + 1e-8)
+
+
+def test_omega_ema_after_decode_matches_oracle(gpu):
+    """The decode's partial_scratch (m, l) views feed the omega update in place
+    (spherical_kv_pipeline.py:1690-1701), with absent pages and a head whose
+    pages are all absent."""
+    import omega_ema
+    w = synth.make_modea_workload(seed=17, num_kv=4, kv_groups=4, dh=128, page_size=16, ctx=3000,
+                                  tiers=(1, 2), holes=0.2)
+    w["block_table"] = w["block_table"].copy()
+    w["block_table"][3, :] = -1
+    _, part, _ = _modea_call(w, gpu)
+    rng = np.random.default_rng(2)
+    prev = rng.random((w["num_kv"], w["max_blocks"])).astype(np.float32)
+    scratch = torch.from_numpy(part).to(gpu)
+    ml = scratch[:, :, :2]
+    for beta in (0.9, 0.0):
+        got = omega_ema.omega_ema(ml[..., 0], ml[..., 1], _t(prev, gpu), w["num_kv"], 4, w["max_blocks"], beta)
+        want = oracle.omega_ema(part[:, :, 0], part[:, :, 1], prev, w["num_kv"], 4, beta)
+        err = np.abs(got.cpu().numpy() - want).max()
+        log(f"omega beta={beta} max abs err {err:.3e}")
+        np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-5, atol=1e-7)
+    # in place, and a pool-like object through update_omega_gpu
+    om = _t(prev, gpu)
+    omega_ema.omega_ema(ml[..., 0], ml[..., 1], om, w["num_kv"], 4, w["max_blocks"], 0.9, out=om)
+    np.testing.assert_allclose(om.cpu().numpy(), oracle.omega_ema(part[:, :, 0], part[:, :, 1], prev, 4, 4, 0.9),
+                               rtol=1e-5, atol=1e-7)
+    pool = type("P", (), dict(num_kv=w["num_kv"], kv_groups=4, max_blocks=w["max_blocks"], device=gpu,
+                              _partial_scratch=scratch))()
+    d = {}
+    first = omega_ema.update_omega_gpu(d, 0, pool)
+    want1 = oracle.omega_ema(part[:, :, 0], part[:, :, 1], np.ones_like(prev), 4, 4, 0.9)
+    np.testing.assert_allclose(first.cpu().numpy(), want1, rtol=1e-5, atol=1e-7)
+    assert (first.cpu().numpy()[3] == np.float32(0.9)).all()   # head without pages: mass 0
