@@ -259,6 +259,23 @@ int sphkv_omega_ema(const float* m_q, const float* l_q, int64_t q_stride, int64_
                     const float* omega_prev, float* omega_out, int32_t num_kv, int32_t kv_groups,
                     int32_t max_blocks, float ema_beta, void* stream);
 
+/*
+ * LayerPool page build from per-(head, tier) token arrays; replaces the
+ * per-page loop of LayerPool.__init__ (sphkv_lut.py:44-66, 83-87).
+ * r fp32 / theta int32: concatenated [rows, G_t] arrays (n_elems elements);
+ * v fp16 [n_vrows, dh].  page_src int32 [n_pages, 4]: per page (element
+ * offset of its first r / theta row, its first V row, npg, G_t).  Page i
+ * becomes pool page pid0 + i: r_scales[g] = max(max_n r, 1e-8), radius code
+ * clamp(round_half_even(r / r_scale * 255), 0, 255), theta code = low byte,
+ * V rows copied; slots >= npg and groups >= G_t are untouched (the pools
+ * start zeroed, as the reference allocates them).  A descriptor outside the
+ * given arrays leaves its page untouched.  G_max <= 256.
+ */
+int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems, const uint16_t* v,
+                           int64_t n_vrows, const int32_t* page_src, int32_t n_pages, int32_t pid0,
+                           uint8_t* theta_codes, uint8_t* radius_codes, float* r_scales, uint16_t* v_pool,
+                           int64_t pool_pages, int32_t page_size, int32_t G_max, int32_t dh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -426,3 +426,54 @@ def omega_ema(m_q, l_q, omega_prev, num_kv: int, kv_groups: int, ema_beta: float
     z = np.maximum(w.sum(axis=1, keepdims=True), 1e-12)
     mass_kv = (w / z).reshape(num_kv, kv_groups, -1).mean(axis=1)
     return np.asarray(omega_prev, np.float64) * ema_beta + mass_kv * (1.0 - ema_beta)
+
+
+def layer_pool_page(r_chunk: np.ndarray, theta_chunk: np.ndarray):
+    """One LayerPool page's quantisation (sphkv_lut.py:56-61) in the
+    reference's fp32 arithmetic: r_scale = max(max_n r, 1e-8); radius code =
+    clamp(round_half_even(r / r_scale * 255), 0, 255); theta code = low byte.
+    Returns (theta uint8 [npg, G_t], radius uint8 [npg, G_t], r_scale fp32 [G_t])."""
+    r = np.asarray(r_chunk, np.float32)
+    rscl = np.maximum(r.max(axis=0), np.float32(1e-8))
+    q = np.rint((r / rscl) * np.float32(255.0))
+    rad = np.clip(q, 0, 255).astype(np.uint8)
+    th = (np.asarray(theta_chunk).astype(np.int64) & 0xFF).astype(np.uint8)
+    return th, rad, rscl.astype(np.float32)
+
+
+def layer_pool(per_head: dict, num_kv: int, page_size: int, G_max: int, dh: int, decode_capacity: int,
+               tier_of_btheta: dict):
+    """LayerPool.__init__ pools and tables (sphkv_lut.py:36-98) in numpy.
+    per_head[h] = list of (b_theta, n_tokens, V fp16 [n, dh], r fp32 [n, G_t],
+    theta int [n, G_t]); tier_of_btheta[b_theta] = (tier index, G_t).
+    Returns dict(theta, radius, r_scales, v_pool, block_table, bits_table,
+    ctx_lens, max_blocks, num_pages_used)."""
+    pages, head_blocks, ctx = [], {h: [] for h in range(num_kv)}, [0] * num_kv
+    for h in range(num_kv):
+        for b_theta, n_tokens, V, r, th in per_head.get(h, []):
+            t_idx, G_t = tier_of_btheta[b_theta]
+            for pg in range(-(-n_tokens // page_size)):
+                s, e = pg * page_size, min((pg + 1) * page_size, n_tokens)
+                tpg, rpg, spg = layer_pool_page(r[s:e], th[s:e])
+                head_blocks[h].append((len(pages), t_idx))
+                pages.append((G_t, e - s, tpg, rpg, spg, np.asarray(V[s:e], np.float16)))
+        ctx[h] = len(head_blocks[h]) * page_size
+    n_used = len(pages)
+    n_total = n_used + decode_capacity
+    max_blk = max((len(v) for v in head_blocks.values()), default=0) + decode_capacity // max(num_kv, 1) + 2
+    theta = np.zeros((n_total, page_size, G_max), np.uint8)
+    radius = np.zeros_like(theta)
+    r_scales = np.zeros((n_total, G_max), np.float32)
+    v_pool = np.zeros((n_total, page_size, dh), np.float16)
+    for pid, (G_t, n, tpg, rpg, spg, v) in enumerate(pages):
+        theta[pid, :n, :G_t] = tpg
+        radius[pid, :n, :G_t] = rpg
+        r_scales[pid, :G_t] = spg
+        v_pool[pid, :n] = v
+    bt = np.full((num_kv, max_blk), -1, np.int32)
+    bits = np.zeros((num_kv, max_blk), np.int32)
+    for h, bl in head_blocks.items():
+        for lb, (pid, ti) in enumerate(bl):
+            bt[h, lb], bits[h, lb] = pid, ti
+    return dict(theta=theta, radius=radius, r_scales=r_scales, v_pool=v_pool, block_table=bt, bits_table=bits,
+                ctx_lens=np.asarray(ctx, np.int32), max_blocks=max_blk, num_pages_used=n_used)

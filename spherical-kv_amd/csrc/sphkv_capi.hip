@@ -307,4 +307,25 @@ int sphkv_omega_ema(const float* m_q, const float* l_q, int64_t q_stride, int64_
   return launch_status(sphkv::launch_omega(L, (hipStream_t)stream), fn);
 }
 
+int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems, const uint16_t* v,
+                           int64_t n_vrows, const int32_t* page_src, int32_t n_pages, int32_t pid0,
+                           uint8_t* theta_codes, uint8_t* radius_codes, float* r_scales, uint16_t* v_pool,
+                           int64_t pool_pages, int32_t page_size, int32_t G_max, int32_t dh, void* stream) {
+  const char* fn = "sphkv_build_layer_pool";
+  if (n_pages < 0 || pid0 < 0 || n_elems < 0 || n_vrows < 0 || pool_pages < 0)
+    return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if ((int64_t)pid0 + n_pages > pool_pages)
+    return fail(SPHKV_EINVAL, "%s: pages %d..%lld exceed the pool (%lld pages)", fn, pid0,
+                (long long)pid0 + n_pages, (long long)pool_pages);
+  if (page_size < 1 || G_max < 1 || G_max > sphkv::kPoolBuildMaxG || dh < 2 || (dh & 1))
+    return fail(SPHKV_EINVAL, "%s: bad geometry (page_size %d, G_max %d, dh %d)", fn, page_size, G_max, dh);
+  if (n_pages == 0) return ok();
+  if (!r || !theta || !v || !page_src || !theta_codes || !radius_codes || !r_scales || !v_pool)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::PoolBuildLaunch L{r, theta, n_elems, reinterpret_cast<const _Float16*>(v), n_vrows, page_src, n_pages, pid0,
+                           theta_codes, radius_codes, r_scales, reinterpret_cast<_Float16*>(v_pool), page_size,
+                           G_max, dh};
+  return launch_status(sphkv::launch_pool_build(L, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

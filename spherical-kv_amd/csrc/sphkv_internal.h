@@ -73,8 +73,18 @@ struct OmegaLaunch {
   int32_t num_kv, kv_groups, max_blocks; float beta;
 };
 
+constexpr int kPoolBuildMaxG = 256;
+struct PoolBuildLaunch {
+  const float* r; const int32_t* theta; int64_t n_elems;    // concatenated [rows, G_t] token arrays
+  const _Float16* v; int64_t n_vrows;                       // concatenated fp16 V rows [rows, dh]
+  const int32_t* page_src; int32_t n_pages, pid0;           // per page (r offset, V row, npg, G_t)
+  uint8_t* theta_codes; uint8_t* radius_codes; float* r_scales; _Float16* v_pool;
+  int32_t page_size, G_max, dh;
+};
+
 int launch_append(const AppendLaunch& L, hipStream_t stream);
 int launch_omega(const OmegaLaunch& L, hipStream_t stream);
+int launch_pool_build(const PoolBuildLaunch& L, hipStream_t stream);
 int launch_modea(const ModeALaunch& L, hipStream_t stream);
 int launch_qlut(const ModeALaunch& L, float* lut, hipStream_t stream);
 int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream);

@@ -1023,3 +1023,51 @@ int launch_omega(const OmegaLaunch& L, hipStream_t stream) {
 }
 
 }  // namespace sphkv
+
+namespace sphkv {
+
+// ---------------------------------------------------------------------------
+// LayerPool pages from per-(head, tier) token arrays (sphkv_lut.py:44-66):
+// page i (pool page pid0 + i) takes npg <= page_size tokens of a tier with
+// G_t groups: r_scale[g] = max(max_n r[n, g], 1e-8); radius code =
+// clamp(round_half_even(r / r_scale * 255), 0, 255); theta code = low byte of
+// theta; V rows copied.  Slots past npg and groups past G_t are left as they
+// are (the caller's pools start zeroed).  One workgroup per page.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void layer_pool_build_kernel(PoolBuildLaunch a) {
+  __shared__ float rscl[kPoolBuildMaxG];
+  const int i = blockIdx.x;
+  const int32_t* d = a.page_src + 4 * (int64_t)i;
+  const int64_t off = d[0], voff = d[1];
+  const int npg = d[2], Gt = d[3];
+  if (npg < 0 || npg > a.page_size || Gt < 1 || Gt > a.G_max || off < 0 || voff < 0 ||
+      off + (int64_t)npg * Gt > a.n_elems || voff + npg > a.n_vrows)
+    return;                                          // malformed descriptor: page left untouched
+  const int64_t pid = (int64_t)a.pid0 + i;
+  for (int g = threadIdx.x; g < Gt; g += blockDim.x) {
+    float m = -INFINITY;
+    for (int n = 0; n < npg; ++n) m = fmaxf(m, a.r[off + (int64_t)n * Gt + g]);
+    const float s = fmaxf(m, 1e-8f);                 // .amax(dim=0).clamp(min=1e-8)
+    rscl[g] = s;
+    a.r_scales[pid * a.G_max + g] = s;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < npg * Gt; e += blockDim.x) {
+    const int n = e / Gt, g = e - n * Gt;
+    const float q = rintf(a.r[off + e] / rscl[g] * 255.0f);
+    const int64_t dst = (pid * a.page_size + n) * a.G_max + g;
+    a.radius_codes[dst] = (uint8_t)fminf(fmaxf(q, 0.f), 255.f);
+    a.theta_codes[dst] = (uint8_t)(a.theta[off + e] & 0xFF);
+  }
+  const uint32_t* vs = reinterpret_cast<const uint32_t*>(a.v + voff * a.dh);
+  uint32_t* vd = reinterpret_cast<uint32_t*>(a.v_pool + pid * a.page_size * a.dh);
+  for (int e = threadIdx.x; e < npg * a.dh / 2; e += blockDim.x) vd[e] = vs[e];
+}
+
+int launch_pool_build(const PoolBuildLaunch& L, hipStream_t stream) {
+  if (L.n_pages > 0)
+    hipLaunchKernelGGL(layer_pool_build_kernel, dim3(L.n_pages), dim3(256), 0, stream, L);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace sphkv

@@ -157,3 +157,24 @@ def test_lut_logits_equal_rebuilt_key_dot_products():
             K = _rebuilt_keys(w, hkv, p)
             want = K @ w["q"][hq].astype(np.float64) * w["sm_scale"]
             np.testing.assert_allclose(lg[hq, n0:n1], want[:n1 - n0], atol=1e-9)
+
+
+def test_layer_pool_page_closed_forms():
+    r = np.array([[2.0, 0.0, 1.0], [1.0, 0.0, 3.0], [0.5, 0.0, 3.0]], np.float32)
+    th, rad, rs = oracle.layer_pool_page(r, np.array([[1, 2, 300], [4, 5, 6], [7, 8, 9]]))
+    np.testing.assert_array_equal(rs, np.array([2.0, 1e-8, 3.0], np.float32))
+    assert rad[0, 0] == 255 and rad[1, 0] == 128 and rad[2, 0] == 64   # 127.5 -> 128 (even), 63.75 -> 64
+    assert (rad[:, 1] == 0).all()                                       # all-zero group
+    assert rad[1, 2] == 255 and rad[2, 2] == 255 and rad[0, 2] == 85
+    assert th[0, 2] == 300 & 0xFF                                       # .to(torch.uint8) keeps the low byte
+
+
+def test_layer_pool_page_rounding_bound_and_monotone():
+    rng = np.random.default_rng(4)
+    r = np.abs(rng.standard_normal((128, 8))).astype(np.float32)
+    _, rad, rs = oracle.layer_pool_page(r, np.zeros((128, 8), np.int32))
+    exact = r.astype(np.float64) / rs.astype(np.float64) * 255.0
+    assert np.abs(rad - exact).max() <= 0.5 + 1e-4
+    for g in range(8):
+        o = np.argsort(r[:, g], kind="stable")
+        assert (np.diff(rad[o, g].astype(int)) >= 0).all()
