@@ -276,6 +276,37 @@ int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems
                            uint8_t* theta_codes, uint8_t* radius_codes, float* r_scales, uint16_t* v_pool,
                            int64_t pool_pages, int32_t page_size, int32_t G_max, int32_t dh, void* stream);
 
+/*
+ * Device page planning for prefill; replaces the grouping, sort, chunking and
+ * offset computation of _build_per_head_pages (spherical_kv_pipeline.py:
+ * 1146-1228; offsets :1202-1213).  The result equals
+ * sphkv_format.plan_pages with logical placement.
+ *
+ * tier_of uint8 [num_seqs * num_kv, tier_stride]: tier id of each token for
+ * (sequence s, kv head h) in row s * num_kv + h (0 dropped, 1..3, 0xFF
+ * dense); only the first lens[s] entries of a row are read.
+ *
+ * Phase 1, sphkv_plan_pages_count: work int32 [num_seqs * num_kv, 16];
+ * row_start int32 [num_seqs * num_kv + 1]; totals int32 [4], zero on entry,
+ * receives (rows, byte-pool size or -1 when >= 2 GiB, invalid tier ids,
+ * offset overflows).
+ *
+ * Phase 2, sphkv_plan_pages_fill: per row (capacity max_rows >= totals[0])
+ * tier, count, ptable [rows, 3], seq_head, vslot (= row), tokens int64
+ * [rows, 16] (token index, -1 pad), positions_out int32 [rows, 16]
+ * (positions[s * pos_stride + t], or t when positions is null; -1 pad) and,
+ * when row_base is given, src_rows int64 [rows, 16] = row_base[s * num_kv +
+ * h] + t (-1 pad).
+ */
+int sphkv_plan_pages_count(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, int32_t num_seqs,
+                           int32_t num_kv, int32_t dh, int32_t* work, int32_t* row_start, int32_t* totals,
+                           void* stream);
+int sphkv_plan_pages_fill(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, const int32_t* positions,
+                          int64_t pos_stride, const int64_t* row_base, int32_t num_seqs, int32_t num_kv, int32_t dh,
+                          const int32_t* work, int32_t max_rows, int32_t* tier, int32_t* count, int32_t* ptable,
+                          int32_t* seq_head, int32_t* vslot, int64_t* tokens, int32_t* positions_out,
+                          int64_t* src_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

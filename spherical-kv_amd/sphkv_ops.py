@@ -166,6 +166,27 @@ class PagedPool:
             seq_head=torch.as_tensor(plan.seq_head, device=dev),
         )
 
+    @staticmethod
+    def allocate_device(plan: "DevicePlan", codebooks: Dict[int, np.ndarray], device="cuda",
+                        rows_per_item: Optional[int] = None) -> "PagedPool":
+        """A pool over a plan built on the GPU (plan_pages_gpu): the plan's
+        device arrays are used in place; its layout holds by construction."""
+        dev = torch.device(device)
+        if rows_per_item is None:
+            rows_per_item = auto_rows_per_item(plan.row_start, torch.cuda.get_device_properties(dev).multi_processor_count)
+        work, ws = make_work(plan.row_start, rows_per_item)
+        cbs = {int(t): torch.as_tensor(np.ascontiguousarray(c, np.float32), device=dev) for t, c in codebooks.items()}
+        for tid, c in cbs.items():
+            g, b = fmt.TIER_GEOMETRY[tid]
+            if tuple(c.shape) != (plan.num_kv, plan.dh // g, 2 ** b, g):
+                raise ValueError(f"tier {tid} codebook shape {tuple(c.shape)}")
+        return PagedPool(
+            plan=plan, pages=torch.zeros(plan.pages_bytes, dtype=torch.uint8, device=dev), ptable=plan.ptable,
+            vslot=plan.vslot, positions=plan.positions,
+            v_pool=torch.zeros((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
+            codebooks=cbs, work=torch.as_tensor(work, device=dev), work_start=torch.as_tensor(ws, device=dev),
+            tier=plan.tier, count=plan.count, seq_head=plan.seq_head)
+
     def cb_ptrs(self):
         return tuple(_ptr(self.codebooks.get(t)) for t in (1, 2, 3))
 
@@ -286,6 +307,94 @@ def merge_partials(pool: PagedPool, workspace: torch.Tensor, gqa: int,
         plan.num_seqs, plan.num_kv, gqa, plan.dh, out.data_ptr(), _stream())
     check(rc, "sphkv_decode_merge_partials")
     return out
+
+
+@dataclass
+class DevicePlan:
+    """A page plan built on the GPU by plan_pages_gpu.  Per-row arrays stay on
+    the device; only the totals and the (seq, head) row ranges come back to
+    the host.  Duck-types the fields of sphkv_format.PagePlan that pools and
+    kernels use."""
+    dh: int
+    page_size: int
+    num_seqs: int
+    num_kv: int
+    pages_bytes: int
+    num_vpages: int
+    rows: int
+    row_start: np.ndarray       # [num_seqs*num_kv + 1] int32 (host)
+    tier: torch.Tensor          # [P] int32
+    count: torch.Tensor         # [P] int32
+    ptable: torch.Tensor        # [P, 3] int32
+    seq_head: torch.Tensor      # [P] int32
+    vslot: torch.Tensor         # [P] int32
+    tokens: torch.Tensor        # [P, 16] int64
+    positions: torch.Tensor     # [P, 16] int32
+    src_rows: Optional[torch.Tensor]   # [P, 16] int64 rows of the K/V matrices, or None
+
+    @property
+    def num_rows(self) -> int:
+        return self.rows
+
+    def to_host(self) -> fmt.PagePlan:
+        return fmt.PagePlan(dh=self.dh, page_size=self.page_size, num_seqs=self.num_seqs, num_kv=self.num_kv,
+                            tier=self.tier.cpu().numpy(), count=self.count.cpu().numpy(),
+                            tokens=self.tokens.cpu().numpy(), positions=self.positions.cpu().numpy(),
+                            seq_head=self.seq_head.cpu().numpy(), row_start=self.row_start.copy(),
+                            ptable=self.ptable.cpu().numpy(), vslot=self.vslot.cpu().numpy(),
+                            pages_bytes=self.pages_bytes, num_vpages=self.num_vpages)
+
+
+def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: int,
+                   positions: Optional[torch.Tensor] = None, row_base: Optional[torch.Tensor] = None) -> DevicePlan:
+    """Device-side equivalent of sphkv_format.plan_pages (logical placement):
+    the grouping / sort / chunk / offset steps of _build_per_head_pages
+    (spherical_kv_pipeline.py:1146-1228) on the GPU.
+
+    tier_of: uint8 [num_seqs*num_kv, L_max] tier id per token (row s*num_kv+h);
+    lens: int32 [num_seqs]; positions: int32 [num_seqs, L_max] or None (token
+    index); row_base: int64 [num_seqs*num_kv] K row of each (seq, head)'s
+    token 0, or None (no src_rows).  One host synchronisation (the totals)."""
+    dev = tier_of.device
+    _need(tier_of, torch.uint8, "tier_of", dev)
+    _need(lens, torch.int32, "lens", dev)
+    if tier_of.dim() != 2 or lens.dim() != 1 or tier_of.shape[0] != lens.shape[0] * num_kv:
+        raise ValueError("tier_of must be [num_seqs*num_kv, L_max] and lens [num_seqs]")
+    num_seqs, num_sh = int(lens.shape[0]), int(tier_of.shape[0])
+    if positions is not None:
+        _need(positions, torch.int32, "positions", dev)
+        if positions.dim() != 2 or positions.shape[0] != num_seqs or positions.shape[1] < tier_of.shape[1]:
+            raise ValueError("positions must be [num_seqs, >= L_max]")
+    if row_base is not None:
+        _need(row_base, torch.int64, "row_base", dev)
+        if tuple(row_base.shape) != (num_sh,):
+            raise ValueError("row_base must be [num_seqs*num_kv]")
+    lib = load()
+    work = torch.empty(max(num_sh, 1) * 16, dtype=torch.int32, device=dev)
+    row_start = torch.zeros(num_sh + 1, dtype=torch.int32, device=dev)
+    totals = torch.zeros(4, dtype=torch.int32, device=dev)
+    rc = lib.sphkv_plan_pages_count(tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), num_seqs, int(num_kv),
+                                    int(dh), work.data_ptr(), row_start.data_ptr(), totals.data_ptr(), _stream())
+    check(rc, "sphkv_plan_pages_count")
+    rows, nbytes, bad, ovf = (int(x) for x in totals.cpu())
+    if bad:
+        raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")
+    if nbytes < 0 or ovf:
+        raise ValueError("page byte pool exceeds int32 offsets")
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = dict(tier=torch.empty(rows, **i32), count=torch.empty(rows, **i32), ptable=torch.empty((rows, 3), **i32),
+               seq_head=torch.empty(rows, **i32), vslot=torch.empty(rows, **i32),
+               tokens=torch.empty((rows, 16), dtype=torch.int64, device=dev), positions=torch.empty((rows, 16), **i32),
+               src_rows=None if row_base is None else torch.empty((rows, 16), dtype=torch.int64, device=dev))
+    rc = lib.sphkv_plan_pages_fill(
+        tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), _ptr(positions),
+        0 if positions is None else positions.stride(0), _ptr(row_base), num_seqs, int(num_kv), int(dh),
+        work.data_ptr(), rows, out["tier"].data_ptr(), out["count"].data_ptr(), out["ptable"].data_ptr(),
+        out["seq_head"].data_ptr(), out["vslot"].data_ptr(), out["tokens"].data_ptr(), out["positions"].data_ptr(),
+        _ptr(out["src_rows"]), _stream())
+    check(rc, "sphkv_plan_pages_fill")
+    return DevicePlan(dh=int(dh), page_size=16, num_seqs=num_seqs, num_kv=int(num_kv), pages_bytes=nbytes,
+                      num_vpages=rows, rows=rows, row_start=row_start.cpu().numpy(), **out)
 
 
 def build_pool_gpu(wl, device="cuda", rows_per_item: Optional[int] = None, with_codes: bool = False):
