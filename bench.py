@@ -13,8 +13,10 @@ kernels run on (torch's current stream), around exactly K steps.
 Prints one JSON line (see the "roofline" and "cpu_baseline" objects).
 
 `--path modea` measures the Mode-A (LayerPool) decode instead, on the same
-attention shape with unpacked uint8 pools (fused_decode.sphkv_decode); the
-default line is the angle-domain (Mode-B) decode above.
+attention shape with unpacked uint8 pools (fused_decode.sphkv_decode);
+`--path prefill` measures prefill paging of the same layer on the GPU (device
+page plan + fused encode / bitpack / V placement).  The default line is the
+angle-domain (Mode-B) decode above.
 """
 from __future__ import annotations
 
@@ -191,6 +193,73 @@ def bench_modea(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_prefill(args, dev):
+    """One step = page one layer's retained K/V: device plan
+    (plan_pages_gpu, including its one host synchronisation) + fused encode
+    into a fresh pool.  CPU baseline: the host planner plus the oracle's C
+    encode / page build over the same tokens."""
+    log(f"[bench] building config{args.config} workload for prefill paging")
+    wl = synth.make_decode_workload(args.config, layout="sequential")
+    L_max = max(wl.lengths)
+    t = np.zeros((len(wl.tier_of), L_max), np.uint8)
+    for sh, arr in enumerate(wl.tier_of):
+        t[sh, :len(arr)] = np.asarray(arr, np.int64) & 0xFF
+    tier_of = torch.from_numpy(t).to(dev)
+    lens = torch.tensor(np.asarray(wl.lengths, np.int32), device=dev)
+    row_base = torch.from_numpy(wl.row_base()).to(dev)
+    k = torch.as_tensor(wl.k_rows(), device=dev)
+    v = torch.as_tensor(wl.v_rows(), device=dev)
+
+    def step():
+        dp = ops.plan_pages_gpu(tier_of, lens, wl.num_kv, wl.dh, row_base=row_base)
+        pool = ops.PagedPool.allocate_device(dp, wl.codebooks, dev)
+        ops.encode_pages(pool, k, v, dp.src_rows)
+        return dp, pool
+
+    for _ in range(args.warmup):
+        dp, pool = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dp, pool = step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = e0.elapsed_time(e1) / args.steps
+    n_tok = int(sum(len(x) for x in wl.tier_of))
+    kept = int(sum(int(np.count_nonzero(np.asarray(x))) for x in wl.tier_of))
+    nbytes = kept * wl.dh * 2 * 2 + dp.pages_bytes + dp.rows * 16 * wl.dh * 2
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] prefill paging {ms * 1e3:.1f} us/layer ({wall_ms * 1e3:.1f} us host wall), rows {dp.rows}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, ROOT)
+        import oracle
+        c0 = time.perf_counter()
+        plan = fmt.plan_pages(wl.tier_of, None, wl.num_seqs, wl.num_kv, wl.dh, 16)
+        oracle.build_pool(synth.Workload(**{**wl.__dict__, "plan": plan}))
+        cpu_us = (time.perf_counter() - c0) * 1e6
+        cpu = {"value": round(cpu_us, 1), "unit": "µs/layer", "cores": 1, "kind": "port",
+               "sample": f"the whole layer ({kept} kept of {n_tok} token-heads): sphkv_format.plan_pages + "
+                         f"oracle C encode / page build (spherical_kv_pipeline.py:1130-1228, pagebuilder.py:8-33)"}
+    line = {
+        "metric": "µs per prefill paging of one layer (plan + encode + bitpack + V placement), 1 GPU",
+        "value": round(ms * 1e3, 3), "unit": "µs/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 in, u8 pages", "data": "synthetic (seeded generator, config spec of BASELINE.json)",
+        "config": {"workload": f"config{args.config}: {wl.num_kv} kv heads, dh {wl.dh}, {wl.num_seqs} seq x "
+                               f"{L_max} tokens, tier mix of BASELINE", "rows": dp.rows,
+                   "algorithmic_bytes_per_step": int(nbytes)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "plan_count/scan/fill + encode_pages_kernel", "kernel_us": round(ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,8 +270,9 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
                     help="page placement: the config's own (random for configs 2-5) or sequential")
-    ap.add_argument("--path", default="modeb", choices=["modeb", "modea"],
-                    help="modeb: the angle-domain paged decode (the headline); modea: LayerPool decode")
+    ap.add_argument("--path", default="modeb", choices=["modeb", "modea", "prefill"],
+                    help="modeb: the angle-domain paged decode (the headline); modea: LayerPool decode; "
+                         "prefill: device page plan + fused encode")
     ap.add_argument("--page-size", type=int, default=16, help="Mode-A page size (16..128, multiple of 16)")
     ap.add_argument("--calibrate", action="store_true",
                     help="after timing, run plain device copies of COPY_BYTES (torch copy_), the "
@@ -220,6 +290,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.path == "modea":
         bench_modea(args, dev)
+        return
+    if args.path == "prefill":
+        bench_prefill(args, dev)
         return
 
     log(f"[bench] building config{args.config} workload")

@@ -286,10 +286,14 @@ int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems
  * (sequence s, kv head h) in row s * num_kv + h (0 dropped, 1..3, 0xFF
  * dense); only the first lens[s] entries of a row are read.
  *
- * Phase 1, sphkv_plan_pages_count: work int32 [num_seqs * num_kv, 16];
- * row_start int32 [num_seqs * num_kv + 1]; totals int32 [4], zero on entry,
- * receives (rows, byte-pool size or -1 when >= 2 GiB, invalid tier ids,
- * offset overflows).
+ * lens[s] <= max_len <= tier_stride for every sequence; tokens are
+ * processed in chunks, max_len sizes the grid.  The workspace holds
+ * sphkv_plan_pages_work_ints(num_seqs, num_kv, max_len) int32 and carries
+ * the counts from phase 1 to phase 2 (same arguments in both).
+ *
+ * Phase 1, sphkv_plan_pages_count: row_start int32
+ * [num_seqs * num_kv + 1]; totals int32 [4], zero on entry, receives (rows,
+ * byte-pool size or -1 when >= 2 GiB, invalid tier ids, offset overflows).
  *
  * Phase 2, sphkv_plan_pages_fill: per row (capacity max_rows >= totals[0])
  * tier, count, ptable [rows, 3], seq_head, vslot (= row), tokens int64
@@ -298,14 +302,15 @@ int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems
  * when row_base is given, src_rows int64 [rows, 16] = row_base[s * num_kv +
  * h] + t (-1 pad).
  */
+int64_t sphkv_plan_pages_work_ints(int32_t num_seqs, int32_t num_kv, int32_t max_len);
 int sphkv_plan_pages_count(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, int32_t num_seqs,
-                           int32_t num_kv, int32_t dh, int32_t* work, int32_t* row_start, int32_t* totals,
-                           void* stream);
+                           int32_t num_kv, int32_t max_len, int32_t dh, int32_t* work, int64_t work_ints,
+                           int32_t* row_start, int32_t* totals, void* stream);
 int sphkv_plan_pages_fill(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, const int32_t* positions,
-                          int64_t pos_stride, const int64_t* row_base, int32_t num_seqs, int32_t num_kv, int32_t dh,
-                          const int32_t* work, int32_t max_rows, int32_t* tier, int32_t* count, int32_t* ptable,
-                          int32_t* seq_head, int32_t* vslot, int64_t* tokens, int32_t* positions_out,
-                          int64_t* src_rows, void* stream);
+                          int64_t pos_stride, const int64_t* row_base, int32_t num_seqs, int32_t num_kv,
+                          int32_t max_len, int32_t dh, const int32_t* work, int32_t max_rows, int32_t* tier,
+                          int32_t* count, int32_t* ptable, int32_t* seq_head, int32_t* vslot, int64_t* tokens,
+                          int32_t* positions_out, int64_t* src_rows, void* stream);
 
 #ifdef __cplusplus
 }

@@ -328,35 +328,44 @@ int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems
   return launch_status(sphkv::launch_pool_build(L, (hipStream_t)stream), fn);
 }
 
+int64_t sphkv_plan_pages_work_ints(int32_t num_seqs, int32_t num_kv, int32_t max_len) {
+  if (num_seqs < 0 || num_kv < 1 || max_len < 0) return -1;
+  return sphkv::plan_work_ints(num_seqs * num_kv, max_len);
+}
+
 int sphkv_plan_pages_count(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, int32_t num_seqs,
-                           int32_t num_kv, int32_t dh, int32_t* work, int32_t* row_start, int32_t* totals,
-                           void* stream) {
+                           int32_t num_kv, int32_t max_len, int32_t dh, int32_t* work, int64_t work_ints,
+                           int32_t* row_start, int32_t* totals, void* stream) {
   const char* fn = "sphkv_plan_pages_count";
   if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
-  if (num_seqs < 0 || num_kv < 1 || tier_stride < 0) return fail(SPHKV_EINVAL, "%s: bad sizes", fn);
+  if (num_seqs < 0 || num_kv < 1 || tier_stride < 0 || max_len < 0 || max_len > tier_stride)
+    return fail(SPHKV_EINVAL, "%s: bad sizes (need 0 <= max_len <= tier_stride)", fn);
   if (num_seqs == 0) return ok();
+  if (work_ints < sphkv::plan_work_ints(num_seqs * num_kv, max_len))
+    return fail(SPHKV_EINVAL, "%s: workspace too small", fn);
   if (!tier_of || !lens || !work || !row_start || !totals) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
   sphkv::PlanLaunch L{};
-  L.tier_of = tier_of; L.tier_stride = tier_stride; L.lens = lens; L.num_sh = num_seqs * num_kv;
+  L.tier_of = tier_of; L.tier_stride = tier_stride; L.lens = lens; L.max_len = max_len; L.num_sh = num_seqs * num_kv;
   L.num_kv = num_kv; L.dh = dh; L.work = work; L.totals = totals; L.row_start = row_start;
   return launch_status(sphkv::launch_plan(L, 0, (hipStream_t)stream), fn);
 }
 
 int sphkv_plan_pages_fill(const uint8_t* tier_of, int64_t tier_stride, const int32_t* lens, const int32_t* positions,
-                          int64_t pos_stride, const int64_t* row_base, int32_t num_seqs, int32_t num_kv, int32_t dh,
-                          const int32_t* work, int32_t max_rows, int32_t* tier, int32_t* count, int32_t* ptable,
-                          int32_t* seq_head, int32_t* vslot, int64_t* tokens, int32_t* positions_out,
-                          int64_t* src_rows, void* stream) {
+                          int64_t pos_stride, const int64_t* row_base, int32_t num_seqs, int32_t num_kv,
+                          int32_t max_len, int32_t dh, const int32_t* work, int32_t max_rows, int32_t* tier,
+                          int32_t* count, int32_t* ptable, int32_t* seq_head, int32_t* vslot, int64_t* tokens,
+                          int32_t* positions_out, int64_t* src_rows, void* stream) {
   const char* fn = "sphkv_plan_pages_fill";
   if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
-  if (num_seqs < 0 || num_kv < 1 || tier_stride < 0 || pos_stride < 0 || max_rows < 0)
+  if (num_seqs < 0 || num_kv < 1 || tier_stride < 0 || pos_stride < 0 || max_rows < 0 || max_len < 0 ||
+      max_len > tier_stride || (positions && max_len > pos_stride && num_seqs > 1))
     return fail(SPHKV_EINVAL, "%s: bad sizes", fn);
   if (num_seqs == 0 || max_rows == 0) return ok();
   if (!tier_of || !lens || !work || !tier || !count || !ptable || !seq_head || !vslot || !tokens || !positions_out)
     return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
   sphkv::PlanLaunch L{};
-  L.tier_of = tier_of; L.tier_stride = tier_stride; L.lens = lens; L.pos = positions; L.pos_stride = pos_stride;
-  L.row_base = row_base; L.num_sh = num_seqs * num_kv; L.num_kv = num_kv; L.dh = dh;
+  L.tier_of = tier_of; L.tier_stride = tier_stride; L.lens = lens; L.max_len = max_len; L.pos = positions;
+  L.pos_stride = pos_stride; L.row_base = row_base; L.num_sh = num_seqs * num_kv; L.num_kv = num_kv; L.dh = dh;
   L.work = const_cast<int32_t*>(work); L.max_rows = max_rows; L.tier = tier; L.count = count; L.ptable = ptable;
   L.seq_head = seq_head; L.vslot = vslot; L.tokens = tokens; L.positions = positions_out; L.src_rows = src_rows;
   return launch_status(sphkv::launch_plan(L, 1, (hipStream_t)stream), fn);

@@ -83,14 +83,15 @@ struct PoolBuildLaunch {
 };
 
 // Device page planning (sphkv_plan.hip)
-constexpr int kPlanRecInts = 16;        // workspace int32 per (sequence, kv head)
 struct PlanLaunch {
   const uint8_t* tier_of; int64_t tier_stride;   // [num_sh, >= L_s] tier id per token
   const int32_t* lens;                           // [num_seqs] tokens per sequence
+  int32_t max_len;                               // >= every lens[s]: sizes the token chunks
+  int32_t nchunks;                               // set by launch_plan
   const int32_t* pos; int64_t pos_stride;        // [num_seqs, >= L_s] positions, or null (token index)
   const int64_t* row_base;                       // [num_sh] K row of token 0, or null (no src_rows)
   int32_t num_sh, num_kv, dh;
-  int32_t* work;                                 // [num_sh, kPlanRecInts]
+  int32_t* work;                                 // plan_work_ints(num_sh, max_len) int32
   int32_t* totals;                               // [4]: rows, pool bytes (-1: >= 2 GiB), invalid ids, overflow
   int32_t* row_start;                            // [num_sh + 1]
   int32_t max_rows;                              // capacity of the per-row outputs
@@ -99,6 +100,7 @@ struct PlanLaunch {
   int64_t* tokens; int32_t* positions; int64_t* src_rows;   // [rows, 16]; src_rows may be null
 };
 int launch_plan(const PlanLaunch& L, int phase, hipStream_t stream);
+int64_t plan_work_ints(int num_sh, int max_len);
 
 int launch_append(const AppendLaunch& L, hipStream_t stream);
 int launch_omega(const OmegaLaunch& L, hipStream_t stream);

@@ -10,14 +10,17 @@
 // 16-byte aligned offsets (a dense fp16 page so that its payload after the
 // 8-byte header is 16-byte aligned).
 //
-// Kernels:
-//   plan_count_kernel  per (sequence, head): tokens and first index per tier
-//   plan_scan_kernel   one thread: row starts and each tier run's byte start
-//                      (page i of a run starts at run_start + i * align16(size
-//                      of a full page), so a run is placed in O(1))
-//   plan_fill_kernel   per (sequence, head): page rows, then each token's
-//                      rank within its tier (wave ballots + a block scan) puts
-//                      it in its page slot
+// Kernels (a (sequence, head)'s tokens are cut into chunks of kPlanChunk):
+//   plan_count_kernel  per (sequence, head, chunk): tokens and first index
+//                      per tier, by wave ballots
+//   plan_scan_kernel   one workgroup: per (sequence, head) the chunks' rank
+//                      bases, tier order and rows (a thread each), then one
+//                      thread places the tier runs back to back (page i of a
+//                      run starts at run_start + i * align16(size of a full
+//                      page), so a run is placed in O(1))
+//   plan_fill_kernel   per (sequence, head, chunk): its share of the page
+//                      rows, then each token's rank within its tier (chunk
+//                      base + wave ballots) puts it in its page slot
 #include "sphkv_common.h"
 #include "sphkv_internal.h"
 
@@ -48,34 +51,73 @@ __device__ __forceinline__ int64_t place(int64_t off, int k) {
   return o < 0 ? o + 16 : o;
 }
 
-// per (sequence, head) record in the workspace
+// per (sequence, head) record in the workspace, followed by the chunks' records
 enum : int { kCnt = 0, kFirst = 4, kRows = 8, kOrder = 9, kRunStart = 10, kRowStart = 14, kRec = 16 };
+enum : int { kChCnt = 0, kChFirst = 4, kChRec = 8 };    // per chunk: counts (then rank bases), first index
+constexpr int kPlanChunk = 2048;
+
+__device__ __forceinline__ int32_t* sh_rec(const PlanLaunch& a, int sh) { return a.work + (int64_t)sh * kRec; }
+__device__ __forceinline__ int32_t* ch_rec(const PlanLaunch& a, int sh, int c) {
+  return a.work + (int64_t)a.num_sh * kRec + ((int64_t)sh * a.nchunks + c) * kChRec;
+}
 
 }  // namespace
 
 __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(PlanLaunch a) {
-  __shared__ int cnt[4], first[4], bad;
-  const int sh = blockIdx.x, s = sh / a.num_kv;
-  if (threadIdx.x < 4) { cnt[threadIdx.x] = 0; first[threadIdx.x] = 0x7FFFFFFF; }
-  if (threadIdx.x == 0) bad = 0;
-  __syncthreads();
-  const int L = a.lens[s];
+  __shared__ int wc[kPlanThreads / 64][4], wf[kPlanThreads / 64][4], wbad[kPlanThreads / 64];
+  const int sh = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks, s = sh / a.num_kv;
+  const int L = min(a.lens[s], a.max_len), t0 = c * kPlanChunk, t1 = min(L, t0 + kPlanChunk);
+  if (c == 0 && threadIdx.x == 0 && (a.lens[s] > a.max_len || a.lens[s] < 0)) atomicAdd(a.totals + 3, 1);
   const uint8_t* t_of = a.tier_of + (int64_t)sh * a.tier_stride;
-  for (int t = threadIdx.x; t < L; t += kPlanThreads) {
-    const int k = tier_slot(t_of[t]);
-    if (k >= 0) {
-      atomicAdd(&cnt[k], 1);
-      atomicMin(&first[k], t);
-    } else if (k == -2) {
-      atomicAdd(&bad, 1);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int cnt[4] = {0, 0, 0, 0}, first[4] = {0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF}, bad = 0;
+  for (int b = t0; b < t1; b += kPlanThreads) {        // wave-uniform trip count
+    const int t = b + threadIdx.x;
+    const int k = t < t1 ? tier_slot(t_of[t]) : -1;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint64_t m = __builtin_amdgcn_ballot_w64(k == kk);
+      cnt[kk] += __builtin_popcountll(m);
+      if (m) first[kk] = min(first[kk], b + 64 * wave + (int)__builtin_ctzll(m));
     }
+    bad += __builtin_popcountll(__builtin_amdgcn_ballot_w64(k == -2));
+  }
+  if (lane == 0) {
+    for (int kk = 0; kk < 4; ++kk) { wc[wave][kk] = cnt[kk]; wf[wave][kk] = first[kk]; }
+    wbad[wave] = bad;
   }
   __syncthreads();
+  if (threadIdx.x < 4) {
+    int n = 0, f = 0x7FFFFFFF;
+    for (int w = 0; w < kPlanThreads / 64; ++w) { n += wc[w][threadIdx.x]; f = min(f, wf[w][threadIdx.x]); }
+    int32_t* r = ch_rec(a, sh, c);
+    r[kChCnt + threadIdx.x] = n;
+    r[kChFirst + threadIdx.x] = f;
+  }
   if (threadIdx.x == 0) {
-    int32_t* rec = a.work + (int64_t)sh * kRec;
+    int nb = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) nb += wbad[w];
+    if (nb) atomicAdd(a.totals + 2, nb);
+  }
+}
+
+__global__ __launch_bounds__(1024) void plan_scan_kernel(PlanLaunch a) {
+  // per (sequence, head): chunk rank bases, counts, first index, tier order, rows
+  for (int sh = threadIdx.x; sh < a.num_sh; sh += blockDim.x) {
+    int cnt[4] = {0, 0, 0, 0}, first[4] = {0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF};
+    for (int c = 0; c < a.nchunks; ++c) {
+      int32_t* r = ch_rec(a, sh, c);
+      for (int k = 0; k < 4; ++k) {
+        const int n = r[kChCnt + k];
+        r[kChCnt + k] = cnt[k];                          // exclusive rank base of the chunk
+        cnt[k] += n;
+        first[k] = min(first[k], r[kChFirst + k]);
+      }
+    }
+    int32_t* rec = sh_rec(a, sh);
     int order = 0, n_runs = 0, rows = 0;
     bool used[4] = {false, false, false, false};
-    for (int r = 0; r < 4; ++r) {               // tiers by first appearance
+    for (int q = 0; q < 4; ++q) {                        // tiers by first appearance
       int best = -1;
       for (int k = 0; k < 4; ++k)
         if (!used[k] && cnt[k] > 0 && (best < 0 || first[k] < first[best])) best = k;
@@ -85,30 +127,27 @@ __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(PlanLaunch a) 
       ++n_runs;
       rows += (cnt[best] + 15) / 16;
     }
-    for (int r = n_runs; r < 4; ++r) order |= 0xF << (4 * r);
+    for (int q = n_runs; q < 4; ++q) order |= 0xF << (4 * q);
     for (int k = 0; k < 4; ++k) { rec[kCnt + k] = cnt[k]; rec[kFirst + k] = first[k]; }
     rec[kRows] = rows;
     rec[kOrder] = order;
-    if (bad) atomicAdd(a.totals + 2, bad);
   }
-}
-
-__global__ void plan_scan_kernel(PlanLaunch a) {
+  __syncthreads();
   if (threadIdx.x != 0) return;
   int64_t off = 0;
   int row = 0;
   for (int sh = 0; sh < a.num_sh; ++sh) {
-    int32_t* rec = a.work + (int64_t)sh * kRec;
+    int32_t* rec = sh_rec(a, sh);
     rec[kRowStart] = row;
     a.row_start[sh] = row;
     row += rec[kRows];
-    for (int r = 0; r < 4; ++r) {
-      const int k = (rec[kOrder] >> (4 * r)) & 0xF;
-      if (k == 0xF) { rec[kRunStart + r] = -1; continue; }
+    for (int q = 0; q < 4; ++q) {
+      const int k = (rec[kOrder] >> (4 * q)) & 0xF;
+      if (k == 0xF) { rec[kRunStart + q] = -1; continue; }
       const int n = rec[kCnt + k], pages = (n + 15) / 16, last = n - 16 * (pages - 1);
       const int64_t start = place(off, k);
-      if (start > 0x7FFFFF00LL) { atomicAdd(a.totals + 3, 1); rec[kRunStart + r] = 0; continue; }
-      rec[kRunStart + r] = (int32_t)start;
+      if (start > 0x7FFFFF00LL) { atomicAdd(a.totals + 3, 1); rec[kRunStart + q] = 0; continue; }
+      rec[kRunStart + q] = (int32_t)start;
       off = start + (int64_t)(pages - 1) * align16(page_bytes(k, 16, a.dh)) + page_bytes(k, last, a.dh);
     }
   }
@@ -119,32 +158,36 @@ __global__ void plan_scan_kernel(PlanLaunch a) {
 }
 
 __global__ __launch_bounds__(kPlanThreads) void plan_fill_kernel(PlanLaunch a) {
-  __shared__ int page0[4], run_start[4], base[4], wsum[kPlanThreads / 64][4];
-  const int sh = blockIdx.x, s = sh / a.num_kv;
-  const int32_t* rec = a.work + (int64_t)sh * kRec;
+  __shared__ int page0[4], npages[4], run_start[4], base[4], wsum[kPlanThreads / 64][4];
+  const int sh = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks, s = sh / a.num_kv;
+  const int32_t* rec = sh_rec(a, sh);
   const int row0 = rec[kRowStart];
-  if (threadIdx.x == 0) {
-    int p = 0;
-    for (int k = 0; k < 4; ++k) page0[k] = -1;
-    for (int r = 0; r < 4; ++r) {
-      const int k = (rec[kOrder] >> (4 * r)) & 0xF;
-      if (k == 0xF) break;
-      page0[k] = p;
-      run_start[k] = rec[kRunStart + r];
-      p += (rec[kCnt + k] + 15) / 16;
-    }
-    for (int k = 0; k < 4; ++k) base[k] = 0;
-  }
-  __syncthreads();
-  // page rows: tier, count, pointer-table row, (seq, head), V slot; slots padded with -1
   const int rows = rec[kRows];
   if (row0 < 0 || row0 + rows > a.max_rows) return;       // outputs too small: nothing is written
-  for (int j = threadIdx.x; j < rows; j += kPlanThreads) {
+  if (threadIdx.x == 0) {
+    int p = 0;
+    for (int k = 0; k < 4; ++k) { page0[k] = -1; npages[k] = 0; }
+    for (int q = 0; q < 4; ++q) {
+      const int k = (rec[kOrder] >> (4 * q)) & 0xF;
+      if (k == 0xF) break;
+      page0[k] = p;
+      npages[k] = (rec[kCnt + k] + 15) / 16;
+      run_start[k] = rec[kRunStart + q];
+      p += npages[k];
+    }
+    const int32_t* cr = ch_rec(a, sh, c);
+    for (int k = 0; k < 4; ++k) base[k] = cr[kChCnt + k];
+  }
+  __syncthreads();
+  // this chunk's share of the page rows: tier, count, pointer-table row,
+  // (seq, head), V slot; the slots past a page's count are padding (-1)
+  const int j0 = (int)((int64_t)rows * c / a.nchunks), j1 = (int)((int64_t)rows * (c + 1) / a.nchunks);
+  for (int j = j0 + (int)threadIdx.x; j < j1; j += kPlanThreads) {
     int k = 0;
     for (int kk = 0; kk < 4; ++kk)
-      if (page0[kk] >= 0 && j >= page0[kk] && j < page0[kk] + (rec[kCnt + kk] + 15) / 16) k = kk;
-    const int i = j - page0[k], n_k = rec[kCnt + k];
-    const int n = min(16, n_k - 16 * i);
+      if (page0[kk] >= 0 && j >= page0[kk] && j < page0[kk] + npages[kk]) k = kk;
+    const int i = j - page0[k];
+    const int n = min(16, rec[kCnt + k] - 16 * i);
     const int64_t off = (int64_t)run_start[k] + (int64_t)i * align16(page_bytes(k, 16, a.dh));
     const int row = row0 + j;
     a.tier[row] = slot_tier(k);
@@ -163,21 +206,20 @@ __global__ __launch_bounds__(kPlanThreads) void plan_fill_kernel(PlanLaunch a) {
     a.ptable[3 * (int64_t)row] = (int32_t)off;
     a.ptable[3 * (int64_t)row + 1] = (int32_t)th;
     a.ptable[3 * (int64_t)row + 2] = (int32_t)rd;
-    for (int q = 0; q < 16; ++q) {
+    for (int q = n; q < 16; ++q) {
       a.tokens[(int64_t)row * 16 + q] = -1;
       a.positions[(int64_t)row * 16 + q] = -1;
       if (a.src_rows) a.src_rows[(int64_t)row * 16 + q] = -1;
     }
   }
-  __syncthreads();
-  // each kept token's rank within its tier -> (page, slot)
-  const int L = a.lens[s];
+  // each kept token of the chunk: rank within its tier -> (page, slot)
+  const int L = min(a.lens[s], a.max_len), t0 = c * kPlanChunk, t1 = min(L, t0 + kPlanChunk);
   const uint8_t* t_of = a.tier_of + (int64_t)sh * a.tier_stride;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t rb = a.row_base ? a.row_base[sh] : 0;
-  for (int c0 = 0; c0 < L; c0 += kPlanThreads) {
-    const int t = c0 + threadIdx.x;
-    const int k = t < L ? tier_slot(t_of[t]) : -1;
+  for (int b0 = t0; b0 < t1; b0 += kPlanThreads) {
+    const int t = b0 + threadIdx.x;
+    const int k = t < t1 ? tier_slot(t_of[t]) : -1;
     int below = 0;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -201,13 +243,22 @@ __global__ __launch_bounds__(kPlanThreads) void plan_fill_kernel(PlanLaunch a) {
   }
 }
 
-int launch_plan(const PlanLaunch& L, int phase, hipStream_t stream) {
-  if (L.num_sh <= 0) return 0;
+int64_t plan_work_ints(int num_sh, int max_len) {
+  const int64_t nch = max_len <= 0 ? 1 : (max_len + kPlanChunk - 1) / kPlanChunk;
+  return (int64_t)num_sh * kRec + (int64_t)num_sh * nch * kChRec;
+}
+
+int launch_plan(const PlanLaunch& L0, int phase, hipStream_t stream) {
+  if (L0.num_sh <= 0) return 0;
+  PlanLaunch L = L0;
+  L.nchunks = L.max_len <= 0 ? 1 : (L.max_len + kPlanChunk - 1) / kPlanChunk;
+  const int64_t grid = (int64_t)L.num_sh * L.nchunks;
+  if (grid > 0x7FFFFFFF) return -1;
   if (phase == 0) {
-    hipLaunchKernelGGL(plan_count_kernel, dim3(L.num_sh), dim3(kPlanThreads), 0, stream, L);
-    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(64), 0, stream, L);
+    hipLaunchKernelGGL(plan_count_kernel, dim3((unsigned)grid), dim3(kPlanThreads), 0, stream, L);
+    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, stream, L);
   } else {
-    hipLaunchKernelGGL(plan_fill_kernel, dim3(L.num_sh), dim3(kPlanThreads), 0, stream, L);
+    hipLaunchKernelGGL(plan_fill_kernel, dim3((unsigned)grid), dim3(kPlanThreads), 0, stream, L);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -42,9 +42,10 @@ SIGNATURES = {
     "sphkv_logits_lut": (ctypes.c_int, [P, P, P, P, I64, P, P, P, P, I32, I32, I32, I32, I32, I32, I32,
                                         I32, F32, I32, P]),
     "sphkv_omega_ema": (ctypes.c_int, [P, P, I64, I64, P, P, I32, I32, I32, F32, P]),
-    "sphkv_plan_pages_count": (ctypes.c_int, [P, I64, P, I32, I32, I32, P, P, P, P]),
-    "sphkv_plan_pages_fill": (ctypes.c_int, [P, I64, P, P, I64, P, I32, I32, I32, P, I32, P, P, P, P, P, P, P, P,
-                                             P]),
+    "sphkv_plan_pages_work_ints": (I64, [I32, I32, I32]),
+    "sphkv_plan_pages_count": (ctypes.c_int, [P, I64, P, I32, I32, I32, I32, P, I64, P, P, P]),
+    "sphkv_plan_pages_fill": (ctypes.c_int, [P, I64, P, P, I64, P, I32, I32, I32, I32, P, I32, P, P, P, P, P, P, P,
+                                             P, P]),
     "sphkv_build_layer_pool": (ctypes.c_int, [P, P, I64, P, I64, P, I32, I32, P, P, P, P, I64, I32, I32, I32,
                                               P]),
 }

@@ -352,7 +352,7 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
     (spherical_kv_pipeline.py:1146-1228) on the GPU.
 
     tier_of: uint8 [num_seqs*num_kv, L_max] tier id per token (row s*num_kv+h);
-    lens: int32 [num_seqs]; positions: int32 [num_seqs, L_max] or None (token
+    lens: int32 [num_seqs], each <= L_max; positions: int32 [num_seqs, L_max] or None (token
     index); row_base: int64 [num_seqs*num_kv] K row of each (seq, head)'s
     token 0, or None (no src_rows).  One host synchronisation (the totals)."""
     dev = tier_of.device
@@ -370,17 +370,22 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
         if tuple(row_base.shape) != (num_sh,):
             raise ValueError("row_base must be [num_seqs*num_kv]")
     lib = load()
-    work = torch.empty(max(num_sh, 1) * 16, dtype=torch.int32, device=dev)
+    max_len = int(tier_of.shape[1])
+    nw = lib.sphkv_plan_pages_work_ints(num_seqs, int(num_kv), max_len)
+    if nw < 0:
+        raise ValueError("bad planner sizes")
+    work = torch.empty(max(nw, 1), dtype=torch.int32, device=dev)
     row_start = torch.zeros(num_sh + 1, dtype=torch.int32, device=dev)
     totals = torch.zeros(4, dtype=torch.int32, device=dev)
     rc = lib.sphkv_plan_pages_count(tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), num_seqs, int(num_kv),
-                                    int(dh), work.data_ptr(), row_start.data_ptr(), totals.data_ptr(), _stream())
+                                    max_len, int(dh), work.data_ptr(), work.numel(), row_start.data_ptr(),
+                                    totals.data_ptr(), _stream())
     check(rc, "sphkv_plan_pages_count")
     rows, nbytes, bad, ovf = (int(x) for x in totals.cpu())
     if bad:
         raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")
     if nbytes < 0 or ovf:
-        raise ValueError("page byte pool exceeds int32 offsets")
+        raise ValueError("a sequence length exceeds tier_of's width, or the byte pool exceeds int32 offsets")
     i32 = dict(dtype=torch.int32, device=dev)
     out = dict(tier=torch.empty(rows, **i32), count=torch.empty(rows, **i32), ptable=torch.empty((rows, 3), **i32),
                seq_head=torch.empty(rows, **i32), vslot=torch.empty(rows, **i32),
@@ -388,7 +393,7 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
                src_rows=None if row_base is None else torch.empty((rows, 16), dtype=torch.int64, device=dev))
     rc = lib.sphkv_plan_pages_fill(
         tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), _ptr(positions),
-        0 if positions is None else positions.stride(0), _ptr(row_base), num_seqs, int(num_kv), int(dh),
+        0 if positions is None else positions.stride(0), _ptr(row_base), num_seqs, int(num_kv), max_len, int(dh),
         work.data_ptr(), rows, out["tier"].data_ptr(), out["count"].data_ptr(), out["ptable"].data_ptr(),
         out["seq_head"].data_ptr(), out["vslot"].data_ptr(), out["tokens"].data_ptr(), out["positions"].data_ptr(),
         _ptr(out["src_rows"]), _stream())
