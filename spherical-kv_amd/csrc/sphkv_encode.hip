@@ -1,7 +1,7 @@
 // Fused encode + bitpack + page build + V placement (gfx950).
 //
-// One wave per page.  For a compressed page, lane l owns token t = l % 16 and
-// the groups gi = l/16 + 4k.  Per (token, group) it reproduces the torch CPU
+// One wave per four consecutive pages, one lane per token; the codebook of a
+// (tier, kv head) is read as scalar operands.  Per (token, group) it reproduces the torch CPU
 // operation order of _encode_keys_with_codebooks
 // (spherical_kv_pipeline.py:1136-1144) so that radii and codes are bit-exact:
 //   r   = sqrtf(sum over 8 lanes of fmaf(x, x, .) chains, lanes summed in order)
@@ -68,169 +68,264 @@ __device__ __forceinline__ float torch_norm(const float* x, int g) {
   return __builtin_sqrtf(b);  // correctly rounded expansion (v_sqrt_f32 alone is not)
 }
 
+typedef const float __attribute__((address_space(4)))* cb_ptr;   // read through the scalar cache
+
+constexpr int kEncWaves = 4;       // waves per workgroup
+constexpr int kEncPages = 4;       // pages per wave: one lane per token of four pages
+constexpr int kEncMaxG = 8;        // groups per token (dh / g) held in LDS
+
 template <int DH>
-__global__ __launch_bounds__(256) void encode_pages_kernel(EncodeArgs a) {
-  __shared__ uint8_t stage[4][512];
-  __shared__ int32_t codes_s[4][kTile * 8];
+struct EncodeLds {
+  float r[kEncWaves][kEncPages * kTile][kEncMaxG];      // radius of (token, group)
+  int32_t code[kEncWaves][kEncPages * kTile][kEncMaxG];  // code of (token, group)
+  uint8_t stage[kEncWaves][512];                        // page image
+  _Float16 vt[kEncWaves][DH * kTile];                   // V page, dim-major
+};
+
+// Nearest centroid of one (token, group) against the codebook rows cbg[c * GG ..]
+// (wave-uniform, so every centroid coordinate is a scalar operand): the fmaf
+// chain over i of torch's batched path, or its separate multiply and add when
+// the page is small (N*g*C < 400); first index of the maximum, codes scored in
+// ascending order.
+template <int GG, bool NAIVE>
+__device__ __forceinline__ float code_sim(const float* dir, const float* w) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < GG; ++i) {
+    if (NAIVE) s = __fadd_rn(s, __fmul_rn(dir[i], w[i]));
+    else s = __builtin_fmaf(dir[i], w[i], s);
+  }
+  return s;
+}
+
+// Codes are scored in batches of NB rows (NB * GG = 64 floats, the scalar
+// registers one batch holds): scalar loads return in any order, so a batch's
+// rows are waited for together and their NB chains run side by side.
+template <int GG, bool NAIVE>
+__device__ __forceinline__ int argmax_codes(const float* dir, cb_ptr cbg, int C) {
+  constexpr int NB = 64 / GG;
+  float best_sim = 0.f;
+  int best = 0;
+  for (int c = 0; c < C; c += NB) {
+    float w[NB][GG];
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+#pragma unroll
+      for (int i = 0; i < GG; ++i) w[q][i] = cbg[(c + q) * GG + i];
+    float sim[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) sim[q] = code_sim<GG, NAIVE>(dir, w[q]);
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+      if (c + q == 0 || sim[q] > best_sim) { best_sim = sim[q]; best = c + q; }
+  }
+  return best;
+}
+
+// Radius (torch_norm) and code of the group of GG values at element kofs of K.
+template <int GG>
+__device__ __forceinline__ void encode_group(const EncodeArgs& a, int64_t kofs, bool naive, cb_ptr cbg, int C,
+                                             float& r_out, int& code_out) {
+  float x[GG];
+  if (a.k_is_fp32) {
+    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(a.k) + kofs);
+#pragma unroll
+    for (int i = 0; i < GG / 4; ++i) {
+      const float4 v4 = src[i];
+      x[4 * i] = v4.x; x[4 * i + 1] = v4.y; x[4 * i + 2] = v4.z; x[4 * i + 3] = v4.w;
+    }
+  } else {
+    const half8* src = reinterpret_cast<const half8*>(static_cast<const __half*>(a.k) + kofs);
+#pragma unroll
+    for (int i = 0; i < GG / 8; ++i) {
+      const half8 hv = src[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)hv[e];
+    }
+  }
+  const float r = torch_norm(x, GG);
+  const float den = __fadd_rn(r, 1e-8f);
+  float dir[GG];
+#pragma unroll
+  for (int i = 0; i < GG; ++i) dir[i] = __fdiv_rn(x[i], den);
+  r_out = r;
+  code_out = naive ? argmax_codes<GG, true>(dir, cbg, C) : argmax_codes<GG, false>(dir, cbg, C);
+}
+
+// One wave per four consecutive pages (one lane per token).  The radius and
+// code of every (token, group) are computed with the codebook of a
+// (tier, kv head) as scalar operands: the lanes whose page shares the first
+// unhandled page's (tier, head) are encoded together, so four pages of one
+// run take one pass.  Then each page is built in LDS (header, scales,
+// LSB-first codes, int8 radius codes; pagebuilder.py:8-33) and stored, its V
+// rows placed dim-major, or, for a dense page, its fp16 K rows copied.
+template <int DH>
+__global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs a) {
+  __shared__ EncodeLds<DH> sm;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  const int p = blockIdx.x * 4 + wave;
-  if (p >= a.num_pages) return;
+  const int pw = (blockIdx.x * kEncWaves + wave) * kEncPages;   // this wave's first page
+  if (pw >= a.num_pages) return;                                  // waves never wait for each other
 
-  const int tid = a.tier[p];
-  const int n = min(max(a.count[p], 0), kTile);
-  const int64_t page_off = a.ptable[3 * p];
-  const int64_t th_off = a.ptable[3 * p + 1];
-  const int64_t vs = a.vslot[p];
-  const int t = lane & 15;
-  const int gs = lane >> 4;
-  const bool tok_ok = t < n;
-  int64_t row = tok_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
-  if (row >= a.num_src_rows) row = -1;
+  // ---- this lane's token: page slot j = lane / 16, token t = lane % 16 ----
+  {
+    const int j = lane >> 4, t = lane & 15;
+    const int p = pw + j;
+    const bool p_ok = p < a.num_pages;
+    const int tid_l = p_ok ? a.tier[p] : 0;
+    const int n_l = p_ok ? min(max(a.count[p], 0), kTile) : 0;
+    const int head_l = p_ok ? a.seq_head[p] % a.num_kv : 0;
+    int64_t row = (p_ok && t < n_l) ? a.src_rows[(int64_t)p * kTile + t] : -1;
+    if (row >= a.num_src_rows) row = -1;
+    const bool comp_l = tid_l >= 1 && tid_l <= 3;
+    uint64_t todo = __builtin_amdgcn_ballot_w64(comp_l);
+    while (todo) {
+      const int lead = (int)__builtin_ctzll(todo);                 // first lane not yet encoded
+      const int tid = uniform(__builtin_amdgcn_readlane(tid_l, lead));
+      const int h = uniform(__builtin_amdgcn_readlane(head_l, lead));
+      const bool mine = comp_l && tid_l == tid && head_l == h;
+      todo &= ~__builtin_amdgcn_ballot_w64(mine);
+      const int g = uniform(tier_g(tid)), C = uniform(tier_C(tid)), G = DH / g;
+      const uint64_t cba = (uint64_t)(a.cb[tid] + (int64_t)h * G * C * g);
+      const cb_ptr cbh = (cb_ptr)(((uint64_t)(uint32_t)uniform((int)(cba >> 32)) << 32) |
+                                  (uint32_t)uniform((int)(uint32_t)cba));
+      if (mine) {
+        const bool naive = n_l * g * C < 400;                     // torch's own small-bmm loop
+        for (int gi = 0; gi < G; ++gi) {
+          float r = 0.f;
+          int code = 0;
+          if (row >= 0) {
+            if (g == 16) encode_group<16>(a, row * DH + gi * 16, naive, cbh + gi * C * 16, C, r, code);
+            else encode_group<32>(a, row * DH + gi * 32, naive, cbh + gi * C * 32, C, r, code);
+          }
+          sm.r[wave][lane][gi] = r;
+          sm.code[wave][lane][gi] = code;
+        }
+      }
+    }
+  }
+  wave_lds_sync();
 
-  // ---- V placement, dim-major: element (token k, dim d) of page vs at half
-  //      d * 16 + k, so one dim's 16 tokens are 32 contiguous bytes ---------
-  if (vs >= 0 && vs < a.num_vpages) {
-    constexpr int DPL = DH / 64;  // dims per lane
-    for (int dd = 0; dd < DPL; ++dd) {
-      const int d = lane + 64 * dd;
-      half8 h[2];
-      for (int tok = 0; tok < kTile; ++tok) {
-        int64_t rr = -1;
-        if (tok < n) rr = a.src_rows[(int64_t)p * kTile + tok];
-        _Float16 val = (_Float16)0.f;
+  // ---- per page: V placement, then the page image ------------------------
+  uint8_t* st = sm.stage[wave];
+  _Float16* vt = sm.vt[wave];
+  const int t = lane & 15, gs = lane >> 4;
+  for (int j = 0; j < kEncPages; ++j) {
+    const int p = pw + j;
+    if (p >= a.num_pages) break;
+    const int tid = a.tier[p];
+    const int n = min(max(a.count[p], 0), kTile);
+    const int64_t page_off = a.ptable[3 * p];
+    const int64_t th_off = a.ptable[3 * p + 1];
+    const int64_t vs = a.vslot[p];
+    const bool tok_ok = t < n;
+
+    // V: lane (token t, quarter gs) loads DH / 4 dims of its row into LDS
+    // dim-major (element (token k, dim d) at d * 16 + k), then each lane
+    // stores whole 32-byte dim rows
+    if (vs >= 0 && vs < a.num_vpages) {
+      int64_t vr = tok_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
+      if (vr >= a.num_src_rows) vr = -1;
+      constexpr int QD = DH / 4;
+#pragma unroll
+      for (int c8 = 0; c8 < QD / 8; ++c8) {
+        const int d0 = gs * QD + c8 * 8;
+        half8 hv;
+        if (vr >= 0) {
+          hv = *reinterpret_cast<const half8*>(a.v + vr * DH + d0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hv[e] = (_Float16)0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(d0 + e) * kTile + t] = hv[e];
+      }
+      wave_lds_sync();
+      half8* dst = reinterpret_cast<half8*>(a.v_pool + vs * DH * kTile);
+      for (int i = lane; i < DH * kTile / 8; i += kWave) dst[i] = *reinterpret_cast<const half8*>(vt + 8 * i);
+      wave_lds_sync();
+    }
+
+    if (tid == kDenseTier) {
+      // header: tier id, count, six zero bytes; payload fp16 [n, DH]
+      if (lane < 8 && page_off + 8 <= a.pages_bytes)
+        a.pages[page_off + lane] = lane == 0 ? (uint8_t)kDenseTier : (lane == 1 ? (uint8_t)n : 0);
+      for (int i = lane; i < n * DH / 8; i += kWave) {
+        const int tt = i / (DH / 8), c8 = i % (DH / 8);
+        int64_t rr = a.src_rows[(int64_t)p * kTile + tt];
+        half8 hv;
         if (rr >= 0 && rr < a.num_src_rows) {
-          __half hv = a.v[rr * DH + d];
-          val = *reinterpret_cast<_Float16*>(&hv);
-        }
-        h[tok >> 3][tok & 7] = val;
-      }
-      half8* dst = reinterpret_cast<half8*>(a.v_pool + vs * DH * kTile + d * kTile);
-      dst[0] = h[0];
-      dst[1] = h[1];
-    }
-  }
-
-  if (tid == kDenseTier) {
-    // header: tier id, count, six zero bytes; payload fp16 [n, DH]
-    if (lane < 8 && page_off + 8 <= a.pages_bytes)
-      a.pages[page_off + lane] = lane == 0 ? (uint8_t)kDenseTier : (lane == 1 ? (uint8_t)n : 0);
-    for (int i = lane; i < n * DH / 8; i += kWave) {
-      const int tt = i / (DH / 8), c8 = i % (DH / 8);
-      int64_t rr = a.src_rows[(int64_t)p * kTile + tt];
-      half8 hv;
-      if (rr >= 0 && rr < a.num_src_rows) {
-        if (a.k_is_fp32) {
-          const float* src = static_cast<const float*>(a.k) + rr * DH + c8 * 8;
-          for (int j = 0; j < 8; ++j) hv[j] = (_Float16)src[j];
+          if (a.k_is_fp32) {
+            const float* src = static_cast<const float*>(a.k) + rr * DH + c8 * 8;
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)src[e];
+          } else {
+            hv = *reinterpret_cast<const half8*>(static_cast<const __half*>(a.k) + rr * DH + c8 * 8);
+          }
         } else {
-          hv = *reinterpret_cast<const half8*>(static_cast<const __half*>(a.k) + rr * DH + c8 * 8);
+          for (int e = 0; e < 8; ++e) hv[e] = (_Float16)0.f;
         }
-      } else {
-        for (int j = 0; j < 8; ++j) hv[j] = (_Float16)0.f;
+        const int64_t dst = th_off + ((int64_t)tt * DH + c8 * 8) * 2;
+        if (dst + 16 <= a.pages_bytes) *reinterpret_cast<half8*>(a.pages + dst) = hv;
       }
-      const int64_t dst = th_off + ((int64_t)tt * DH + c8 * 8) * 2;
-      if (dst + 16 <= a.pages_bytes) *reinterpret_cast<half8*>(a.pages + dst) = hv;
+      continue;
     }
-    return;
-  }
-  if (tid < 1 || tid > 3) return;
+    if (tid < 1 || tid > 3) continue;
 
-  const int g = tier_g(tid), b = tier_b(tid), C = tier_C(tid);
-  const int G = DH / g;
-  const int h = a.seq_head[p] % a.num_kv;
-  const float* cbh = a.cb[tid] + (int64_t)h * G * C * g;
-  const bool naive = n * g * C < 400;  // torch's own small-bmm loop
-  uint8_t* st = stage[wave];
-  int32_t* cs = codes_s[wave];
-
-  float rr_[2];
-  int best_[2];
-  const int nk = (G + 3) / 4;  // groups per lane (2 for g=16, 1 for g=32 at DH=128)
-  for (int k = 0; k < 2; ++k) {
-    rr_[k] = 0.f;
-    best_[k] = 0;
-    if (k >= nk) break;
-    const int gi = gs + 4 * k;
-    if (gi >= G || row < 0) continue;
-    float x[32];
-    load_group<DH>(a, row, gi * g, g, x);
-    const float r = torch_norm(x, g);
-    const float den = __fadd_rn(r, 1e-8f);
-    float dir[32];
-    for (int i = 0; i < g; ++i) dir[i] = __fdiv_rn(x[i], den);
-    const float* cbg = cbh + (int64_t)gi * C * g;
-    float best_sim = 0.f;
-    int best = 0;
-    for (int c = 0; c < C; ++c) {
-      const float4* row4 = reinterpret_cast<const float4*>(cbg + c * g);
-      float s = 0.f;
-      for (int i4 = 0; i4 < g / 4; ++i4) {
-        const float4 w = row4[i4];
-        if (naive) {
-          s = __fadd_rn(s, __fmul_rn(dir[4 * i4], w.x));
-          s = __fadd_rn(s, __fmul_rn(dir[4 * i4 + 1], w.y));
-          s = __fadd_rn(s, __fmul_rn(dir[4 * i4 + 2], w.z));
-          s = __fadd_rn(s, __fmul_rn(dir[4 * i4 + 3], w.w));
-        } else {
-          s = __builtin_fmaf(dir[4 * i4], w.x, s);
-          s = __builtin_fmaf(dir[4 * i4 + 1], w.y, s);
-          s = __builtin_fmaf(dir[4 * i4 + 2], w.z, s);
-          s = __builtin_fmaf(dir[4 * i4 + 3], w.w, s);
-        }
+    const int g = tier_g(tid), b = tier_b(tid);
+    const int G = DH / g;
+    const int nk = (G + 3) / 4;                 // groups per lane (2 for g=16, 1 for g=32 at DH=128)
+    float rr_[2] = {0.f, 0.f};
+    int best_[2] = {0, 0};
+    for (int k = 0; k < nk; ++k) {
+      const int gi = gs + 4 * k;
+      if (gi < G) { rr_[k] = sm.r[wave][16 * j + t][gi]; best_[k] = sm.code[wave][16 * j + t][gi]; }
+    }
+    // radius scale per group: max over the page's tokens (lanes of one 16-row)
+    float scale_[2];
+    for (int k = 0; k < 2; ++k) {
+      float m = tok_ok ? rr_[k] : 0.f;
+      for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, shfl_xor(m, o));
+      scale_[k] = m;
+    }
+    const int nG = n * G;
+    const int tb = (nG * b + 7) / 8;
+    const int hdr = kHeaderBytes + 4 * G;
+    const int size = hdr + tb + nG;
+    int32_t* cs = reinterpret_cast<int32_t*>(vt);     // the page's codes, token-major
+    if (lane < kHeaderBytes) st[lane] = lane == 0 ? (uint8_t)tid : (lane == 1 ? (uint8_t)n : 0);
+    for (int k = 0; k < nk; ++k) {
+      const int gi = gs + 4 * k;
+      if (t == 0 && gi < G) *reinterpret_cast<float*>(st + kHeaderBytes + 4 * gi) = scale_[k];
+    }
+    for (int k = 0; k < nk; ++k) {
+      const int gi = gs + 4 * k;
+      if (!tok_ok || gi >= G) continue;
+      const int item = t * G + gi;
+      cs[item] = best_[k];
+      const float safe = scale_[k] < 1e-8f ? 1e-8f : scale_[k];
+      float qv = __fmul_rn(__fdiv_rn(rr_[k], safe), 127.0f);
+      qv = __builtin_rintf(qv);
+      qv = fminf(fmaxf(qv, -127.f), 127.f);
+      st[hdr + tb + item] = (uint8_t)(int8_t)(int)qv;
+      if (a.r_out) a.r_out[((int64_t)p * kTile + t) * (DH / 16) + gi] = rr_[k];
+      if (a.code_out) a.code_out[((int64_t)p * kTile + t) * (DH / 16) + gi] = best_[k];
+    }
+    wave_lds_sync();
+    // LSB-first bit stream (bitpacking.py:14-27): bit j of item i at bit i*b + j
+    for (int byte = lane; byte < tb; byte += kWave) {
+      uint32_t v = 0;
+      for (int bit = 0; bit < 8; ++bit) {
+        const int gb = byte * 8 + bit;
+        const int item = gb / b;
+        if (item < nG) v |= (uint32_t)((cs[item] >> (gb - item * b)) & 1) << bit;
       }
-      if (c == 0 || s > best_sim) { best_sim = s; best = c; }
+      st[hdr + byte] = (uint8_t)v;
     }
-    rr_[k] = r;
-    best_[k] = best;
+    wave_lds_sync();
+    if (page_off >= 0 && page_off + size <= a.pages_bytes)
+      for (int i = lane; i < size; i += kWave) a.pages[page_off + i] = st[i];
+    wave_lds_sync();
   }
-
-  // radius scale per group: max over the page's tokens (lanes of one 16-row)
-  float scale_[2];
-  for (int k = 0; k < 2; ++k) {
-    float m = tok_ok ? rr_[k] : 0.f;
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, shfl_xor(m, o));
-    scale_[k] = m;
-  }
-
-  const int nG = n * G;
-  const int tb = (nG * b + 7) / 8;
-  const int hdr = kHeaderBytes + 4 * G;
-  const int size = hdr + tb + nG;
-  // header + scales
-  if (lane < kHeaderBytes) st[lane] = lane == 0 ? (uint8_t)tid : (lane == 1 ? (uint8_t)n : 0);
-  for (int k = 0; k < nk; ++k) {
-    const int gi = gs + 4 * k;
-    if (t == 0 && gi < G) *reinterpret_cast<float*>(st + kHeaderBytes + 4 * gi) = scale_[k];
-  }
-  // codes to LDS, int8 radius codes into the page image
-  for (int k = 0; k < nk; ++k) {
-    const int gi = gs + 4 * k;
-    if (!tok_ok || gi >= G) continue;
-    const int item = t * G + gi;
-    cs[item] = best_[k];
-    const float safe = scale_[k] < 1e-8f ? 1e-8f : scale_[k];
-    float qv = __fmul_rn(__fdiv_rn(rr_[k], safe), 127.0f);
-    qv = __builtin_rintf(qv);
-    qv = fminf(fmaxf(qv, -127.f), 127.f);
-    st[hdr + tb + item] = (uint8_t)(int8_t)(int)qv;
-    if (a.r_out) a.r_out[((int64_t)p * kTile + t) * (DH / 16) + gi] = rr_[k];
-    if (a.code_out) a.code_out[((int64_t)p * kTile + t) * (DH / 16) + gi] = best_[k];
-  }
-  wave_lds_sync();
-  // LSB-first bit stream (bitpacking.py:14-27): bit j of item i at bit i*b + j
-  for (int byte = lane; byte < tb; byte += kWave) {
-    uint32_t v = 0;
-    for (int bit = 0; bit < 8; ++bit) {
-      const int gb = byte * 8 + bit;
-      const int item = gb / b;
-      if (item < nG) v |= (uint32_t)((cs[item] >> (gb - item * b)) & 1) << bit;
-    }
-    st[hdr + byte] = (uint8_t)v;
-  }
-  wave_lds_sync();
-  if (page_off >= 0 && page_off + size <= a.pages_bytes)
-    for (int i = lane; i < size; i += kWave) a.pages[page_off + i] = st[i];
 }
 
 int launch_encode(const EncodeLaunch& L, hipStream_t stream) {
@@ -241,7 +336,8 @@ int launch_encode(const EncodeLaunch& L, hipStream_t stream) {
   a.num_kv = L.num_kv; a.cb[0] = nullptr; a.cb[1] = L.cb1; a.cb[2] = L.cb2; a.cb[3] = L.cb3;
   a.pages = L.pages; a.pages_bytes = L.pages_bytes; a.v_pool = reinterpret_cast<__half*>(L.v_pool);
   a.num_vpages = L.num_vpages; a.r_out = L.r_out; a.code_out = L.code_out;
-  const dim3 grid((L.num_pages + 3) / 4), block(256);
+  const int per_block = kEncWaves * kEncPages;
+  const dim3 grid((L.num_pages + per_block - 1) / per_block), block(kEncWaves * 64);
   if (L.dh == 128) hipLaunchKernelGGL(encode_pages_kernel<128>, grid, block, 0, stream, a);
   else hipLaunchKernelGGL(encode_pages_kernel<64>, grid, block, 0, stream, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
