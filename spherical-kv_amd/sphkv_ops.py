@@ -170,20 +170,27 @@ class PagedPool:
     def allocate_device(plan: "DevicePlan", codebooks: Dict[int, np.ndarray], device="cuda",
                         rows_per_item: Optional[int] = None) -> "PagedPool":
         """A pool over a plan built on the GPU (plan_pages_gpu): the plan's
-        device arrays are used in place; its layout holds by construction."""
+        device arrays are used in place; its layout holds by construction.
+        Codebooks may be given as resident fp32 tensors (used in place)."""
         dev = torch.device(device)
         if rows_per_item is None:
             rows_per_item = auto_rows_per_item(plan.row_start, torch.cuda.get_device_properties(dev).multi_processor_count)
         work, ws = make_work(plan.row_start, rows_per_item)
-        cbs = {int(t): torch.as_tensor(np.ascontiguousarray(c, np.float32), device=dev) for t, c in codebooks.items()}
+        cbs = {}
+        for t, c in codebooks.items():
+            if isinstance(c, torch.Tensor) and c.device == dev and c.dtype == torch.float32 and c.is_contiguous():
+                cbs[int(t)] = c                       # already resident: used in place
+            else:
+                cbs[int(t)] = torch.as_tensor(np.ascontiguousarray(np.asarray(c), np.float32), device=dev)
         for tid, c in cbs.items():
             g, b = fmt.TIER_GEOMETRY[tid]
             if tuple(c.shape) != (plan.num_kv, plan.dh // g, 2 ** b, g):
                 raise ValueError(f"tier {tid} codebook shape {tuple(c.shape)}")
+        # every V slot of every page is written by encode_pages (zeros past a page's tokens)
         return PagedPool(
             plan=plan, pages=torch.zeros(plan.pages_bytes, dtype=torch.uint8, device=dev), ptable=plan.ptable,
             vslot=plan.vslot, positions=plan.positions,
-            v_pool=torch.zeros((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
+            v_pool=torch.empty((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
             codebooks=cbs, work=torch.as_tensor(work, device=dev), work_start=torch.as_tensor(ws, device=dev),
             tier=plan.tier, count=plan.count, seq_head=plan.seq_head)
 
