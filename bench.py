@@ -199,7 +199,8 @@ def bench_prefill(args, dev):
     into a fresh pool.  CPU baseline: the host planner plus the oracle's C
     encode / page build over the same tokens."""
     log(f"[bench] building config{args.config} workload for prefill paging")
-    wl = synth.make_decode_workload(args.config, layout="sequential")
+    wl = synth.make_encode_workload() if args.config == 3 else synth.make_decode_workload(args.config,
+                                                                                         layout="sequential")
     L_max = max(wl.lengths)
     t = np.zeros((len(wl.tier_of), L_max), np.uint8)
     for sh, arr in enumerate(wl.tier_of):
@@ -278,7 +279,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
+                    help="1, 2, 4, 5: decode configs; 3: the encode config (with --path prefill)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
@@ -307,6 +309,9 @@ def main():
     if args.path == "prefill":
         bench_prefill(args, dev)
         return
+    if args.config == 3:
+        print("bench.py: config 3 is the encode workload; use --path prefill --config 3", file=sys.stderr)
+        sys.exit(2)
 
     log(f"[bench] building config{args.config} workload")
     wl = synth.make_decode_workload(args.config, layout=args.layout)
