@@ -99,10 +99,13 @@ int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32
  * page-resident context and the missing fused_decode_ragged kernel's callers
  * (:1102-1125, :1865-1870).
  *
- *   work       host-computed work list: work int32 [num_items, 3] =
- *              (seq*num_kv + head, row_begin, row_end) with the items of one
- *              (seq, head) contiguous and in order, and at least one item
- *              (possibly empty) per (seq, head); work_start int32
+ *   work       host-computed work list: work int32 [num_items, 4] =
+ *              (seq*num_kv + head, first_row, end_row, stride): the item
+ *              covers rows first_row, first_row + stride, ... < end_row
+ *              (stride >= 1; contiguous items use 1).  The items of one
+ *              (seq, head) are contiguous in the list, together cover each
+ *              of its rows once, and there is at least one item (possibly
+ *              empty) per (seq, head); work_start int32
  *              [num_seqs*num_kv + 1] = first item of each (seq, head).
  *   q          fp16 [num_seqs, num_kv*gqa, dh];  out fp16, same shape.
  *   workspace  device scratch of sphkv_decode_paged_workspace_bytes() bytes.

@@ -1,7 +1,9 @@
 // Angle-domain paged attention decode (gfx950).
 //
-// Work decomposition: one workgroup (kWaves waves) per work item = a
-// contiguous range of pointer-table rows of one (sequence, kv head).  The
+// Work decomposition: one workgroup (kWaves waves) per work item = the
+// pointer-table rows first, first + stride, ... (< end) of one (sequence, kv
+// head); the host interleaves a head's rows over its items (stride = the
+// head's item count), so every item holds the same mix of tiers.  The
 // workgroup stages that head's tier codebooks and the RoPE tables in LDS once;
 // each wave walks every kWaves-th page of the range with its own online-softmax
 // state; the states are merged in LDS and written as one (m, l, acc) partial.
@@ -365,9 +367,11 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int item = xcd_item(blockIdx.x, gridDim.x);
-  const int sh = a.work[3 * item];
-  const int rb = a.work[3 * item + 1];
-  const int re = min(a.work[3 * item + 2], a.num_rows);
+  const int sh = a.work[4 * item];
+  const int rb = a.work[4 * item + 1];
+  const int re = min(a.work[4 * item + 2], a.num_rows);
+  const int rstride = max(a.work[4 * item + 3], 1);   // rows between consecutive pages of the item
+  const int wstride = kWaves * rstride;                // rows between consecutive pages of a wave
   const int h = sh % a.num_kv;
   const int seq = sh / a.num_kv;
   const int t = lane & 15;
@@ -375,12 +379,12 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   uint8_t* st = smem + L::o_stage + wave * 512;
   _Float16* qr = reinterpret_cast<_Float16*>(smem + L::o_qr) + wave * L::qr_wave;   // [hi, lo][GQA][qrow]
 
-  int p = rb + wave;
+  int p = rb + wave * rstride;
   const Res rs = make_res(a);
   // ---- first pages' pointer-table rows, then the shared tables' loads ----
   RowLd rl_c = row_issue(rs, p, re, lane);
-  RowLd rl_n = row_issue(rs, p + kWaves, re, lane);
-  RowLd rl_2 = row_issue(rs, p + 2 * kWaves, re, lane);
+  RowLd rl_n = row_issue(rs, p + wstride, re, lane);
+  RowLd rl_2 = row_issue(rs, p + 2 * wstride, re, lane);
   // codebooks: every load of a thread is issued before its first LDS store
   constexpr int kT = kWaves * 64;
   constexpr int n4_1 = L::cb_n1 / 20 * 4, n4_2 = L::cb_n2 / 20 * 4, n4_3 = L::cb_n3 / 36 * 8;  // float4s
@@ -427,7 +431,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   load_v<DH>(a, row_c, lane, vreg);
   uint4 kd[NC];
   load_dense<DH>(rs, row_c, t, u, kd);
-  Row row_n = row_take(a, rl_n, p + kWaves, re);
+  Row row_n = row_take(a, rl_n, p + wstride, re);
   {
     int slot = 0;
 #pragma unroll
@@ -488,9 +492,9 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
     // ---- issue: row three pages ahead, stage/positions one page ahead -----
-    rl_issue = row_issue(rs, p + 3 * kWaves, re, lane);
+    rl_issue = row_issue(rs, p + 3 * wstride, re, lane);
     stg_n = load_stage(rs, row_n, lane);
-    pos_n = load_pos(rs, row_n, p + kWaves, t);
+    pos_n = load_pos(rs, row_n, p + wstride, t);
 
     // ---- this page's header (lane 0's 16 bytes of the stage) --------------
     const int rel = (int)(row_c.page_off & 15);
@@ -691,15 +695,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     wave_lds_sync();
 
     row_c = row_n;
-    row_n = row_take(a, rl_take, p + 2 * kWaves, re);
+    row_n = row_take(a, rl_take, p + 2 * wstride, re);
   };
   uint4 stg_b;
   int pos_b;
   RowLd rl_3;
-  for (; p < re; p += 2 * kWaves) {
+  for (; p < re; p += 2 * wstride) {
     step(p, stg_c, pos_c, stg_b, pos_b, rl_3, rl_2);
-    if (p + kWaves >= re) break;
-    step(p + kWaves, stg_b, pos_b, stg_c, pos_c, rl_2, rl_3);
+    if (p + wstride >= re) break;
+    step(p + wstride, stg_b, pos_b, stg_c, pos_c, rl_2, rl_3);
   }
 
   // ---- merge the waves' states in LDS, write this item's partial ----------

@@ -57,19 +57,31 @@ def auto_rows_per_item(row_start: np.ndarray, num_cus: int, slots_per_cu: int = 
     return rpi
 
 
-def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM):
-    """Split each (seq, head) row range into items of <= rows_per_item rows.
-    Returns (work int32 [n_items, 3], work_start int32 [num_sh + 1])."""
+def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM, interleave: bool = True):
+    """Split each (seq, head) row range [b, e) into n = ceil((e - b) /
+    rows_per_item) items of <= rows_per_item rows.  Returns (work int32
+    [n_items, 4] = (sh, first_row, end_row, stride), work_start int32
+    [num_sh + 1]).
+
+    interleave (default): item i takes rows b + i, b + i + n, ... -- a head's
+    rows are grouped by tier, so contiguous items would each hold one tier and
+    run at that tier's cost (dense pages load 4 KB of K more); interleaved
+    items all hold the head's tier mix.  Otherwise items are contiguous
+    ranges (stride 1)."""
     rs = np.asarray(row_start, np.int64)
     work, ws = [], [0]
     for sh in range(rs.shape[0] - 1):
         b, e = int(rs[sh]), int(rs[sh + 1])
         if e == b:
-            work.append((sh, b, b))          # empty context still writes its output
-        for r0 in range(b, e, rows_per_item):
-            work.append((sh, r0, min(e, r0 + rows_per_item)))
+            work.append((sh, b, b, 1))       # empty context still writes its output
+        n = -(-(e - b) // rows_per_item)
+        for i in range(n):
+            if interleave:
+                work.append((sh, b + i, e, n))
+            else:
+                work.append((sh, b + i * rows_per_item, min(e, b + (i + 1) * rows_per_item), 1))
         ws.append(len(work))
-    w = np.asarray(work, np.int32).reshape(-1, 3)
+    w = np.asarray(work, np.int32).reshape(-1, 4)
     return w, np.asarray(ws, np.int32)
 
 
@@ -118,7 +130,7 @@ class PagedPool:
     positions: torch.Tensor    # int32 [P, 16]
     v_pool: torch.Tensor       # fp16 [num_vpages, 16 * dh] (dim-major pages: [dh][16])
     codebooks: Dict[int, torch.Tensor]   # tier -> fp32 [num_kv, G, C, g]
-    work: torch.Tensor         # int32 [n_items, 3]
+    work: torch.Tensor         # int32 [n_items, 4] (sh, first_row, end_row, stride)
     work_start: torch.Tensor   # int32 [num_seqs*num_kv + 1]
     tier: torch.Tensor         # int32 [P]
     count: torch.Tensor        # int32 [P]

@@ -58,6 +58,20 @@ def test_decode_work_split_invariance(gpu):
     assert max_err(outs[0], outs[1]) < 2e-3 * 0.25 and max_err(outs[1], outs[2]) < 2e-3 * 0.25
 
 
+def test_decode_interleaved_and_contiguous_items_agree(gpu):
+    # the same pool decoded with interleaved (strided) and contiguous work
+    # items: only the order of the log-sum-exp merge differs
+    wl = synth.make_decode_workload(2, ctx_override=6000)
+    pool, cpu = pool_from_oracle(wl, gpu, rows_per_item=32)
+    w, ws = ops.make_work(wl.plan.row_start, 32, interleave=False)
+    pool2 = ops.PagedPool(**{**pool.__dict__, "work": torch.as_tensor(w, device=gpu),
+                             "work_start": torch.as_tensor(ws, device=gpu)})
+    a, b = _decode(pool, wl, gpu), _decode(pool2, wl, gpu)
+    want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+    assert max_err(a, want) <= 2e-3 and max_err(b, want) <= 2e-3
+    assert max_err(a, b) < 2e-3 * 0.25
+
+
 def test_decode_edge_cases(gpu):
     rng = np.random.default_rng(3)
     dh, num_kv, gqa = 128, 4, 4
