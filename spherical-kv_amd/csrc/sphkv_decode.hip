@@ -353,7 +353,11 @@ __device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8&
 
 template <int DH, int GQA>
 __global__ __launch_bounds__(decode_waves<GQA>() * 64)
-__attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() / 4))) void decode_kernel(DecodeArgs a) {
+__attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() / 4))) void decode_kernel(
+    const int32_t* __restrict__ work, int32_t num_items, DecodeArgs a) {
+  // work and num_items lead the argument list: the build preloads the first
+  // kernel-argument dwords into SGPRs, so the work item's load is issued at
+  // wave start instead of after two dependent argument loads
   constexpr int kWaves = decode_waves<GQA>();
   constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
   constexpr int NP = NC / 2;         // chunks holding the first RoPE half
@@ -366,12 +370,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  const int item = xcd_item(blockIdx.x, gridDim.x);
-  const int sh = a.work[4 * item];
-  const int rb = a.work[4 * item + 1];
-  const int re = min(a.work[4 * item + 2], a.num_rows);
-  const int rstride = max(a.work[4 * item + 3], 1);   // rows between consecutive pages of the item
+  const int item = xcd_item(blockIdx.x, num_items);
+  const int sh = work[4 * item];
+  const int rb = work[4 * item + 1];
+  const int re = min(work[4 * item + 2], a.num_rows);
+  const int rstride = max(work[4 * item + 3], 1);     // rows between consecutive pages of the item
   const int wstride = kWaves * rstride;                // rows between consecutive pages of a wave
+  // pages of this wave (rows rb + rstride (wave + kWaves k) < re)
+  const int npg = re > rb ? (re - rb + rstride - 1) / rstride : 0;
+  const int nwp = npg > wave ? (npg - wave + kWaves - 1) / kWaves : 0;
   const int h = sh % a.num_kv;
   const int seq = sh / a.num_kv;
   const int t = lane & 15;
@@ -477,6 +484,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     for (int hf = 0; hf < NHF; ++hf) acc[hs][hf] = (floatx4){0.f, 0.f, 0.f, 0.f};
   _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
 
+  int pages_done = 0;                                   // pages of this wave processed so far
   // One page of the pipeline.  The staging window and positions of the next
   // page are loaded into the other register set of a pair, and the pointer-
   // table rows into the other slot of a pair, so the loop (unrolled by two)
@@ -491,6 +499,17 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     asm volatile("" : "+v"(lane_v));
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
+    // ---- issue priority from this wave's share of pages still to do: a
+    //      SIMD serves its waves oldest first, so without it the youngest
+    //      wave would finish last, alone on its SIMD ---------------------------
+    {
+      const int left = nwp - pages_done;                                // pages left, this one included
+      const int lvl = 4 * left > 3 * nwp ? 3 : (2 * left > nwp ? 2 : (4 * left > nwp ? 1 : 0));
+      if (lvl >= 3) __builtin_amdgcn_s_setprio(3);
+      else if (lvl == 2) __builtin_amdgcn_s_setprio(2);
+      else if (lvl == 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     // ---- issue: row three pages ahead, stage/positions one page ahead -----
     rl_issue = row_issue(rs, p + 3 * wstride, re, lane);
     stg_n = load_stage(rs, row_n, lane);
@@ -696,6 +715,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 
     row_c = row_n;
     row_n = row_take(a, rl_take, p + 2 * wstride, re);
+    ++pages_done;
   };
   uint4 stg_b;
   int pos_b;
@@ -706,6 +726,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     step(p + wstride, stg_b, pos_b, stg_c, pos_c, rl_2, rl_3);
   }
 
+  __builtin_amdgcn_s_setprio(0);
   // ---- merge the waves' states in LDS, write this item's partial ----------
   constexpr int PS = partial_stride<DH, GQA>();
   __syncthreads();
@@ -720,29 +741,31 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
         for (int hf = 0; hf < NHF; ++hf) mrg[(wave * GQA + 4 * hs + i) * DH + 64 * hf + lane] = acc[hs][hf][i];
   if (hl < GQA && u == 0) { mrg_ml[(wave * GQA + hl) * 2] = m_run; mrg_ml[(wave * GQA + hl) * 2 + 1] = l_run; }
   __syncthreads();
+  // every output thread derives its head's wave weights 2^(m_w - M) itself
+  // (the kWaves reads of a head hit one LDS address each: broadcasts), so
+  // the merge is one LDS round trip instead of a serial pass per head
   float* part = a.partials + (int64_t)item * PS;
-  float* fw = mrg_ml + kWaves * GQA * 2;              // [GQA][kWaves] wave weights 2^(m_w - M)
-  if (threadIdx.x < GQA) {
-    const int hh = threadIdx.x;
-    float M = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mrg_ml[(w * GQA + hh) * 2]);
-    float Ls = 0.f;
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = mrg_ml[(w * GQA + hh) * 2];
-      const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-      fw[hh * kWaves + w] = f;
-      Ls += f * mrg_ml[(w * GQA + hh) * 2 + 1];
-    }
-    part[hh] = M;
-    part[GQA + hh] = Ls;
-  }
-  __syncthreads();
   for (int i = threadIdx.x; i < GQA * DH; i += kWaves * 64) {
     const int hh = i / DH, d = i % DH;
-    float A = 0.f;
+    float mw[kWaves];
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) A += fw[hh * kWaves + w] * mrg[(w * GQA + hh) * DH + d];
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = mrg_ml[(w * GQA + hh) * 2];
+      M = fmaxf(M, mw[w]);
+    }
+    float A = 0.f, Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = (mw[w] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
+      A += f * mrg[(w * GQA + hh) * DH + d];
+      Ls += f * mrg_ml[(w * GQA + hh) * 2 + 1];
+    }
     part[16 + hh * DH + d] = A;
+    if (d == 0) {
+      part[hh] = M;
+      part[GQA + hh] = Ls;
+    }
   }
 }
 
@@ -837,7 +860,8 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.log2_theta = __builtin_log2(L.rope_theta);
   if (L.num_items > 0) {
     if (phases & kPhasePartials)
-      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream, a);
+      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream,
+                         L.work, L.num_items, a);
     const int nsh = L.num_seqs * L.num_kv;
     if ((phases & kPhaseMerge) && nsh > 0)
       hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
