@@ -10,6 +10,11 @@ Infinity Cache (256 MB) is defeated by rotating through ROTATE independent
 copies of the KV pool (each ~80 MB).  Timing uses HIP events on the stream the
 kernels run on (torch's current stream), around exactly K steps.
 
+Before the W counted warmup steps, every path runs an untimed settle phase
+of the same step for at least SETTLE_S seconds: on a fresh process the GPU's
+clocks and translation caches take a few hundred steps to reach steady state
+(measured: 31.2, 28.8, 28.3 us/step over three consecutive 220-step rounds).
+
 Prints one JSON line (see the "roofline" and "cpu_baseline" objects).
 
 `--path modea` measures the Mode-A (LayerPool) decode instead, on the same
@@ -41,6 +46,18 @@ PEAK_HBM_GBPS = 8000.0
 METRIC = "µs/decode step + achieved HBM GB/s (compressed KV), 8B shape, 32K ctx, 1 GPU"
 ROTATE = 6
 COPY_BYTES = 256 << 20
+SETTLE_S = 0.3
+
+
+def settle(step_fn):
+    """Untimed: repeat step_fn(i) until SETTLE_S seconds of wall time have
+    passed (synchronising every 50 steps)."""
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(50):
+            step_fn(i)
+            i += 1
+        torch.cuda.synchronize()
 
 
 def log(msg):
@@ -163,6 +180,7 @@ def bench_modea(args, dev):
                                   w["kv_groups"], w["num_tiers"], mb, w["page_size"], w["dh"], w["G_max"],
                                   w["cb_max"], w["g_max"], w["sm_scale"], w["max_ctx"])
 
+    settle(step)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -278,7 +296,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="1, 2, 4, 5: decode configs; 3: the encode config (with --path prefill)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -324,6 +342,7 @@ def main():
     nbytes = fmt.decode_bytes(wl.plan)
     log(f"[bench] rows={wl.plan.num_rows} items={pool0.num_items} algorithmic bytes/step={nbytes}")
 
+    settle(lambda i: ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws))
     for i in range(args.warmup):
         ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
     torch.cuda.synchronize()
