@@ -62,6 +62,7 @@ struct DecodeArgs {
   float* partials;
   int32_t num_kv;
   int32_t num_rows;
+  int32_t num_sh;        // num_seqs * num_kv
   float scale_log2;      // sm_scale * log2(e)
   double log2_theta;
 };
@@ -371,10 +372,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int item = xcd_item(blockIdx.x, num_items);
-  const int sh = work[4 * item];
-  const int rb = work[4 * item + 1];
-  const int re = min(work[4 * item + 2], a.num_rows);
-  const int rstride = max(work[4 * item + 3], 1);     // rows between consecutive pages of the item
+  // the work list comes from the caller: an item naming no (seq, head) is
+  // empty, rows are clamped to the table and the stride to [1, num_rows]
+  // (so no row index below overflows and the page loop is bounded)
+  const int32_t* wi = work + 4 * item;
+  const bool item_ok = wi[0] >= 0 && wi[0] < a.num_sh;
+  const int sh = item_ok ? wi[0] : 0;
+  const int rb = max(wi[1], 0);
+  const int re = item_ok ? min(wi[2], a.num_rows) : 0;
+  const int rstride = min(max(wi[3], 1), max(a.num_rows, 1));   // rows between consecutive pages of the item
   const int wstride = kWaves * rstride;                // rows between consecutive pages of a wave
   // pages of this wave (rows rb + rstride (wave + kWaves k) < re)
   const int npg = re > rb ? (re - rb + rstride - 1) / rstride : 0;
@@ -778,7 +784,8 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 template <int DH, int GQA>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ partials,
                                                            const int32_t* __restrict__ work_start,
-                                                           int32_t num_kv, _Float16* __restrict__ out) {
+                                                           int32_t num_items, int32_t num_kv,
+                                                           _Float16* __restrict__ out) {
   constexpr int PS = partial_stride<DH, GQA>();
   constexpr int SL = GQA * DH < 128 ? GQA * DH : 128; // floats per output slice
   constexpr int NSL = (GQA * DH) / SL;                // slices per (seq, kv head)
@@ -787,7 +794,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   __shared__ float4 red_v[IL][32];
   __shared__ float red_m[IL][32], red_l[IL][32];
   const int sh = blockIdx.x / NSL, slice = blockIdx.x % NSL;
-  const int ib = work_start[sh], ni = work_start[sh + 1] - ib;
+  // item range of this (seq, head), clamped to the partials that exist
+  const int ib = min(max(work_start[sh], 0), num_items);
+  const int ni = min(max(work_start[sh + 1], ib), num_items) - ib;
   const int c = threadIdx.x & 31, il = threadIdx.x >> 5;
   const bool col_ok = 4 * c < SL;
   const int f0 = slice * SL + (col_ok ? 4 * c : 0);   // first float of this column in [GQA*DH]
@@ -855,7 +864,7 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.num_vpages = L.num_vpages; a.cb[0] = nullptr; a.cb[1] = L.cb1; a.cb[2] = L.cb2; a.cb[3] = L.cb3;
   a.work = L.work; a.work_start = L.work_start; a.q = reinterpret_cast<const _Float16*>(L.q);
   a.out = reinterpret_cast<_Float16*>(L.out); a.partials = L.partials;
-  a.num_kv = L.num_kv; a.num_rows = L.num_rows;
+  a.num_kv = L.num_kv; a.num_rows = L.num_rows; a.num_sh = L.num_seqs * L.num_kv;
   a.scale_log2 = L.sm_scale * 1.4426950408889634f;
   a.log2_theta = __builtin_log2(L.rope_theta);
   if (L.num_items > 0) {
@@ -865,7 +874,7 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
     const int nsh = L.num_seqs * L.num_kv;
     if ((phases & kPhaseMerge) && nsh > 0)
       hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
-                         dim3(256), 0, stream, L.partials, L.work_start, L.num_kv,
+                         dim3(256), 0, stream, L.partials, L.work_start, L.num_items, L.num_kv,
                          reinterpret_cast<_Float16*>(L.out));
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -72,6 +72,31 @@ def test_decode_interleaved_and_contiguous_items_agree(gpu):
     assert max_err(a, b) < 2e-3 * 0.25
 
 
+def test_decode_malformed_work_items_stay_in_bounds(gpu):
+    # work items naming no (seq, head), negative or past-the-end rows and
+    # absurd strides are clamped by the kernels: the call completes and the
+    # well-formed items' heads are decoded as before
+    wl = synth.make_decode_workload(2, ctx_override=3000)
+    pool, cpu = pool_from_oracle(wl, gpu)
+    ref = _decode(pool, wl, gpu)
+    w = pool.work.cpu().numpy().copy()
+    ws = pool.work_start.cpu().numpy()
+    bad = w.copy()
+    last = ws[-2]                                     # first item of the last (seq, head)
+    bad[last:, 0] = 1 << 30                           # names no (seq, head)
+    bad[last:, 1] = -(1 << 30)
+    bad[last:, 2] = 1 << 30
+    bad[last:, 3] = 1 << 30
+    p2 = ops.PagedPool(**{**pool.__dict__, "work": torch.as_tensor(bad, device=gpu)})
+    got = _decode(p2, wl, gpu)
+    gqa = wl.gqa
+    h_last = wl.plan.num_kv - 1
+    keep = np.ones(got.shape[1], bool)
+    keep[h_last * gqa:(h_last + 1) * gqa] = False
+    assert (got[:, keep] == ref[:, keep]).all()
+    assert np.isfinite(got).all()
+
+
 def test_decode_edge_cases(gpu):
     rng = np.random.default_rng(3)
     dh, num_kv, gqa = 128, 4, 4
