@@ -41,20 +41,32 @@ def _need(t: torch.Tensor, dtype, name: str, device=None):
 
 
 def auto_rows_per_item(row_start: np.ndarray, num_cus: int, slots_per_cu: int = 1) -> int:
-    """Rows per work item so that the items fill the chip in whole waves of
-    workgroups: about num_cus * slots_per_cu items (one 8-wave workgroup per
-    CU at the decode kernel's register budget), at least 8 rows per item."""
+    """Rows per work item.  When one item per CU can cover every (seq, head)
+    range, the smallest row count whose item total fits num_cus * slots_per_cu
+    (one workgroup per CU, all running at once; at least 8 rows).  When there
+    are more ranges than that (each needs an item of its own), about four
+    smaller items per CU, which the dispatcher balances as CUs free up."""
     rs = np.asarray(row_start, np.int64)
-    total = int(rs[-1] - rs[0])
+    lens = rs[1:] - rs[:-1]
+    total = int(lens.sum())
     target = max(1, num_cus * slots_per_cu)
-    rpi = max(8, -(-total // target))
-    # the per-head rounding adds up to one item per head: shrink until it fits
-    while rpi > 8:
-        n = int(np.sum(np.maximum(1, -(-(rs[1:] - rs[:-1]) // rpi))))
-        if n <= target or n > 2 * target:
-            break
-        rpi += 1
-    return rpi
+    if total == 0 or lens.size == 0:
+        return 8
+
+    def items(r: int) -> int:
+        return int(np.sum(np.maximum(1, -(-lens // r))))
+
+    lo = max(8, -(-total // target))
+    hi = max(lo, int(lens.max()))
+    if items(hi) > target:
+        return max(8, -(-total // (4 * target)))
+    while lo < hi:                      # items(r) does not grow with r
+        mid = (lo + hi) // 2
+        if items(mid) <= target:
+            hi = mid
+        else:
+            lo = mid + 1
+    return lo
 
 
 def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM, interleave: bool = True):

@@ -17,6 +17,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Dict, List, Optional
 
+import sys
+
 import numpy as np
 
 import sphkv_format as fmt
@@ -126,17 +128,33 @@ def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: 
         lengths = [int(x) for x in rng.integers(lo, hi + 1, size=num_seqs)]
     scale = (np.exp(rng.normal(0.0, 0.5, size=(num_kv, dh))) if kscale
              else np.ones((num_kv, dh)))
-    K = [(rng.standard_normal((num_kv, L, dh)) * scale[:, None, :]).astype(np.float16) for L in lengths]
+    # large workloads (configs 4, 5) take minutes on the host: report progress
+    big = sum(lengths) * num_kv >= (1 << 22)
+
+    def progress(what, i=None):
+        if big and (i is None or i % 16 == 15):
+            print(f"[synth] config{config}: {what}" + ("" if i is None else f" {i + 1}/{len(lengths)}"),
+                  file=sys.stderr, flush=True)
+
+    K = []
+    for i, L in enumerate(lengths):
+        K.append((rng.standard_normal((num_kv, L, dh)) * scale[:, None, :]).astype(np.float16))
+        progress("K", i)
     tier_of = []
     for L in lengths:
         for h in range(num_kv):
             tier_of.append(_assign_tiers(rng, L, fracs, sink, recent))
-    V = [rng.standard_normal((num_kv, L, dh)).astype(np.float16) for L in lengths]
+    progress("tiers")
+    V = []
+    for i, L in enumerate(lengths):
+        V.append(rng.standard_normal((num_kv, L, dh)).astype(np.float16))
+        progress("V", i)
     q = rng.standard_normal((num_seqs, num_kv * gqa, dh)).astype(np.float16)
     # config 1 uses an identity page table, the others a random placement;
     # layout="sequential" forces the identity placement (for locality studies)
     permute = config != 1 and layout != "sequential"
     plan = fmt.plan_pages(tier_of, None, num_seqs, num_kv, dh, 16, rng=rng if permute else None)
+    progress("page plan")
     return Workload(name=f"config{config}", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=num_seqs,
                     lengths=lengths, rope_theta=theta, codebooks=cbs, K=K, V=V, q=q,
                     tier_of=tier_of, plan=plan)

@@ -34,3 +34,24 @@ def test_interleaved_items_spread_each_tier_run():
     for it in work:
         r = np.array(_rows(it))
         assert ((r < 60).sum(), ((r >= 60) & (r < 90)).sum(), (r >= 90).sum()) == (12, 6, 2)
+
+
+def test_auto_rows_per_item_fits_one_wave_of_workgroups():
+    # one (seq, head) of 2049 rows x 8 heads on 256 CUs: 65 rows -> 256 items
+    rs = np.arange(9, dtype=np.int64) * 2049
+    r = ops.auto_rows_per_item(rs, 256)
+    assert r == 65 and sum(-(-2049 // r) for _ in range(8)) == 256
+    # the answer is the smallest fitting row count
+    assert sum(-(-2049 // (r - 1)) for _ in range(8)) > 256
+
+
+def test_auto_rows_per_item_with_more_ranges_than_cus_terminates():
+    # 512 ranges of 128..2048 rows on 256 CUs: each range needs an item, so
+    # about four smaller items per CU
+    rng = np.random.default_rng(0)
+    lens = rng.integers(128, 2049, size=512)
+    rs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    r = ops.auto_rows_per_item(rs, 256)
+    assert r == max(8, -(-int(lens.sum()) // 1024))
+    work, ws = ops.make_work(rs, r)
+    assert len(work) >= 512
