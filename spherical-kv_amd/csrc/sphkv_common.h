@@ -50,4 +50,40 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // xor-shuffle within a wave (ds_bpermute / DPP chosen by the compiler).
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with the gfx950 row-swap instructions (VALU, no LDS round trip).
+// v_permlane32_swap a, b: a's upper 32 lanes <-> b's lower 32 lanes;
+// v_permlane16_swap a, b: a's odd rows <-> b's even rows.  With a = b = x the
+// sum a + b pairs every lane with its partner row.  Issued as inline asm: the
+// clang builtin of this toolchain reads the first result twice when both
+// inputs are the same value, and the instructions need the s_nop guard
+// (measured: results are wrong without it, right with it).
+__device__ __forceinline__ void swap32(float& a, float& b) {
+  asm volatile("s_nop 4\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+  asm volatile("s_nop 4\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float rows_max(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  float c = fmaxf(a, b), d = c;
+  swap16(c, d);
+  return fmaxf(c, d);
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  float c = a + b, d = c;
+  swap16(c, d);
+  return c + d;
+}
+__device__ __forceinline__ uint32_t rows_or(uint32_t x) {
+  float a = __builtin_bit_cast(float, x), b = a;
+  swap32(a, b);
+  float c = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) | __builtin_bit_cast(uint32_t, b)), d = c;
+  swap16(c, d);
+  return __builtin_bit_cast(uint32_t, c) | __builtin_bit_cast(uint32_t, d);
+}
+
 }  // namespace sphkv

@@ -287,35 +287,6 @@ __device__ __forceinline__ int xcd_item(int b, int nb) {
   return (b & 7) * (full >> 3) + (b >> 3);
 }
 
-// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
-// with the gfx950 row-swap instructions (VALU, no LDS round trip).
-// v_permlane32_swap a, b: a's upper 32 lanes <-> b's lower 32 lanes;
-// v_permlane16_swap a, b: a's odd rows <-> b's even rows.  With a = b = x the
-// sum a + b pairs every lane with its partner row.  Issued as inline asm: the
-// clang builtin of this toolchain reads the first result twice when both
-// inputs are the same value, and the instructions need the s_nop guard
-// (measured: results are wrong without it, right with it).
-__device__ __forceinline__ void swap32(float& a, float& b) {
-  asm volatile("s_nop 4\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap16(float& a, float& b) {
-  asm volatile("s_nop 4\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ float rows_max(float x) {
-  float a = x, b = x;
-  swap32(a, b);
-  float c = fmaxf(a, b), d = c;
-  swap16(c, d);
-  return fmaxf(c, d);
-}
-__device__ __forceinline__ float rows_sum(float x) {
-  float a = x, b = x;
-  swap32(a, b);
-  float c = a + b, d = c;
-  swap16(c, d);
-  return c + d;
-}
-
 // e^{i 2 pi x} with x a phase in turns (fp32 hardware sine/cosine take turns).
 __device__ __forceinline__ float2 turn_phasor(double x) {
   const float ph = (float)__builtin_amdgcn_fract(x);

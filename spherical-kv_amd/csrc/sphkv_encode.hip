@@ -75,14 +75,39 @@ constexpr int kEncWaves = 8;       // waves per workgroup: one per group in the 
 constexpr int kEncPages = 4;       // pages per workgroup: one lane per token of four pages
 constexpr int kEncMaxG = 8;        // groups per token (dh / g)
 
+constexpr int kCbRow = 20;         // floats per staged codebook row (16 + pad)
+
 template <int DH>
 struct EncodeLds {
   float r[kEncPages * kTile][kEncMaxG];        // radius of (token, group)
   int32_t code[kEncPages * kTile][kEncMaxG];   // code of (token, group)
-  uint8_t stage[kEncPages][512];               // page images
-  int32_t cs[kEncPages][kTile * kEncMaxG];     // a page's codes, token-major
-  _Float16 vt[kEncPages][DH * kTile];          // V pages, dim-major
+  union {
+    struct {                                   // argmax phase, per wave (group)
+      float cb[kEncWaves][64][kCbRow];                  // the group's codebook rows (g = 16 tiers)
+      _Float16 dh[kEncWaves][kEncPages * kTile][20];    // fp16 direction, token-major (rows padded)
+    } arg;
+    struct {                                   // build phase
+      uint8_t stage[kEncPages][512];           // page images
+      int32_t cs[kEncPages][kTile * kEncMaxG]; // a page's codes, token-major
+      _Float16 vt[kEncPages][DH * kTile];      // V pages, dim-major
+    } build;
+  } u;
 };
+
+// Nearest-centroid search of the g = 16 tiers in two stages, with the
+// group's codebook rows staged in LDS once per (tier, kv head) run.
+//  1. Approximate similarities of 16 tokens x 16 codes per
+//     v_mfma_f32_16x16x16_f16, from fp16 copies of the direction and the
+//     codebook rows.  Both are unit vectors, so |approx - s| <= 2^-10 from the
+//     two fp16 roundings (sum_i |d_i c_i| <= |d| |c| <= 1), plus at most
+//     16 * 2^-14 if the unit flushes fp16 denormals, plus the fp32 rounding of
+//     the chains (< 1e-5): eps < 2.1e-3, where s is the exact fp32 score.
+//  2. Every code c with approx_c >= max_approx - kCandSlack (>= 2 eps) is
+//     scored exactly (the torch-order chain below), in ascending order; the
+//     first maximum among them is the first maximum over all codes, because
+//     every code whose exact score equals the exact maximum passes the test.
+//     No candidate (NaN similarities) falls back to scoring every code.
+constexpr float kCandSlack = 5e-3f;
 
 // Nearest centroid of one (token, group) against the codebook rows cbg[c * GG ..]
 // (wave-uniform, so every centroid coordinate is a scalar operand): the fmaf
@@ -174,19 +199,208 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     const int j = lane >> 4, t = lane & 15;
     const int p = p0 + j;
     const bool p_ok = p < a.num_pages;
+    // the token's source row is loaded together with the page's metadata (its
+    // address does not depend on them) and masked by the count afterwards
+    const int64_t row_raw = p_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
     const int tid_l = p_ok ? a.tier[p] : 0;
     const int n_l = p_ok ? min(max(a.count[p], 0), kTile) : 0;
-    const int head_l = p_ok ? a.seq_head[p] % a.num_kv : 0;
-    int64_t row = (p_ok && t < n_l) ? a.src_rows[(int64_t)p * kTile + t] : -1;
+    const int sh_l = p_ok ? a.seq_head[p] : -1;
+    const int head_l = sh_l >= 0 ? sh_l % a.num_kv : 0;
+    int64_t row = t < n_l ? row_raw : -1;
     if (row >= a.num_src_rows) row = -1;
-    const bool comp_l = tid_l >= 1 && tid_l <= 3 && wave < DH / tier_g(tid_l);
+    // a page is encoded only with its tier's codebook and a valid (seq, head)
+    const bool comp_l = tid_l >= 1 && tid_l <= 3 && wave < DH / tier_g(tid_l) && sh_l >= 0 &&
+                        a.cb[tid_l >= 1 && tid_l <= 3 ? tid_l : 0] != nullptr;
     const int gi = wave;
-    uint64_t todo = __builtin_amdgcn_ballot_w64(comp_l);
+    // ---- g = 16 tiers (1, 2): MFMA similarities, exact scores for candidates
+    const bool m16_l = comp_l && tier_g(tid_l) == 16;
+    const uint64_t m16 = __builtin_amdgcn_ballot_w64(m16_l);
+    if (m16) {
+      const bool live = m16_l && row >= 0;
+      const int tl = lane & 15, kg = lane >> 4;
+      float (*cbs)[kCbRow] = sm.u.arg.cb[wave];
+      // codebook rows of the first g = 16 page's (tier, head), loaded before K
+      const int j0 = (int)__builtin_ctzll(m16) >> 4;
+      const int tid0 = uniform(__builtin_amdgcn_readlane(tid_l, 16 * j0));
+      const int h0 = uniform(__builtin_amdgcn_readlane(head_l, 16 * j0));
+      const int C0 = tier_C(tid0);                                  // 64 or 16
+      float4 crow[4];
+      {
+        const float* cbg = a.cb[tid0] + ((int64_t)h0 * (DH / 16) + gi) * C0 * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          crow[i] = lane < C0 ? *reinterpret_cast<const float4*>(cbg + lane * 16 + 4 * i) : float4{0.f, 0.f, 0.f, 0.f};
+      }
+      // do all g = 16 pages of the workgroup use (tid0, h0)?
+      bool same = true;
+#pragma unroll
+      for (int jj = 0; jj < kEncPages; ++jj)
+        if ((m16 >> (16 * jj)) & 0xFFFFull)
+          same = same && __builtin_amdgcn_readlane(tid_l, 16 * jj) == tid0 &&
+                 __builtin_amdgcn_readlane(head_l, 16 * jj) == h0;
+      float dir[16];
+      float r = 0.f;
+      {
+        float x[16];
+        if (live) {
+          const int64_t kofs = row * DH + gi * 16;
+          if (a.k_is_fp32) {
+            const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(a.k) + kofs);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float4 v4 = src[i];
+              x[4 * i] = v4.x; x[4 * i + 1] = v4.y; x[4 * i + 2] = v4.z; x[4 * i + 3] = v4.w;
+            }
+          } else {
+            const half8* src = reinterpret_cast<const half8*>(static_cast<const __half*>(a.k) + kofs);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              const half8 hv = src[i];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)hv[e];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) x[i] = 0.f;
+        }
+        r = live ? torch_norm(x, 16) : 0.f;
+        const float den = __fadd_rn(r, 1e-8f);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dir[i] = live ? __fdiv_rn(x[i], den) : 0.f;
+      }
+      {
+        _Float16* d = sm.u.arg.dh[wave][lane];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<half4*>(d + 4 * q4) = half4{(_Float16)dir[4 * q4], (_Float16)dir[4 * q4 + 1],
+                                                        (_Float16)dir[4 * q4 + 2], (_Float16)dir[4 * q4 + 3]};
+      }
+      if (lane < C0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&cbs[lane][4 * i]) = crow[i];
+      }
+      wave_lds_sync();
+      // candidate codes of 16 tokens of page jj against the staged rows (A
+      // operands, codes 16 b + row); lane (tl, kg) ends with token tl's mask
+      auto page_masks = [&](int jj, int C, const half4 (&A)[4], uint32_t& lo, uint32_t& hi) {
+        const half4 B = *reinterpret_cast<const half4*>(sm.u.arg.dh[wave][16 * jj + tl] + 4 * kg);
+        floatx4 D[4];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          if (16 * b < C) {
+            D[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[b], B, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, D[b][i]);    // D[b][i]: code 16 b + 4 kg + i, token tl
+          }
+        }
+        const float thr = rows_max(mloc) - kCandSlack;
+        lo = 0u;
+        hi = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          if (16 * b < C) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int c = 16 * b + 4 * kg + i;
+              if (D[b][i] >= thr) {
+                if (c < 32) lo |= 1u << c;
+                else hi |= 1u << (c - 32);
+              }
+            }
+          }
+        }
+        lo = rows_or(lo);
+        hi = rows_or(hi);
+      };
+      auto load_A = [&](int C, half4 (&A)[4]) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float4 cv = 16 * b < C ? *reinterpret_cast<const float4*>(&cbs[16 * b + tl][4 * kg]) : float4{0.f, 0.f, 0.f, 0.f};
+          A[b] = half4{(_Float16)cv.x, (_Float16)cv.y, (_Float16)cv.z, (_Float16)cv.w};
+        }
+      };
+      // exact scores of this lane's token over the codes of mask (lo, hi)
+      auto score = [&](uint32_t lo, uint32_t hi, int C) {
+        uint64_t mk = (uint64_t)lo | ((uint64_t)hi << 32);
+        if (C < 64) mk &= (1ull << C) - 1;
+        if (mk == 0) mk = C == 64 ? ~0ull : ((1ull << C) - 1);      // NaN similarities: score every code
+        const bool naive = n_l * 16 * C < 400;                       // torch's own small-bmm loop
+        float best_sim = 0.f;
+        int best = -1;
+        while (mk) {
+          const int c = (int)__builtin_ctzll(mk);
+          mk &= mk - 1;
+          float w[16];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float4 v4 = *reinterpret_cast<const float4*>(&cbs[c][4 * i]);
+            w[4 * i] = v4.x; w[4 * i + 1] = v4.y; w[4 * i + 2] = v4.z; w[4 * i + 3] = v4.w;
+          }
+          const float sc = naive ? code_sim<16, true>(dir, w) : code_sim<16, false>(dir, w);
+          if (best < 0 || sc > best_sim) { best_sim = sc; best = c; }
+        }
+        return best;
+      };
+      if (same) {
+        // one set of A operands and one exact pass for all four pages
+        half4 A[4];
+        load_A(C0, A);
+        uint32_t mlo = 0u, mhi = 0u;
+#pragma unroll
+        for (int jj = 0; jj < kEncPages; ++jj) {
+          if (((m16 >> (16 * jj)) & 0xFFFFull) == 0) continue;
+          uint32_t lo, hi;
+          page_masks(jj, C0, A, lo, hi);
+          if ((lane >> 4) == jj) { mlo = lo; mhi = hi; }               // lane 16 jj + t: token t of page jj
+        }
+        if (live) {
+          sm.r[lane][gi] = r;
+          sm.code[lane][gi] = score(mlo, mhi, C0);
+        }
+      } else {
+        // pages of several (tier, head) runs: one page at a time, restaging
+        int st_tid = tid0, st_h = h0;
+        for (int jj = 0; jj < kEncPages; ++jj) {
+          if (((m16 >> (16 * jj)) & 0xFFFFull) == 0) continue;
+          const int tid = uniform(__builtin_amdgcn_readlane(tid_l, 16 * jj));
+          const int h = uniform(__builtin_amdgcn_readlane(head_l, 16 * jj));
+          const int C = tier_C(tid);
+          if (tid != st_tid || h != st_h) {
+            wave_lds_sync();
+            const float* cbg = a.cb[tid] + ((int64_t)h * (DH / 16) + gi) * C * 16;
+            if (lane < C) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<float4*>(&cbs[lane][4 * i]) = *reinterpret_cast<const float4*>(cbg + lane * 16 + 4 * i);
+            }
+            st_tid = tid;
+            st_h = h;
+            wave_lds_sync();
+          }
+          half4 A[4];
+          load_A(C, A);
+          uint32_t lo, hi;
+          page_masks(jj, C, A, lo, hi);
+          if (live && (lane >> 4) == jj) {
+            sm.r[lane][gi] = r;
+            sm.code[lane][gi] = score(lo, hi, C);
+          }
+        }
+      }
+      if (m16_l && !live) {
+        sm.r[lane][gi] = 0.f;
+        sm.code[lane][gi] = 0;
+      }
+    }
+    // ---- other tiers (g = 32): exact scan with scalar codebook rows
+    uint64_t todo = __builtin_amdgcn_ballot_w64(comp_l && !m16_l);
     while (todo) {
       const int lead = (int)__builtin_ctzll(todo);                 // first lane not yet encoded
       const int tid = uniform(__builtin_amdgcn_readlane(tid_l, lead));
       const int h = uniform(__builtin_amdgcn_readlane(head_l, lead));
-      const bool mine = comp_l && tid_l == tid && head_l == h;
+      const bool mine = comp_l && !m16_l && tid_l == tid && head_l == h;
       todo &= ~__builtin_amdgcn_ballot_w64(mine);
       const int g = uniform(tier_g(tid)), C = uniform(tier_C(tid)), G = DH / g;
       const uint64_t cba = (uint64_t)(a.cb[tid] + ((int64_t)h * G + gi) * C * g);
@@ -221,7 +435,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     // the wave stores whole 32-byte dim rows
     const int64_t vs = a.vslot[p];
     if (vs < 0 || vs >= a.num_vpages) return;
-    _Float16* vt = sm.vt[j];
+    _Float16* vt = sm.u.build.vt[j];
     int64_t vr = tok_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
     if (vr >= a.num_src_rows) vr = -1;
     constexpr int QD = DH / 4;
@@ -288,8 +502,8 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, shfl_xor(m, o));
     scale_[k] = m;
   }
-  uint8_t* st = sm.stage[j];
-  int32_t* cs = sm.cs[j];
+  uint8_t* st = sm.u.build.stage[j];
+  int32_t* cs = sm.u.build.cs[j];
   const int nG = n * G;
   const int tb = (nG * b + 7) / 8;
   const int hdr = kHeaderBytes + 4 * G;
