@@ -95,3 +95,50 @@ def test_encode_partial_and_edge_pages(gpu):
         cpu = oracle.build_pool(wl, with_codes=True)
         assert (pool.pages.cpu().numpy() == cpu["pages"]).all()
         assert (pool.v_pool.cpu().numpy().view(np.uint16) == cpu["v_pool"].view(np.uint16)).all()
+
+
+def test_encode_near_ties_and_degenerate_groups(gpu):
+    # Keys built to stress the nearest-centroid search: the sum of two
+    # centroids of the group (an exact tie in real arithmetic, decided by the
+    # rounding of the reference's fp32 dot products), a centroid itself at
+    # several scales, a centroid plus a tiny share of another, and all-zero
+    # groups.  Codes and radii must match the C oracle bit for bit.
+    rng = np.random.default_rng(23)
+    dh, H, L = 128, 2, 160
+    tier_of = [np.array([[1, 2, 3][(i + h) % 3] for i in range(L)], np.int32) for h in range(H)]
+    cbs = synth.make_codebooks(rng, H, dh, [1, 2, 3])
+    K = np.zeros((H, L, dh), np.float32)
+    for h in range(H):
+        for t in range(L):
+            tid = int(tier_of[h][t])
+            cb = cbs[tid][h]                      # [G, C, g]
+            G, C, g = cb.shape
+            for j in range(G):
+                a, b = rng.choice(C, size=2, replace=False)
+                kind = (t + j) % 5
+                if kind == 0:
+                    v = cb[j, a] + cb[j, b]
+                elif kind == 1:
+                    v = cb[j, a] * np.float32(2.0 ** rng.integers(-6, 7))
+                elif kind == 2:
+                    v = cb[j, a] + np.float32(1e-3) * cb[j, b]
+                elif kind == 3:
+                    v = np.zeros(g, np.float32)
+                else:
+                    v = (cb[j, a] - cb[j, b]) * np.float32(0.5)
+                K[h, t, j * g:(j + 1) * g] = v
+    K16 = [K.astype(np.float16)]
+    V = [rng.standard_normal((H, L, dh)).astype(np.float16)]
+    plan = fmt.plan_pages(tier_of, None, 1, H, dh, 16, rng=rng, num_vpages=None)
+    wl = synth.Workload(name="ties", dh=dh, num_kv=H, gqa=1, num_seqs=1, lengths=[L], rope_theta=5e5,
+                        codebooks=cbs, K=K16, V=V, q=np.zeros((1, H, dh), np.float16), tier_of=tier_of,
+                        plan=plan)
+    log(f"encode near-ties dh={dh} rows={plan.num_rows}")
+    pool, r_out, c_out = ops.build_pool_gpu(wl, gpu, with_codes=True)
+    torch.cuda.synchronize()
+    cpu = oracle.build_pool(wl, with_codes=True)
+    r, c = r_out.cpu().numpy(), c_out.cpu().numpy()
+    comp = wl.plan.tier != fmt.DENSE_TIER_ID
+    assert (c[comp] == cpu["codes"][comp]).all(), f"{int((c[comp] != cpu['codes'][comp]).sum())} codes differ"
+    assert (r[comp].view(np.uint32) == cpu["r"][comp].view(np.uint32)).all()
+    assert (pool.pages.cpu().numpy() == cpu["pages"]).all()
