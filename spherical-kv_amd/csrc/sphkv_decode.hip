@@ -20,27 +20,29 @@
 // Per page (16 tokens, positions pos_t), lane l = (token t = l % 16, quarter
 // u = l / 16), page centre t_mid = (min pos + max pos) / 2:
 //   1. the query rows are rotated once per page by -t_mid (fp32, lanes = RoPE
-//      frequencies j) and kept in LDS as hi + lo fp16 halves;
+//      frequencies j) and kept in LDS in the QK MFMA's operand order;
 //   2. k_hat of token t on this lane's 32 dimensions (chunk_dim):
 //      compressed  k_hat_d = r_hat_g * centroid_g[code][d mod g],
 //                  r_hat_g = int8 / 127 * scale_g         (pagebuilder.py:17-21)
 //      dense       k_hat_d = K[t][d] (fp16);
 //   3. k_rot = R(pos_t - t_mid) k_hat in fp32 with phasors from an LDS table
-//      of e^{i 2 pi f_j d}, |d| < kDelta (formed directly beyond), split as
-//      hi + lo fp16.  Since <R(-pos) q, k_hat> = <R(-t_mid) q, R(pos - t_mid)
-//      k_hat>, this is the reference's back-rotated query
-//      (spherical_kv_pipeline.py:2143-2176; its clip of the cosine to [-1, 1]
-//      only acts on rounding error).  Phases are formed in fp64 turns and
-//      reduced to [0, 1) before the fp32 hardware sine / cosine;
-//   4. S[h][t] = q_rot_h . k_rot on MFMA (16x16x32 f16) as hi*hi + lo*hi +
-//      hi*lo: about fp32 accuracy whatever the logit scale;
+//      of e^{i 2 pi f_j d}, |d| < kDelta (formed directly beyond).  Since
+//      <R(-pos) q, k_hat> = <R(-t_mid) q, R(pos - t_mid) k_hat>, this is the
+//      reference's back-rotated query (spherical_kv_pipeline.py:2143-2176;
+//      its clip of the cosine to [-1, 1] only acts on rounding error).  Phases
+//      are formed in fp64 turns and reduced to [0, 1) before the fp32 hardware
+//      sine / cosine;
+//   4. S[t][h] = k_rot . q_rot_h on the fp32 MFMA (4x4x1, 16 blocks = 4 lane
+//      quarters x 4 token groups, one dimension per instruction), then the
+//      quarters' partial sums are added with row swaps: fp32 products and
+//      sums, no operand splitting;
 //   5. online softmax in the log2 domain.  The running reference max of a head
 //      only moves when a page's max exceeds it by more than 2^8, so the
 //      accumulator rescale is rare; p = 2^(s - m) <= 256 is rounded to fp16 and
 //      the same rounded p is summed into l, so the output stays an exact
 //      convex combination of V rows;
-//   6. O[h][d] += P[h][t] V[t][d] on MFMA (16x16x16 f16), V read in the
-//      pool's MFMA operand order.
+//   6. O[h][d] += P[h][t] V[t][d] on MFMA (4x4x4 f16, 16 blocks of 4 dims),
+//      V read in the pool's MFMA operand order.
 #include "sphkv_common.h"
 #include "sphkv_internal.h"
 
@@ -192,9 +194,10 @@ __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 //    rows padded by 16 bytes;
 //  * f_j in turns per token (fp64);
 //  * per wave: the 512-byte staging window of its page, the query rows
-//    rotated to the page centre split as hi + lo fp16 ([2][GQA][DH + 8]), and
-//    the page's softmax weights P as fp16 [max(GQA, 4)][16 tokens] (rows >=
-//    GQA stay zero), read back as the PV MFMA's A operand.
+//    rotated to the page centre (fp32, in the QK MFMA's operand order; slots
+//    of heads >= GQA stay zero), and the page's softmax weights P as fp16
+//    [max(GQA, 4)][16 tokens] (rows >= GQA stay zero), read back as the PV
+//    MFMA's A operand.
 template <int DH, int GQA>
 struct DecodeLds {
   static constexpr int kWaves = decode_waves<GQA>();
@@ -207,15 +210,21 @@ struct DecodeLds {
     return tid == 3 ? cb_n1 + cb_n2 : (tid == 2 ? cb_n1 : 0);
   }
   static constexpr int drow = NJ * 8 + 16;                       // bytes
-  static constexpr int qrow = DH + 8;                            // halves
   static constexpr int o_cb = 0;
   static constexpr int o_dtab = align16(4 * (cb_n1 + cb_n2 + cb_n3));
   static constexpr int o_ftab = o_dtab + kDelta * drow;
   static constexpr int o_stage = o_ftab + NJ * 8;
+  static constexpr int PR = GQA < 4 ? 4 : GQA;                   // heads padded to 4 (slots)
+  static constexpr int NHS = PR / 4;                             // sets of 4 head slots
+  // rotated query, fp32, per set of 4 head slots: float4 group kq (dims kk =
+  // 4 kq .. 4 kq + 3 of a lane quarter's 32) x (quarter u, slot j), groups
+  // kq_stride floats apart: the MFMA operand reads (16 float4s of one group)
+  // and the per-frequency writes (one float per lane) are both conflict-free
+  static constexpr int kq_stride = 68;
+  static constexpr int qs_floats = (DH / 16) * kq_stride;
   static constexpr int o_qr = o_stage + kWaves * 512;
-  static constexpr int qr_wave = 2 * GQA * qrow;                 // halves per wave
-  static constexpr int PR = GQA < 4 ? 4 : GQA;                   // P rows (heads padded to 4)
-  static constexpr int o_pt = o_qr + kWaves * qr_wave * 2;
+  static constexpr int qr_wave = NHS * qs_floats * 4;            // bytes per wave
+  static constexpr int o_pt = o_qr + kWaves * qr_wave;
   static constexpr int total = o_pt + kWaves * PR * 32;
   // the end-of-item wave merge reuses the space: [kWaves][GQA][DH] acc,
   // [kWaves][GQA][2] (m, l), [GQA][kWaves] weights
@@ -293,34 +302,36 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
   return float2{__builtin_amdgcn_cosf(ph), __builtin_amdgcn_sinf(ph)};
 }
 
-// x = hi + lo with hi, lo fp16: hi = x rounded toward zero (v_cvt_pkrtz), lo =
-// fp16(x - hi) formed by one mixed-precision FMA per half (fp32 x, fp16 hi)
-// that writes that half of the packed result.  The pair carries x to about
-// 2^-22 relative, so products on the fp16 MFMA lose nothing that matters
-// against the 2e-3 tolerance.  The FMAs are inline asm (the compiler forms
-// them only when fp32 denormals are flushed); the s_nop after each covers the
-// forwarding hazard of a partial (one-half) VGPR write, which the compiler's
-// hazard recognizer does not track through inline asm.  Inputs are never the
-// direct result of a transcendental instruction.
-__device__ __forceinline__ uint32_t pk_rtz(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+// Rotation by N lanes within each 16-lane row (DPP row_ror).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, false));
 }
-__device__ __forceinline__ uint32_t pk_rest(float a, float b, uint32_t hi) {
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
-      "s_nop 0\n\t"
-      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
-      "s_nop 0"
-      : "=&v"(d) : "v"(a), "v"(b), "v"(hi));
-  return d;
+
+// Max / sum over the 16 lanes l' with l' = l (mod 4): the four lanes of each
+// row (row_ror 4, 8), then the four rows.
+__device__ __forceinline__ float head_max(float x) {
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<8>(x));
+  return rows_max(x);
 }
-__device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8& lo) {
-  uint4 h, l;
-  h.x = pk_rtz(x[0], x[1]); h.y = pk_rtz(x[2], x[3]); h.z = pk_rtz(x[4], x[5]); h.w = pk_rtz(x[6], x[7]);
-  l.x = pk_rest(x[0], x[1], h.x); l.y = pk_rest(x[2], x[3], h.y);
-  l.z = pk_rest(x[4], x[5], h.z); l.w = pk_rest(x[6], x[7], h.w);
-  hi = __builtin_bit_cast(half8, h);
-  lo = __builtin_bit_cast(half8, l);
+__device__ __forceinline__ float head_sum(float x) {
+  x += row_ror<4>(x);
+  x += row_ror<8>(x);
+  return rows_sum(x);
+}
+
+// Sums the four lane quarters' partials of a 4x4x1 MFMA result: element i of
+// lane l holds (token 4 ((l >> 2) & 3) + i, head slot l & 3) summed over the
+// 32 dimensions of quarter l >> 4.  Two row-swap rounds pair the quarters and
+// leave lane l with the full sum of element {0, 2, 1, 3}[l >> 4].
+__device__ __forceinline__ float quarter_sum(floatx4 s) {
+  float a0 = s[0], a1 = s[1], b0 = s[2], b1 = s[3];
+  swap32(a0, a1);
+  swap32(b0, b1);
+  float a = a0 + a1, b = b0 + b1;
+  swap16(a, b);
+  return a + b;
 }
 
 template <int DH, int GQA>
@@ -361,7 +372,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int t = lane & 15;
   const int u = lane >> 4;
   uint8_t* st = smem + L::o_stage + wave * 512;
-  _Float16* qr = reinterpret_cast<_Float16*>(smem + L::o_qr) + wave * L::qr_wave;   // [hi, lo][GQA][qrow]
+  float* qr = reinterpret_cast<float*>(smem + L::o_qr + wave * L::qr_wave);
 
   int p = rb + wave * rstride;
   const Res rs = make_res(a);
@@ -402,10 +413,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       qv[hh] = __builtin_bit_cast(uint32_t, v);
     }
   }
-  if (GQA < 4 && lane < (4 - GQA) * 2) {              // zero P rows GQA..3 of this wave
-    half8 z;
-    for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.f;
-    *reinterpret_cast<half8*>(reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile + GQA * kTile + 8 * lane) = z;
+  if (GQA < 4) {
+    // zero P rows GQA..3 and the query slots GQA..3 of this wave (never written)
+    if (lane < (4 - GQA) * 2) {
+      half8 z;
+      for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.f;
+      *reinterpret_cast<half8*>(reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile + GQA * kTile + 8 * lane) = z;
+    }
+    for (int i = lane; i < DH; i += 64)              // i = (kq, u, slot j)
+      if ((i & 3) >= GQA) *reinterpret_cast<floatx4*>(qr + (i >> 4) * L::kq_stride + 4 * (i & 15)) = (floatx4){0.f, 0.f, 0.f, 0.f};
   }
   // first page's data and the next page's row
   Row row_c = row_take(a, rl_c, p, re);
@@ -447,13 +463,14 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // no wait inside the loop has to account for it
   __builtin_amdgcn_s_waitcnt(0);
 
-  // online-softmax state of head hl = lane % 16 (replicated over the 4 rows;
-  // lanes hl >= GQA shadow head hl % GQA and are never written out)
-  const int hl = lane & 15;
-  float m_run = -INFINITY, l_run = 0.f;
+  // online-softmax state of head 4 hs + (lane % 4) (the same in all 16 lanes
+  // of that head; slots >= GQA hold zero logits and are never written out)
+  constexpr int NHS = L::NHS, NHF = DH / 64;
+  float m_run[NHS], l_run[NHS];
+#pragma unroll
+  for (int hs = 0; hs < NHS; ++hs) { m_run[hs] = -INFINITY; l_run[hs] = 0.f; }
   // PV accumulators of the 4x4x4 MFMA: acc[hs][hf] lane l, element i =
   // O[head 4 hs + i][dim 64 hf + l]
-  constexpr int NHS = L::PR / 4, NHF = DH / 64;
   floatx4 acc[NHS][NHF];
 #pragma unroll
   for (int hs = 0; hs < NHS; ++hs)
@@ -509,22 +526,20 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
     const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
     if (lane < NJ) {
-      const float2 z = turn_phasor((double)t_mid * ftab[lane_v % NJ]);
+      // lane = frequency j: dims j and j + NJ are element kk = j mod (DH/8)
+      // and kk + DH/8 of quarter j / (DH/8)
+      const int j = lane_v % NJ;
+      const float2 z = turn_phasor((double)t_mid * ftab[j]);
+      const int kk = j % (DH / 8), uq = j / (DH / 8);
+      float* q0 = qr + (kk >> 2) * L::kq_stride + uq * 16 + (kk & 3);
+      float* q1 = q0 + (DH / 32) * L::kq_stride;
 #pragma unroll
       for (int hh = 0; hh < GQA; ++hh) {
         const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
-        const float q0 = (float)qp[0], q1 = (float)qp[1];
-        const float r0 = q0 * z.x + q1 * z.y;
-        const float r1 = q1 * z.x - q0 * z.y;
-        const uint32_t hp = pk_rtz(r0, r1);
-        const half2v hi = __builtin_bit_cast(half2v, hp);
-        const half2v lo = __builtin_bit_cast(half2v, pk_rest(r0, r1, hp));
-        _Float16* qh = qr + hh * L::qrow;
-        _Float16* ql = qr + (GQA + hh) * L::qrow;
-        qh[lane] = hi[0];
-        qh[lane + NJ] = hi[1];
-        ql[lane] = lo[0];
-        ql[lane + NJ] = lo[1];
+        const float a0 = (float)qp[0], a1 = (float)qp[1];
+        const int o = (hh >> 2) * L::qs_floats + (hh & 3) * 4;
+        q0[o] = a0 * z.x + a1 * z.y;
+        q1[o] = a1 * z.x - a0 * z.y;
       }
     }
 
@@ -548,16 +563,18 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     }
     wave_lds_sync();
 
-    // ---- k_rot = R(pos - t_mid) k_hat per chunk pair (c, c + NP), fp32,
-    //      split hi + lo fp16.  Phasors from the delta table (sine negated
-    //      for pos < t_mid), or formed directly when |pos - t_mid| >= kDelta.
-    //      Each chunk pair feeds the QK MFMA (S^T = K_rot q_rot^T as hi*hi +
-    //      lo*hi + hi*lo; lane (u, hl) gets head hl, tokens 4u..4u+3) as soon
-    //      as it is split, so few operand registers are live at a time.
-    floatx4 S = {0.f, 0.f, 0.f, 0.f};
+    // ---- k_rot = R(pos - t_mid) k_hat per chunk pair (c, c + NP), fp32.
+    //      Phasors from the delta table (sine negated for pos < t_mid), or
+    //      formed directly when |pos - t_mid| >= kDelta.  Each chunk pair
+    //      feeds the fp32 4x4x1 MFMA as soon as it is formed: block b = lane /
+    //      4 = (quarter u, token group), A = k_rot of token t (row t % 4),
+    //      B = the rotated query of head slot lane % 4 (column), one
+    //      dimension per instruction; chunks c and c + NP accumulate apart.
+    floatx4 Sa[NHS], Sb[NHS];
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) { Sa[hs] = (floatx4){0.f, 0.f, 0.f, 0.f}; Sb[hs] = Sa[hs]; }
     {
-      const _Float16* qh = qr + (hl % GQA) * L::qrow;
-      const _Float16* ql = qh + GQA * L::qrow;
+      const float* qb = qr + (u * 4 + (lane_v & 3)) * 4;
       const int dl = valid ? pos_c - t_mid : 0;
       const int ad = dl < 0 ? -dl : dl;
       const bool near = ad < kDelta;
@@ -604,51 +621,58 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
           x0[s] = k0[s] * pc[s] - k1[s] * ps[s];
           x1[s] = k1[s] * pc[s] + k0[s] * ps[s];
         }
-        half8 kh0, kl0, kh1, kl1;
-        split_f16(x0, kh0, kl0);
-        split_f16(x1, kh1, kl1);
-        const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u, d1 = chunk_dim<DH>(c + NP, 0) + (DH / 8) * u;
-        const half8 qa0 = *reinterpret_cast<const half8*>(qh + d0);
-        const half8 qb0 = *reinterpret_cast<const half8*>(ql + d0);
-        const half8 qa1 = *reinterpret_cast<const half8*>(qh + d1);
-        const half8 qb1 = *reinterpret_cast<const half8*>(ql + d1);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qa0, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qa0, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qb0, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qa1, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qa1, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qb1, S, 0, 0, 0);
+#pragma unroll
+        for (int hs = 0; hs < NHS; ++hs) {
+          const float* qs = qb + hs * L::qs_floats;
+          const floatx4 qa0 = *reinterpret_cast<const floatx4*>(qs + (2 * c) * L::kq_stride);
+          const floatx4 qa1 = *reinterpret_cast<const floatx4*>(qs + (2 * c + 1) * L::kq_stride);
+          const floatx4 qc0 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP)) * L::kq_stride);
+          const floatx4 qc1 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP) + 1) * L::kq_stride);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[s], qa0[s], Sa[hs], 0, 0, 0);
+            Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[s], qc0[s], Sb[hs], 0, 0, 0);
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[4 + s], qa1[s], Sa[hs], 0, 0, 0);
+            Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[4 + s], qc1[s], Sb[hs], 0, 0, 0);
+          }
+        }
       }
     }
 
-    // ---- online softmax over the page, per head, in the log2 domain -------
+    // ---- online softmax over the page, per head, in the log2 domain:
+    //      after the quarter sum lane l holds token tk, head slot 4 hs + l % 4
     const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
-    float x[4];
+    const int tk = 4 * ((lane_v >> 2) & 3) + ((0xD8 >> (2 * (lane_v >> 4))) & 3);
+    const bool tv = (vmask >> tk) & 1u;
+    float alpha[NHS];
+    bool upd_any = false;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      x[s] = ((vmask >> (4 * u + s)) & 1u) ? S[s] * a.scale_log2 : -INFINITY;
-    const float mx = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-    const bool upd = mx > m_run + kRescaleLog2;
-    const float m_new = upd ? mx : m_run;
-    const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-    half4 pa;
-    float es = 0.f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float e = (x[s] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[s] - m_new);
-      pa[s] = (_Float16)e;
-      es += (float)pa[s];
+    for (int hs = 0; hs < NHS; ++hs) {
+      // the cross-lane sum runs on every lane (never under the token mask)
+      const float lg = quarter_sum(Sa[hs] + Sb[hs]);
+      const float x = tv ? lg * a.scale_log2 : -INFINITY;
+      const float mx = head_max(x);
+      const bool upd = mx > m_run[hs] + kRescaleLog2;
+      const float m_new = upd ? mx : m_run[hs];
+      alpha[hs] = upd ? __builtin_amdgcn_exp2f(m_run[hs] - m_new) : 1.f;
+      const _Float16 ph = (_Float16)(tv ? __builtin_amdgcn_exp2f(x - m_new) : 0.f);
+      l_run[hs] = alpha[hs] * l_run[hs] + head_sum((float)ph);
+      m_run[hs] = m_new;
+      upd_any |= upd;
+      // ---- P[head][token] for the PV MFMA's A operand
+      if (4 * hs + (lane_v & 3) < GQA) pt[(4 * hs + (lane_v & 3)) * kTile + tk] = ph;
     }
-    l_run = alpha * l_run + rows_sum(es);
-    m_run = m_new;
-    if (__ballot(upd) != 0) {
-      // head h's factor lives in lane h (row u = 0); accumulators hold heads
+    if (__ballot(upd_any) != 0) {
+      // head 4 hs + i's factor lives in lane i; accumulators hold heads
       // 4 hs + i in element i
 #pragma unroll
       for (int hs = 0; hs < NHS; ++hs)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 * hs + i));
+          const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[hs]), i));
 #pragma unroll
           for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
         }
@@ -657,7 +681,6 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     // ---- O += P V on the 4x4x4 MFMA (16 blocks = 16 groups of 4 dims):
     //      A = P[4 heads][4 tokens] (same for every block, from LDS),
     //      B = V[4 tokens][dim 64 hf + l] (lane l's own dim) -----------------
-    if (hl < GQA) *reinterpret_cast<half4*>(pt + hl * kTile + 4 * u) = pa;
     // slots without a token get V = 0 (their p is already 0; this keeps
     // whatever bytes an unused slot holds out of the sum)
     if (vmask != 0xFFFFu) {
@@ -716,7 +739,12 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       if (4 * hs + i < GQA)
 #pragma unroll
         for (int hf = 0; hf < NHF; ++hf) mrg[(wave * GQA + 4 * hs + i) * DH + 64 * hf + lane] = acc[hs][hf][i];
-  if (hl < GQA && u == 0) { mrg_ml[(wave * GQA + hl) * 2] = m_run; mrg_ml[(wave * GQA + hl) * 2 + 1] = l_run; }
+#pragma unroll
+  for (int hs = 0; hs < NHS; ++hs)
+    if (lane < 4 && 4 * hs + lane < GQA) {
+      mrg_ml[(wave * GQA + 4 * hs + lane) * 2] = m_run[hs];
+      mrg_ml[(wave * GQA + 4 * hs + lane) * 2 + 1] = l_run[hs];
+    }
   __syncthreads();
   // every output thread derives its head's wave weights 2^(m_w - M) itself
   // (the kWaves reads of a head hit one LDS address each: broadcasts), so

@@ -130,6 +130,33 @@ def test_decode_edge_cases(gpu):
     assert max_err(got[0, :gqa], np.broadcast_to(V[0][0, 0].astype(np.float32), (gqa, dh))) == 0.0
 
 
+@pytest.mark.parametrize("dh,gqa", [(128, 4), (64, 1), (128, 2), (128, 8)])
+def test_decode_partial_and_far_pages(gpu, dh, gqa):
+    # Every tier with a partial last page (250 tokens: 15 full pages + 10), and
+    # pages whose tokens lie 10 positions apart (page span > the phasor table,
+    # so the direct phasors run), full and partial.  Logits span several
+    # units, so a token's weight depends on its own logit.
+    rng = np.random.default_rng(19)
+    H = 2
+    cases = [("dense", 250, lambda i: fmt.DENSE_TIER_ID), ("t1", 250, lambda i: 1), ("t2", 250, lambda i: 2),
+             ("t3", 250, lambda i: 3), ("far", 1600, lambda i: 1 if i % 10 == 0 else fmt.DENSE_TIER_ID),
+             ("far-partial", 1500, lambda i: 1 if i % 10 == 0 else 2)]
+    for name, L, tier in cases:
+        tier_of = [np.array([tier(i) for i in range(L)], np.int32) for _ in range(H)]
+        cbs = synth.make_codebooks(rng, H, dh, [1, 2, 3])
+        K = [rng.standard_normal((H, L, dh)).astype(np.float16)]
+        V = [rng.standard_normal((H, L, dh)).astype(np.float16)]
+        q = (rng.standard_normal((1, H * gqa, dh)) * 2).astype(np.float16)
+        plan = fmt.plan_pages(tier_of, None, 1, H, dh, 16, rng=rng)
+        wl = synth.Workload(name=name, dh=dh, num_kv=H, gqa=gqa, num_seqs=1, lengths=[L], rope_theta=5e5,
+                            codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan)
+        log(f"decode partial/far {name} dh={dh} gqa={gqa} counts={sorted(set(plan.count.tolist()))}")
+        pool, cpu = pool_from_oracle(wl, gpu)
+        err = max_err(_decode(pool, wl, gpu), oracle.decode_mode_b(cpu, plan, cbs, q, gqa, 5e5))
+        log(f"  max abs err {err:.3e}")
+        assert err <= TOL, name
+
+
 def test_decode_masked_positions(gpu):
     # slots with position -1 are excluded even inside full pages
     wl = synth.make_decode_workload(1, ctx_override=512)
