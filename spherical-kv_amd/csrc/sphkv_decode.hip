@@ -305,7 +305,7 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
 // Rotation by N lanes within each 16-lane row (DPP row_ror).
 template <int N>
 __device__ __forceinline__ float row_ror(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, true));
 }
 
 // Max / sum over the 16 lanes l' with l' = l (mod 4): the four lanes of each
@@ -527,8 +527,9 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
     if (lane < NJ) {
       // lane = frequency j: dims j and j + NJ are element kk = j mod (DH/8)
-      // and kk + DH/8 of quarter j / (DH/8)
-      const int j = lane_v % NJ;
+      // and kk + DH/8 of quarter j / (DH/8) (loop-invariant addresses, kept
+      // in registers)
+      const int j = lane % NJ;
       const float2 z = turn_phasor((double)t_mid * ftab[j]);
       const int kk = j % (DH / 8), uq = j / (DH / 8);
       float* q0 = qr + (kk >> 2) * L::kq_stride + uq * 16 + (kk & 3);
