@@ -75,7 +75,7 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
 # with `bench.py --calibrate` under rocprofv3 --pmc (summary and commands in
 # profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
-TRAFFIC_BYTES = {(2, "default"): 85611095}
+TRAFFIC_BYTES = {(2, "default"): 85592537}
 
 
 def measured_traffic(config, layout):

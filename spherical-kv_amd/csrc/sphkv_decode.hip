@@ -223,7 +223,11 @@ struct DecodeLds {
   static constexpr int kq_stride = 68;
   static constexpr int qs_floats = (DH / 16) * kq_stride;
   static constexpr int o_qr = o_stage + kWaves * 512;
-  static constexpr int qr_wave = NHS * qs_floats * 4;            // bytes per wave
+  // GQA > 4 keeps QK on the fp16 16x16x32 MFMA (16 output columns hold 8
+  // heads at once): query rows split hi + lo, [2][GQA][DH + 8] halves
+  static constexpr bool kF32QK = GQA <= 4;
+  static constexpr int qrow = DH + 8;
+  static constexpr int qr_wave = kF32QK ? NHS * qs_floats * 4 : 2 * GQA * qrow * 2;   // bytes per wave
   static constexpr int o_pt = o_qr + kWaves * qr_wave;
   static constexpr int total = o_pt + kWaves * PR * 32;
   // the end-of-item wave merge reuses the space: [kWaves][GQA][DH] acc,
@@ -302,6 +306,36 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
   return float2{__builtin_amdgcn_cosf(ph), __builtin_amdgcn_sinf(ph)};
 }
 
+// x = hi + lo with hi, lo fp16: hi = x rounded toward zero (v_cvt_pkrtz), lo =
+// fp16(x - hi) formed by one mixed-precision FMA per half (fp32 x, fp16 hi)
+// that writes that half of the packed result.  The pair carries x to about
+// 2^-22 relative, so products on the fp16 MFMA lose nothing that matters
+// against the 2e-3 tolerance.  The FMAs are inline asm (the compiler forms
+// them only when fp32 denormals are flushed); the s_nop after each covers the
+// forwarding hazard of a partial (one-half) VGPR write, which the compiler's
+// hazard recognizer does not track through inline asm.  Inputs are never the
+// direct result of a transcendental instruction.
+__device__ __forceinline__ uint32_t pk_rtz(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+__device__ __forceinline__ uint32_t pk_rest(float a, float b, uint32_t hi) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "s_nop 0\n\t"
+      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "s_nop 0"
+      : "=&v"(d) : "v"(a), "v"(b), "v"(hi));
+  return d;
+}
+__device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8& lo) {
+  uint4 h, l;
+  h.x = pk_rtz(x[0], x[1]); h.y = pk_rtz(x[2], x[3]); h.z = pk_rtz(x[4], x[5]); h.w = pk_rtz(x[6], x[7]);
+  l.x = pk_rest(x[0], x[1], h.x); l.y = pk_rest(x[2], x[3], h.y);
+  l.z = pk_rest(x[4], x[5], h.z); l.w = pk_rest(x[6], x[7], h.w);
+  hi = __builtin_bit_cast(half8, h);
+  lo = __builtin_bit_cast(half8, l);
+}
+
 // Rotation by N lanes within each 16-lane row (DPP row_ror).
 template <int N>
 __device__ __forceinline__ float row_ror(float x) {
@@ -373,6 +407,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int u = lane >> 4;
   uint8_t* st = smem + L::o_stage + wave * 512;
   float* qr = reinterpret_cast<float*>(smem + L::o_qr + wave * L::qr_wave);
+  _Float16* qrh = reinterpret_cast<_Float16*>(qr);   // the fp16 form's [hi, lo][GQA][qrow]
 
   int p = rb + wave * rstride;
   const Res rs = make_res(a);
@@ -531,16 +566,35 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       // in registers)
       const int j = lane % NJ;
       const float2 z = turn_phasor((double)t_mid * ftab[j]);
-      const int kk = j % (DH / 8), uq = j / (DH / 8);
-      float* q0 = qr + (kk >> 2) * L::kq_stride + uq * 16 + (kk & 3);
-      float* q1 = q0 + (DH / 32) * L::kq_stride;
+      if constexpr (L::kF32QK) {
+        const int kk = j % (DH / 8), uq = j / (DH / 8);
+        float* q0 = qr + (kk >> 2) * L::kq_stride + uq * 16 + (kk & 3);
+        float* q1 = q0 + (DH / 32) * L::kq_stride;
 #pragma unroll
-      for (int hh = 0; hh < GQA; ++hh) {
-        const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
-        const float a0 = (float)qp[0], a1 = (float)qp[1];
-        const int o = (hh >> 2) * L::qs_floats + (hh & 3) * 4;
-        q0[o] = a0 * z.x + a1 * z.y;
-        q1[o] = a1 * z.x - a0 * z.y;
+        for (int hh = 0; hh < GQA; ++hh) {
+          const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
+          const float a0 = (float)qp[0], a1 = (float)qp[1];
+          const int o = (hh >> 2) * L::qs_floats + (hh & 3) * 4;
+          q0[o] = a0 * z.x + a1 * z.y;
+          q1[o] = a1 * z.x - a0 * z.y;
+        }
+      } else {
+#pragma unroll
+        for (int hh = 0; hh < GQA; ++hh) {
+          const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
+          const float a0 = (float)qp[0], a1 = (float)qp[1];
+          const float r0 = a0 * z.x + a1 * z.y;
+          const float r1 = a1 * z.x - a0 * z.y;
+          const uint32_t hp = pk_rtz(r0, r1);
+          const half2v hi = __builtin_bit_cast(half2v, hp);
+          const half2v lo = __builtin_bit_cast(half2v, pk_rest(r0, r1, hp));
+          _Float16* qh = qrh + hh * L::qrow;
+          _Float16* ql = qrh + (GQA + hh) * L::qrow;
+          qh[j] = hi[0];
+          qh[j + NJ] = hi[1];
+          ql[j] = lo[0];
+          ql[j + NJ] = lo[1];
+        }
       }
     }
 
@@ -571,11 +625,18 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     //      4 = (quarter u, token group), A = k_rot of token t (row t % 4),
     //      B = the rotated query of head slot lane % 4 (column), one
     //      dimension per instruction; chunks c and c + NP accumulate apart.
+    //      (GQA > 4: split hi + lo fp16 and S^T = K_rot q_rot^T on the
+    //      16x16x32 MFMA as hi*hi + lo*hi + hi*lo; lane (u, hl) gets head hl,
+    //      tokens 4u..4u+3.)
     floatx4 Sa[NHS], Sb[NHS];
 #pragma unroll
     for (int hs = 0; hs < NHS; ++hs) { Sa[hs] = (floatx4){0.f, 0.f, 0.f, 0.f}; Sb[hs] = Sa[hs]; }
+    floatx4 S = {0.f, 0.f, 0.f, 0.f};
+    const int hl = lane_v & 15;
     {
       const float* qb = qr + (u * 4 + (lane_v & 3)) * 4;
+      const _Float16* qh = qrh + (hl % GQA) * L::qrow;
+      const _Float16* ql = qh + GQA * L::qrow;
       const int dl = valid ? pos_c - t_mid : 0;
       const int ad = dl < 0 ? -dl : dl;
       const bool near = ad < kDelta;
@@ -622,61 +683,113 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
           x0[s] = k0[s] * pc[s] - k1[s] * ps[s];
           x1[s] = k1[s] * pc[s] + k0[s] * ps[s];
         }
+        if constexpr (!L::kF32QK) {
+          half8 kh0, kl0, kh1, kl1;
+          split_f16(x0, kh0, kl0);
+          split_f16(x1, kh1, kl1);
+          const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u, d1 = chunk_dim<DH>(c + NP, 0) + (DH / 8) * u;
+          const half8 qa0 = *reinterpret_cast<const half8*>(qh + d0);
+          const half8 qb0 = *reinterpret_cast<const half8*>(ql + d0);
+          const half8 qa1 = *reinterpret_cast<const half8*>(qh + d1);
+          const half8 qb1 = *reinterpret_cast<const half8*>(ql + d1);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qa0, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qa0, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qb0, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qa1, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qa1, S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qb1, S, 0, 0, 0);
+        } else {
 #pragma unroll
-        for (int hs = 0; hs < NHS; ++hs) {
-          const float* qs = qb + hs * L::qs_floats;
-          const floatx4 qa0 = *reinterpret_cast<const floatx4*>(qs + (2 * c) * L::kq_stride);
-          const floatx4 qa1 = *reinterpret_cast<const floatx4*>(qs + (2 * c + 1) * L::kq_stride);
-          const floatx4 qc0 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP)) * L::kq_stride);
-          const floatx4 qc1 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP) + 1) * L::kq_stride);
+          for (int hs = 0; hs < NHS; ++hs) {
+            const float* qs = qb + hs * L::qs_floats;
+            const floatx4 qa0 = *reinterpret_cast<const floatx4*>(qs + (2 * c) * L::kq_stride);
+            const floatx4 qa1 = *reinterpret_cast<const floatx4*>(qs + (2 * c + 1) * L::kq_stride);
+            const floatx4 qc0 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP)) * L::kq_stride);
+            const floatx4 qc1 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP) + 1) * L::kq_stride);
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[s], qa0[s], Sa[hs], 0, 0, 0);
-            Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[s], qc0[s], Sb[hs], 0, 0, 0);
-          }
+            for (int s = 0; s < 4; ++s) {
+              Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[s], qa0[s], Sa[hs], 0, 0, 0);
+              Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[s], qc0[s], Sb[hs], 0, 0, 0);
+            }
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[4 + s], qa1[s], Sa[hs], 0, 0, 0);
-            Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[4 + s], qc1[s], Sb[hs], 0, 0, 0);
+            for (int s = 0; s < 4; ++s) {
+              Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[4 + s], qa1[s], Sa[hs], 0, 0, 0);
+              Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[4 + s], qc1[s], Sb[hs], 0, 0, 0);
+            }
           }
         }
       }
     }
 
-    // ---- online softmax over the page, per head, in the log2 domain:
-    //      after the quarter sum lane l holds token tk, head slot 4 hs + l % 4
     const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
-    const int tk = 4 * ((lane_v >> 2) & 3) + ((0xD8 >> (2 * (lane_v >> 4))) & 3);
-    const bool tv = (vmask >> tk) & 1u;
-    float alpha[NHS];
-    bool upd_any = false;
+    if constexpr (L::kF32QK) {
+      // ---- online softmax over the page, per head, in the log2 domain:
+      //      after the quarter sum lane l holds token tk, head slot 4 hs + l % 4
+      const int tk = 4 * ((lane_v >> 2) & 3) + ((0xD8 >> (2 * (lane_v >> 4))) & 3);
+      const bool tv = (vmask >> tk) & 1u;
+      float alpha[NHS];
+      bool upd_any = false;
 #pragma unroll
-    for (int hs = 0; hs < NHS; ++hs) {
-      // the cross-lane sum runs on every lane (never under the token mask)
-      const float lg = quarter_sum(Sa[hs] + Sb[hs]);
-      const float x = tv ? lg * a.scale_log2 : -INFINITY;
-      const float mx = head_max(x);
-      const bool upd = mx > m_run[hs] + kRescaleLog2;
-      const float m_new = upd ? mx : m_run[hs];
-      alpha[hs] = upd ? __builtin_amdgcn_exp2f(m_run[hs] - m_new) : 1.f;
-      const _Float16 ph = (_Float16)(tv ? __builtin_amdgcn_exp2f(x - m_new) : 0.f);
-      l_run[hs] = alpha[hs] * l_run[hs] + head_sum((float)ph);
-      m_run[hs] = m_new;
-      upd_any |= upd;
-      // ---- P[head][token] for the PV MFMA's A operand
-      if (4 * hs + (lane_v & 3) < GQA) pt[(4 * hs + (lane_v & 3)) * kTile + tk] = ph;
-    }
-    if (__ballot(upd_any) != 0) {
-      // head 4 hs + i's factor lives in lane i; accumulators hold heads
-      // 4 hs + i in element i
+      for (int hs = 0; hs < NHS; ++hs) {
+        // the cross-lane sum runs on every lane (never under the token mask)
+        const float lg = quarter_sum(Sa[hs] + Sb[hs]);
+        const float x = tv ? lg * a.scale_log2 : -INFINITY;
+        const float mx = head_max(x);
+        const bool upd = mx > m_run[hs] + kRescaleLog2;
+        const float m_new = upd ? mx : m_run[hs];
+        alpha[hs] = upd ? __builtin_amdgcn_exp2f(m_run[hs] - m_new) : 1.f;
+        const _Float16 ph = (_Float16)(tv ? __builtin_amdgcn_exp2f(x - m_new) : 0.f);
+        l_run[hs] = alpha[hs] * l_run[hs] + head_sum((float)ph);
+        m_run[hs] = m_new;
+        upd_any |= upd;
+        // ---- P[head][token] for the PV MFMA's A operand
+        if (4 * hs + (lane_v & 3) < GQA) pt[(4 * hs + (lane_v & 3)) * kTile + tk] = ph;
+      }
+      if (__ballot(upd_any) != 0) {
+        // head 4 hs + i's factor lives in lane i; accumulators hold heads
+        // 4 hs + i in element i
 #pragma unroll
-      for (int hs = 0; hs < NHS; ++hs)
+        for (int hs = 0; hs < NHS; ++hs)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[hs]), i));
+          for (int i = 0; i < 4; ++i) {
+            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[hs]), i));
 #pragma unroll
-          for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
-        }
+            for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
+          }
+      }
+    } else {
+      // ---- (GQA > 4) lane (u, hl): head hl, tokens 4u..4u+3; state m_run[0]
+      float x[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        x[s] = ((vmask >> (4 * u + s)) & 1u) ? S[s] * a.scale_log2 : -INFINITY;
+      const float mx = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+      const bool upd = mx > m_run[0] + kRescaleLog2;
+      const float m_new = upd ? mx : m_run[0];
+      const float alpha = upd ? __builtin_amdgcn_exp2f(m_run[0] - m_new) : 1.f;
+      half4 pa;
+      float es = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float e = (x[s] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[s] - m_new);
+        pa[s] = (_Float16)e;
+        es += (float)pa[s];
+      }
+      l_run[0] = alpha * l_run[0] + rows_sum(es);
+      m_run[0] = m_new;
+      if (__ballot(upd) != 0) {
+        // head h's factor lives in lane h (row u = 0); accumulators hold heads
+        // 4 hs + i in element i
+#pragma unroll
+        for (int hs = 0; hs < NHS; ++hs)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 * hs + i));
+#pragma unroll
+            for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
+          }
+      }
+      if (hl < GQA) *reinterpret_cast<half4*>(pt + hl * kTile + 4 * u) = pa;
     }
 
     // ---- O += P V on the 4x4x4 MFMA (16 blocks = 16 groups of 4 dims):
@@ -740,12 +853,17 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       if (4 * hs + i < GQA)
 #pragma unroll
         for (int hf = 0; hf < NHF; ++hf) mrg[(wave * GQA + 4 * hs + i) * DH + 64 * hf + lane] = acc[hs][hf][i];
+  if constexpr (L::kF32QK) {
 #pragma unroll
-  for (int hs = 0; hs < NHS; ++hs)
-    if (lane < 4 && 4 * hs + lane < GQA) {
-      mrg_ml[(wave * GQA + 4 * hs + lane) * 2] = m_run[hs];
-      mrg_ml[(wave * GQA + 4 * hs + lane) * 2 + 1] = l_run[hs];
-    }
+    for (int hs = 0; hs < NHS; ++hs)
+      if (lane < 4 && 4 * hs + lane < GQA) {
+        mrg_ml[(wave * GQA + 4 * hs + lane) * 2] = m_run[hs];
+        mrg_ml[(wave * GQA + 4 * hs + lane) * 2 + 1] = l_run[hs];
+      }
+  } else if ((lane & 15) < GQA && lane < 16) {
+    mrg_ml[(wave * GQA + lane) * 2] = m_run[0];
+    mrg_ml[(wave * GQA + lane) * 2 + 1] = l_run[0];
+  }
   __syncthreads();
   // every output thread derives its head's wave weights 2^(m_w - M) itself
   // (the kWaves reads of a head hit one LDS address each: broadcasts), so
