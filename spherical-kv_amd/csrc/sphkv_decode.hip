@@ -35,7 +35,9 @@
 //   4. S[t][h] = k_rot . q_rot_h on the fp32 MFMA (4x4x1, 16 blocks = 4 lane
 //      quarters x 4 token groups, one dimension per instruction), then the
 //      quarters' partial sums are added with row swaps: fp32 products and
-//      sums, no operand splitting;
+//      sums, no operand splitting.  GQA > 4 uses the fp16 16x16x32 MFMA
+//      instead (its 16 output columns hold all heads), both operands split
+//      hi + lo fp16 (hi*hi + lo*hi + hi*lo, about fp32 accuracy);
 //   5. online softmax in the log2 domain.  The running reference max of a head
 //      only moves when a page's max exceeds it by more than 2^8, so the
 //      accumulator rescale is rare; p = 2^(s - m) <= 256 is rounded to fp16 and
