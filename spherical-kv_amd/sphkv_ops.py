@@ -406,13 +406,16 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
     if nw < 0:
         raise ValueError("bad planner sizes")
     work = torch.empty(max(nw, 1), dtype=torch.int32, device=dev)
-    row_start = torch.zeros(num_sh + 1, dtype=torch.int32, device=dev)
-    totals = torch.zeros(4, dtype=torch.int32, device=dev)
+    # totals and row_start in one buffer: phase 1 completes both, so one copy
+    # to the host (the planner's only synchronisation) brings back both
+    meta = torch.zeros(4 + num_sh + 1, dtype=torch.int32, device=dev)
+    totals, row_start = meta[:4], meta[4:]
     rc = lib.sphkv_plan_pages_count(tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), num_seqs, int(num_kv),
                                     max_len, int(dh), work.data_ptr(), work.numel(), row_start.data_ptr(),
                                     totals.data_ptr(), _stream())
     check(rc, "sphkv_plan_pages_count")
-    rows, nbytes, bad, ovf = (int(x) for x in totals.cpu())
+    meta_h = meta.cpu().numpy()
+    rows, nbytes, bad, ovf = (int(x) for x in meta_h[:4])
     if bad:
         raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")
     if nbytes < 0 or ovf:
@@ -430,7 +433,7 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
         _ptr(out["src_rows"]), _stream())
     check(rc, "sphkv_plan_pages_fill")
     return DevicePlan(dh=int(dh), page_size=16, num_seqs=num_seqs, num_kv=int(num_kv), pages_bytes=nbytes,
-                      num_vpages=rows, rows=rows, row_start=row_start.cpu().numpy(), **out)
+                      num_vpages=rows, rows=rows, row_start=meta_h[4:].copy(), **out)
 
 
 def build_pool_gpu(wl, device="cuda", rows_per_item: Optional[int] = None, with_codes: bool = False):
