@@ -14,8 +14,11 @@ Contents and the reference lines each part restates (reference repo paths):
 * numpy part, fp64:
   unpack_page                 inverse of pagebuilder.py:8-33
   build_pool                  spherical_kv_pipeline.py:1187-1213 (encode +
-                              page + pointer-table row per chunk), placed as the
-                              plan says
+                              page + pointer-table row per chunk) over the
+                              chunks of oracle/paging.py's restatement of the
+                              grouping (:1156-1163), placed as the plan says
+* paging.py: retained_tokens, group_pages, page_offsets, build_per_head_pages,
+  check_plan (spherical_kv_pipeline.py:1146-1228, allocation.py:28-37, 207-217)
   decode_mode_b               spherical_kv_pipeline.py:2143-2177 (back-rotated,
                               per-group-normalised q, clipped cosine, radius,
                               / sqrt(dh)), softmax :2347-2348, attn @ V :2364-2367;
@@ -175,38 +178,49 @@ def v_page_rows(v_pool: np.ndarray, vs: int, n: int, dh: int) -> np.ndarray:
 
 def build_pool(wl, with_codes: bool = False):
     """Encode every page of a synthetic workload on the CPU and place it as the
-    plan says.  Returns dict(pages uint8, v_pool fp16 [nv, 16*dh], and, if
-    with_codes, r [P, ps, Gmax] fp32 / codes [P, ps, Gmax] int32)."""
+    plan says.  The pages' token sets come from the oracle's own restatement
+    of the reference grouping (oracle/paging.py: retained tokens -> groups by
+    (seq, head, tier) -> sorted chunks); the plan's rows are first checked to
+    be exactly those chunks (paging.check_plan), so only the placement (byte
+    offsets, V slots) is taken from the plan.  Returns dict(pages uint8,
+    v_pool fp16 [nv, 16*dh], and, if with_codes, r [P, ps, Gmax] fp32 /
+    codes [P, ps, Gmax] int32)."""
+    from oracle import paging
     plan = wl.plan
     dh, ps = wl.dh, plan.page_size
+    groups = paging.group_pages(paging.retained_tokens(wl.tier_of, plan.num_seqs, plan.num_kv), ps)
+    paging.check_plan(plan, groups, positions_of=getattr(wl, "positions", None))
     pages = np.zeros(plan.pages_bytes, np.uint8)
     v_pool = np.zeros((plan.num_vpages, ps * dh), np.float16)
     vidx = v_page_index(dh)
     krows = wl.k_rows()
     vrows = wl.v_rows()
-    src = wl.src_rows()
+    base = wl.row_base()
     Gmax = dh // 16
     r_all = np.zeros((plan.num_rows, ps, Gmax), np.float32)
     c_all = np.zeros((plan.num_rows, ps, Gmax), np.int32)
-    for p in range(plan.num_rows):
-        tid, n = int(plan.tier[p]), int(plan.count[p])
-        rows = src[p, :n]
-        off, th, rad = (int(x) for x in plan.ptable[p])
-        v_pool[plan.vslot[p], vidx[:n]] = vrows[rows]
-        if tid == DENSE_TIER_ID:
-            pages[off] = tid
-            pages[off + 1] = n
-            pages[th:th + n * dh * 2] = np.frombuffer(krows[rows].astype(np.float16).tobytes(), np.uint8)
-            continue
-        g, b = TIER_GEOMETRY[tid]
-        h = int(plan.seq_head[p]) % plan.num_kv
-        cb = wl.codebooks[tid][h]
-        r, codes = encode_groups(krows[rows].astype(np.float32), cb)
-        page = build_page(r, codes, tid, b)
-        pages[off:off + page.size] = page
-        G = dh // g
-        r_all[p, :n, :G] = r
-        c_all[p, :n, :G] = codes
+    for sh in range(plan.num_seqs * plan.num_kv):
+        s, h = divmod(sh, plan.num_kv)
+        p = int(plan.row_start[sh])
+        for tid, chunks in groups.get((s, h), []):
+            for chunk in chunks:
+                n = len(chunk)
+                rows = base[sh] + np.asarray(chunk, np.int64)
+                off, th, rad = (int(x) for x in plan.ptable[p])
+                v_pool[plan.vslot[p], vidx[:n]] = vrows[rows]
+                if tid == DENSE_TIER_ID:
+                    pages[off] = tid
+                    pages[off + 1] = n
+                    pages[th:th + n * dh * 2] = np.frombuffer(krows[rows].astype(np.float16).tobytes(), np.uint8)
+                else:
+                    g, b = TIER_GEOMETRY[tid]
+                    r, codes = encode_groups(krows[rows].astype(np.float32), wl.codebooks[tid][h])
+                    page = build_page(r, codes, tid, b)
+                    pages[off:off + page.size] = page
+                    G = dh // g
+                    r_all[p, :n, :G] = r
+                    c_all[p, :n, :G] = codes
+                p += 1
     out = {"pages": pages, "v_pool": v_pool}
     if with_codes:
         out["r"] = r_all

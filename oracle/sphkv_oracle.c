@@ -26,10 +26,15 @@
  *     reduction with 8-wide vectors.)
  *   - einsum 'ngi,gci->ngc' lowers to a bmm with batch G, contraction g.
  *     When N*g*C < 400 ATen uses its own naive loop: a plain fp32
- *     multiply-then-add chain over i.  Otherwise MKL sgemm: an fmaf chain over
- *     i = 0..g-1 starting from 0.  (MKL's M=1 path, N=1 with N*g*C >= 400,
- *     uses an order that was not identified; the fmaf chain is used there too
- *     and the code is exact unless the top-2 similarity margin is a few ulp.)
+ *     multiply-then-add chain over i.  Otherwise MKL sgemm (oneMKL 2024.2,
+ *     AVX-512 host): for N >= 2 an fmaf chain over i = 0..g-1 starting from 0;
+ *     for N = 1 (reached only by g = 16, C = 64: tier 1) MKL's M = 1 kernel,
+ *     whose order was identified by exact power-of-two probes and confirmed on
+ *     random data (mkl_m1_sim16 below):
+ *       s01  = fmaf(d1, c1, d0*c0)
+ *       L_l  = d_{l+2}*c_{l+2} + d_{l+10}*c_{l+10}   (l = 0..5, products rounded)
+ *       L_6  = d8*c8,  L_7 = d9*c9 + s01
+ *       M_l  = L_l + L_{l+4} (l = 0..3); (M_0 + M_2) + (M_1 + M_3)
  *   - argmax returns the first index of the maximum (strict '>').
  * Compile without -ffast-math and with -ffp-contract=off so that every
  * fmaf / '*' / '+' / '/' below is exactly one IEEE operation.
@@ -89,6 +94,19 @@ static float torch_norm_f32(const float* x, int g)
     return sqrtf(b);
 }
 
+/* MKL's M = 1 sgemm order for a contraction of 16 (see the header). */
+static float mkl_m1_sim16(const float* d, const float* c)
+{
+    float L[8];
+    const float s01 = fmaf(d[1], c[1], d[0] * c[0]);
+    for (int l = 0; l < 6; ++l) L[l] = d[l + 2] * c[l + 2] + d[l + 10] * c[l + 10];
+    L[6] = d[8] * c[8];
+    L[7] = d[9] * c[9] + s01;
+    float M[4];
+    for (int l = 0; l < 4; ++l) M[l] = L[l] + L[l + 4];
+    return (M[0] + M[2]) + (M[1] + M[3]);
+}
+
 /*
  * spherical_kv_pipeline.py:1130-1144.
  * K: [N, G*g] fp32 row-major; cb: [G, C, g] fp32 (unit rows).
@@ -98,6 +116,7 @@ int orc_encode_groups(const float* K, int64_t N, int G, int g,
                       const float* cb, int C, float* r_out, int32_t* code_out)
 {
     const int naive = (N * (int64_t)g * C) < 400;
+    const int m1 = !naive && N == 1 && g == 16;
     float dir[64];
     for (int64_t n = 0; n < N; ++n) {
         for (int gi = 0; gi < G; ++gi) {
@@ -112,6 +131,8 @@ int orc_encode_groups(const float* K, int64_t N, int G, int g,
                 float s = 0.f;
                 if (naive) {
                     for (int i = 0; i < g; ++i) { float p = dir[i] * cbg[c * g + i]; s = s + p; }
+                } else if (m1) {
+                    s = mkl_m1_sim16(dir, cbg + c * g);
                 } else {
                     for (int i = 0; i < g; ++i) s = fmaf(dir[i], cbg[c * g + i], s);
                 }
@@ -192,19 +213,19 @@ void orc_encode_append(const float* k, const float* cb, uint8_t* theta, uint8_t*
     for (int grp = 0; grp < G; ++grp) {
         const float* kg = k + grp * g;
         float norm_sq = 0.f;
-        for (int d = 0; d < g; ++d) norm_sq = fmaf(kg[d], kg[d], norm_sq);          /* :47-48 */
-        const float norm = sqrtf(norm_sq + 1e-16f);                                 /* :49 */
-        const float inv_norm = 1.0f / (norm + 1e-8f);                               /* :50 */
+        for (int d = 0; d < g; ++d) norm_sq = fmaf(kg[d], kg[d], norm_sq);          /* :38-40 */
+        const float norm = sqrtf(norm_sq + 1e-16f);                                 /* :41 */
+        const float inv_norm = 1.0f / (norm + 1e-8f);                               /* :42 */
         const float* cbg = cb + (int64_t)grp * C * g;
         float best_sim = -1e30f;
         int best_code = 0;
-        for (int c = 0; c < C; ++c) {                                               /* :52-61 */
+        for (int c = 0; c < C; ++c) {                                               /* :45-55 */
             float sim = 0.f;
             for (int d = 0; d < g; ++d) sim = fmaf(kg[d] * inv_norm, cbg[c * g + d], sim);
             if (sim > best_sim) { best_sim = sim; best_code = c; }
         }
-        theta[code_base + grp] = (uint8_t)best_code;
-        float r_scale;                                                              /* :66-82 */
+        theta[code_base + grp] = (uint8_t)best_code;                               /* :57 */
+        float r_scale;                                                              /* :59-79 */
         if (is_new_page) {
             r_scales[pid * G_max + grp] = norm;
             r_scale = norm;
@@ -224,7 +245,7 @@ void orc_encode_append(const float* k, const float* cb, uint8_t* theta, uint8_t*
                 r_scale = prev;
             }
         }
-        float r_q = roundf(norm / (r_scale + 1e-8f) * 255.0f);                      /* :83-85 */
+        float r_q = roundf(norm / (r_scale + 1e-8f) * 255.0f);                      /* :80-82 */
         r_q = fminf(fmaxf(r_q, 0.f), 255.f);
         radius[code_base + grp] = (uint8_t)r_q;
     }

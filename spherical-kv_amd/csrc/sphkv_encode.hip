@@ -1,18 +1,24 @@
 // Fused encode + bitpack + page build + V placement (gfx950).
 //
-// One workgroup per four consecutive pages, one lane per token and one wave
-// per group; the codebook of a (tier, kv head) is read as scalar operands.
-// Per (token, group) it reproduces the torch CPU
-// operation order of _encode_keys_with_codebooks
-// (spherical_kv_pipeline.py:1136-1144) so that radii and codes are bit-exact:
-//   r   = sqrtf(sum over 8 lanes of fmaf(x, x, .) chains, lanes summed in order)
-//   dir = x / (r + 1e-8f)                     (IEEE division)
-//   sim = fmaf chain over i (torch's naive small-bmm path, N*g*C < 400:
-//         separate multiply and add)
-//   code = first index of the maximum similarity
-// then builds the page of pagebuilder.py:8-33 in LDS (header, fp32 scales,
-// LSB-first theta codes, int8 radius codes) and stores it.  This file is
-// compiled with -ffp-contract=off so no multiply/add pair is fused.
+// One 8-wave workgroup per four consecutive pages: one lane per token, one
+// wave per group in the nearest-centroid phase, then one wave per page for
+// the page build and one per page for its V placement.  Per (token, group)
+// the radius, direction and code reproduce torch CPU's operation order of
+// _encode_keys_with_codebooks (spherical_kv_pipeline.py:1136-1144) bit for
+// bit:
+//   r    = sqrtf(sum over 8 lanes of fmaf(x, x, .) chains, lanes summed in order)
+//   dir  = x / (r + 1e-8f)                     (IEEE division)
+//   code = first index of the maximum similarity, where the similarity is
+//          scored in the order of the torch path the page's size selects
+//          (code_sim / code_sim_m1 below).
+// The g = 16 tiers (1, 2) first rank all codes on v_mfma_f32_16x16x16_f16
+// with fp16 copies of the direction and the codebook rows (LDS); only the
+// codes within a proven error bound of the approximate maximum are then scored
+// exactly.  The g = 32 tier (3) scores every code exactly with the codebook
+// rows as scalar operands.  The page of pagebuilder.py:8-33 (header, fp32
+// scales, LSB-first theta codes, int8 radius codes) is built in LDS and
+// stored.  This file is compiled with -ffp-contract=off so no multiply/add
+// pair is fused except where fmaf is written.
 #include "sphkv_common.h"
 #include "sphkv_internal.h"
 
@@ -123,6 +129,25 @@ __device__ __forceinline__ float code_sim(const float* dir, const float* w) {
     else s = __builtin_fmaf(dir[i], w[i], s);
   }
   return s;
+}
+
+// torch's N = 1 path for a contraction of 16 with C = 64 (tier 1, one token:
+// N*g*C >= 400 with M = 1) runs MKL's M = 1 sgemm kernel, whose order is
+//   s01 = fmaf(d1, c1, d0*c0); L_l = d_{l+2}c_{l+2} + d_{l+10}c_{l+10} (l < 6);
+//   L_6 = d8 c8; L_7 = d9 c9 + s01; M_l = L_l + L_{l+4}; (M_0 + M_2) + (M_1 + M_3)
+// (identified with exact power-of-two probes against torch 2.10 / oneMKL
+// 2024.2 and pinned by near-tie single-token fixtures).
+__device__ __forceinline__ float code_sim_m1(const float* d, const float* c) {
+  float L[8];
+  const float s01 = __builtin_fmaf(d[1], c[1], __fmul_rn(d[0], c[0]));
+#pragma unroll
+  for (int l = 0; l < 6; ++l) L[l] = __fadd_rn(__fmul_rn(d[l + 2], c[l + 2]), __fmul_rn(d[l + 10], c[l + 10]));
+  L[6] = __fmul_rn(d[8], c[8]);
+  L[7] = __fadd_rn(__fmul_rn(d[9], c[9]), s01);
+  float M[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) M[l] = __fadd_rn(L[l], L[l + 4]);
+  return __fadd_rn(__fadd_rn(M[0], M[2]), __fadd_rn(M[1], M[3]));
 }
 
 // Codes are scored in batches of NB rows (NB * GG = 64 floats, the scalar
@@ -327,6 +352,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
         if (C < 64) mk &= (1ull << C) - 1;
         if (mk == 0) mk = C == 64 ? ~0ull : ((1ull << C) - 1);      // NaN similarities: score every code
         const bool naive = n_l * 16 * C < 400;                       // torch's own small-bmm loop
+        const bool m1 = !naive && n_l == 1;                          // MKL's M = 1 kernel
         float best_sim = 0.f;
         int best = -1;
         while (mk) {
@@ -338,7 +364,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
             const float4 v4 = *reinterpret_cast<const float4*>(&cbs[c][4 * i]);
             w[4 * i] = v4.x; w[4 * i + 1] = v4.y; w[4 * i + 2] = v4.z; w[4 * i + 3] = v4.w;
           }
-          const float sc = naive ? code_sim<16, true>(dir, w) : code_sim<16, false>(dir, w);
+          const float sc = naive ? code_sim<16, true>(dir, w) : (m1 ? code_sim_m1(dir, w) : code_sim<16, false>(dir, w));
           if (best < 0 || sc > best_sim) { best_sim = sc; best = c; }
         }
         return best;
@@ -462,9 +488,14 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
   const int64_t page_off = a.ptable[3 * p];
   const int64_t th_off = a.ptable[3 * p + 1];
   if (tid == kDenseTier) {
-    // header: tier id, count, six zero bytes; payload fp16 [n, DH]
-    if (lane < 8 && page_off + 8 <= a.pages_bytes)
-      a.pages[page_off + lane] = lane == 0 ? (uint8_t)kDenseTier : (lane == 1 ? (uint8_t)n : 0);
+    // header: tier id, count, six zero bytes; payload fp16 [n, DH] at a
+    // 16-byte aligned theta offset.  A pointer-table row that does not place
+    // the whole page inside the byte pool (negative or misaligned offsets
+    // included) writes nothing, as a compressed page's does.
+    if (page_off < 0 || page_off + 8 > a.pages_bytes || th_off < page_off + 8 || (th_off & 15) != 0 ||
+        th_off + (int64_t)n * DH * 2 > a.pages_bytes)
+      return;
+    if (lane < 8) a.pages[page_off + lane] = lane == 0 ? (uint8_t)kDenseTier : (lane == 1 ? (uint8_t)n : 0);
     for (int i = lane; i < n * DH / 8; i += kWave) {
       const int tt = i / (DH / 8), c8 = i % (DH / 8);
       const int64_t rr = a.src_rows[(int64_t)p * kTile + tt];
@@ -479,8 +510,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
       } else {
         for (int e = 0; e < 8; ++e) hv[e] = (_Float16)0.f;
       }
-      const int64_t dst = th_off + ((int64_t)tt * DH + c8 * 8) * 2;
-      if (dst + 16 <= a.pages_bytes) *reinterpret_cast<half8*>(a.pages + dst) = hv;
+      *reinterpret_cast<half8*>(a.pages + th_off + ((int64_t)tt * DH + c8 * 8) * 2) = hv;
     }
     return;
   }

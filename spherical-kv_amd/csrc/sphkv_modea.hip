@@ -6,7 +6,7 @@
 // [n_pages, page_size, dh] (token-major); per kv head a block table (logical
 // page -> pool page, -1 = none) and a bits table (logical page -> tier index);
 // cb_flat fp32 [num_kv, num_tiers, G_max, cb_max, g_max] (zero padded).
-// Radii are uint8 with r_hat = r_scale * code / 255 (decode_kernel.cu:171).
+// Radii are uint8 with r_hat = r_scale * code / 255 (decode_kernel.cu:183).
 // There is no RoPE in Mode A: q and the keys behind the codes are post-RoPE,
 // so a per-query table LUT[g][c] = <q_g, centroid_g[c]> is exact and a key's
 // logit is sum_g r_hat_g * LUT[g][code_g].
@@ -18,7 +18,7 @@
 //                      running-max radius scale.  Bit-exact with the reference
 //                      arithmetic as nvcc compiles it (a*b + c contracted to
 //                      fmaf, IEEE sqrt and divide, roundf).
-//   modea_split_kernel Mode-A decode (decode_kernel.cu:108-220): one
+//   modea_split_kernel Mode-A decode (decode_kernel.cu:108-218): one
 //                      workgroup per (kv head, range of logical pages); the
 //                      kv head's q heads share every page read; per page and q
 //                      head it writes the reference's (m, l) into
@@ -27,7 +27,7 @@
 //                      online-softmax partial (m, l, acc[dh]).
 //   modea_fast_kernel  the same for G_max 4 or 8 with vector loads and a
 //                      two-deep tile prefetch ring (the common case).
-//   modea_merge_kernel log-sum-exp merge of the ranges (decode_kernel.cu:223-246):
+//   modea_merge_kernel log-sum-exp merge of the ranges (decode_kernel.cu:221-246):
 //                      out = acc / (l + 1e-8).
 //   qlut_kernel        the per-query LUT [num_q, num_tiers, G_max, cb_max].
 //   lut_logits_kernel  logits from a given LUT (new_fused_decode.py:22-43).
@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendLaunch a) 
     a.v_pool[row * a.dh + tid] = (_Float16)a.v_new[(int64_t)h * a.dh + tid];   // round to nearest even
   }
   __syncthreads();
-  // decode_kernel.cu:46-50: norm = sqrt(sum k^2 + 1e-16), inv = 1 / (norm + 1e-8)
+  // decode_kernel.cu:38-42: norm = sqrt(sum k^2 + 1e-16), inv = 1 / (norm + 1e-8)
   if (tid < a.G) {
     const float* kg = s_k + tid * a.g;
     float nsq = 0.f;
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendLaunch a) 
     s_inv[tid] = 1.0f / (nrm + 1e-8f);
   }
   __syncthreads();
-  // decode_kernel.cu:52-58: sim_c = sum_d (k_d * inv) * cb[c][d], in d order
+  // decode_kernel.cu:45-55: sim_c = sum_d (k_d * inv) * cb[c][d], in d order
   const int nsim = a.G * a.C;
   for (int i = tid; i < nsim; i += kAppendThreads) {
     const int grp = i / a.C, c = i - grp * a.C;
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendLaunch a) 
       if (v > best) { best = v; code = c; }
     }
     a.theta_codes[row * a.G_max + grp] = (uint8_t)code;
-    // decode_kernel.cu:64-82: per-page running-max radius scale
+    // decode_kernel.cu:59-82: per-page running-max radius scale
     const float nrm = s_norm[grp];
     float* rs = a.r_scales + pid * a.G_max + grp;
     float r_scale;
@@ -135,7 +135,7 @@ __device__ __forceinline__ float lut_entry(const ModeALaunch& a, int hq, int tie
   const float* qg = a.q + (int64_t)hq * a.dh + g * gt;
   const float* cb = a.cb_flat + ((((int64_t)hkv * a.num_tiers + tier) * a.G_max + g) * a.cb_max + c) * a.g_max;
   float dot = 0.f;
-  for (int d = 0; d < gt; ++d) dot = __builtin_fmaf(qg[d], cb[d], dot);   // decode_kernel.cu:175-177 order
+  for (int d = 0; d < gt; ++d) dot = __builtin_fmaf(qg[d], cb[d], dot);   // decode_kernel.cu:187-189 order
   return dot;
 }
 
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void modea_split_kernel(ModeALaunch a) {
         for (int hp = 0; hp < NHP; ++hp) sum[hp] = 0.f;
         for (int g = 0; g < Gt; ++g) {
           const int code = th[g];
-          const float rh = rsc[g] * (float)rd[g] / 255.0f;          // decode_kernel.cu:171
+          const float rh = rsc[g] * (float)rd[g] / 255.0f;          // decode_kernel.cu:183
 #pragma unroll
           for (int hp = 0; hp < NHP; ++hp) {
             const float v = code < a.cb_max ? lt[(int64_t)hp * 4 * a.num_tiers * a.G_max * a.cb_max + g * a.cb_max + code] : 0.f;
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void modea_split_kernel(ModeALaunch a) {
   }
 }
 
-// Log-sum-exp merge of the ranges' partials (decode_kernel.cu:223-246):
+// Log-sum-exp merge of the ranges' partials (decode_kernel.cu:221-246):
 // workgroup = (q head, 64-dim chunk); wave w folds ranges w, w + 8, ... into a
 // running (m, l, acc) with four ranges' loads in flight at a time, then wave 0
 // folds the eight waves and writes out = acc / (l + 1e-8).
@@ -470,12 +470,12 @@ __global__ __launch_bounds__(64 * kMergeWaves) void modea_merge_kernel(ModeALaun
 // 255, so a logit in log2 units is sum_g r_scale_g * rcode_g * T[g][code_g]
 // and softmax runs on the hardware exp2.  Each tile's (max, sum) per q head
 // goes to LDS; after the loop the tiles of each page are combined into the
-// reference's per-page (m, l) (decode_kernel.cu:183-205, in natural units).
+// reference's per-page (m, l) (decode_kernel.cu:198-215, in natural units).
 // ---------------------------------------------------------------------------
 constexpr int kFastWaves = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kNegLogit2 = -1e9f * kLog2e;     // the reference's -1e9 logit (decode_kernel.cu:183), log2 units
+constexpr float kNegLogit2 = -1e9f * kLog2e;     // the reference's -1e9 logit (decode_kernel.cu:194), log2 units
 
 // LDS carve-up of the vector-load kernel (floats unless noted).
 struct FastLds {
@@ -719,7 +719,7 @@ __global__ __launch_bounds__(64 * kFastWaves) void modea_fast_kernel(ModeALaunch
         const float v = lt[g * CMP + (code < (uint32_t)CM ? code : (uint32_t)CM)];
         sum = __builtin_fmaf(rsg * rc, v, sum);
       }
-      lg[hp] = sum == 0.f ? kNegLogit2 : sum;                               // decode_kernel.cu:183
+      lg[hp] = sum == 0.f ? kNegLogit2 : sum;                               // decode_kernel.cu:194
     }
     bool grow = false;
     float fo[NHP];
@@ -791,7 +791,7 @@ __global__ __launch_bounds__(64 * kFastWaves) void modea_fast_kernel(ModeALaunch
     }
   __syncthreads();
 
-  // ---- per-page (m, l) of each q head from its tiles (decode_kernel.cu:199-205)
+  // ---- per-page (m, l) of each q head from its tiles (decode_kernel.cu:198-215)
   for (int i = tid; i < npg * a.kv_groups; i += 64 * W) {
     const int pl = i / a.kv_groups, h = i - pl * a.kv_groups;
     float m = -INFINITY;

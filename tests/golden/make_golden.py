@@ -15,7 +15,8 @@ not imported):
 
 Recorded with every encode case: torch version and the fp64 top-2 similarity
 margin of every group (a margin of a few 1e-7 is where summation order decides
-the argmax).
+the argmax).  The t1_n1_tie* cases are single-token tier-1 pages built on
+near-ties: they pin the summation order of torch's N = 1 path (MKL M = 1).
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -96,6 +97,37 @@ def encode_case(name, rng, N, tier_id, g, b, dh=128, kind="normal"):
             f"{name}__meta": np.array([N, tier_id, g, b, dh], np.int64)}
 
 
+def tie_case(name, rng, dh=128, tries=4096):
+    """One single-token tier-1 page (N = 1, g = 16, C = 64: the only encode
+    that reaches MKL's M = 1 sgemm) whose every group sits on a near-tie:
+    K_g ~ r * (c_a + c_b) for two random centroids a < b, rounded to fp16, and
+    of `tries` fp16 roundings of randomly perturbed copies the one with the
+    smallest fp64 top-2 margin is kept (margins of a few 1e-8 to 1e-7, where
+    the fp32 summation order decides the argmax)."""
+    g, b = 16, 6
+    G, C = dh // g, 2 ** b
+    cb = rng.standard_normal((G, C, g))
+    cb = (cb / np.linalg.norm(cb, axis=-1, keepdims=True)).astype(np.float32)
+    K = np.zeros((1, dh), np.float16)
+    for gi in range(G):
+        a, bb = rng.choice(C, size=2, replace=False)
+        base = cb[gi, a].astype(np.float64) + cb[gi, bb].astype(np.float64)
+        base *= rng.uniform(1.0, 8.0) / np.linalg.norm(base)
+        cand = (base[None, :] * (1.0 + 2e-3 * rng.standard_normal((tries, g)))).astype(np.float16)
+        d = cand.astype(np.float64)
+        d /= np.linalg.norm(d, axis=-1, keepdims=True) + EPS
+        s = d @ cb[gi].astype(np.float64).T                          # [tries, C]
+        top = np.sort(s, axis=-1)
+        pick = int(np.argmin(top[:, -1] - top[:, -2]))
+        K[0, gi * g:(gi + 1) * g] = cand[pick]
+    Kt = torch.from_numpy(K.astype(np.float32))
+    r, codes = t_encode(Kt, torch.from_numpy(cb), g, G)
+    page = t_build_page(r, codes, 1, b)
+    return {f"{name}__K": K, f"{name}__cb": cb, f"{name}__r": r.numpy(), f"{name}__codes": codes.numpy(),
+            f"{name}__page": page.numpy(), f"{name}__margin": margins(K, cb, g, G).astype(np.float64),
+            f"{name}__meta": np.array([1, 1, g, b, dh], np.int64)}
+
+
 def decode_case(name, rng, n_tok, gqa, dh, theta=500000.0):
     """Torch fp32 restatement of the Mode-B reference decode on one KV head
     with one tier-1 block, positions spread over [0, 40000)."""
@@ -147,7 +179,15 @@ def main():
     enc.update(encode_case("t1_zero", rng, 16, 1, 16, 6, kind="zeros"))
     for i in range(24):                                        # 384 more tier-1 tokens, config-3 data
         enc.update(encode_case(f"t1_bulk{i}", rng, 16, 1 + (i % 2), 16, 6 - 2 * (i % 2), kind="config3"))
+    # single-token tier-1 pages on near-ties (MKL's M = 1 order decides the
+    # codes); their own generator, so the cases above are unchanged
+    rng_t = np.random.default_rng(20261202)
+    for i in range(48):
+        enc.update(tie_case(f"t1_n1_tie{i}", rng_t, dh=128))
+    for i in range(16):
+        enc.update(tie_case(f"t1_n1_tie_dh64_{i}", rng_t, dh=64))
     enc["torch_version"] = np.array(torch.__version__)
+    enc["blas"] = np.array("oneMKL 2024.2 (torch CPU, AVX-512 host)")
     np.savez_compressed(os.path.join(HERE, "encode_golden.npz"), **enc)
 
     dec = {}
