@@ -43,6 +43,7 @@ extern "C" {
 #define SPHKV_EINVAL (-1)   /* bad argument (shape, size, alignment, null) */
 #define SPHKV_ELAUNCH (-2)  /* a kernel launch failed */
 #define SPHKV_EDEVICE (-3)  /* no usable device / wrong architecture */
+#define SPHKV_EPAGE (-4)    /* the decode skipped malformed pointer-table rows or pages */
 
 /* Message for the last failure on this thread ("" if none). */
 const char* sphkv_last_error(void);
@@ -81,8 +82,11 @@ int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int6
 
 /*
  * Workspace bytes sphkv_decode_paged needs for num_items work items: one
- * (m, l, acc) partial per item.  No initialisation is needed; calls that share
- * a workspace must not run concurrently.
+ * (m, l, acc) partial per item, then 16 status bytes (uint32 [0]: malformed
+ * rows / pages counted since the last merge, [1]: the count of the last
+ * merged decode).  Zero the workspace once when it is allocated (the status
+ * words must start at zero); calls that share a workspace must not run
+ * concurrently.
  */
 int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32_t dh);
 
@@ -120,6 +124,33 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
                        const uint16_t* q, uint16_t* out, void* workspace, int64_t workspace_bytes,
                        int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
                        void* stream);
+
+/*
+ * Malformed input.  The decode never reads outside the buffers it is given;
+ * a pointer-table row that does not address the pools, a page whose tier id
+ * is not 1, 2, 3 or 0xFF, a count above page_size, a dense page whose K rows
+ * are not 16-byte aligned inside its theta section, or a compressed page
+ * whose sections leave the byte pool (or the 512 bytes from its page's 16-byte
+ * line) contributes no token, and is counted in the workspace's status word.
+ *
+ * sphkv_decode_paged_status: waits for `stream` and returns in *malformed the
+ * count of the last merged decode on this workspace (0 for a well-formed pool).
+ * sphkv_decode_paged_checked: sphkv_decode_paged followed by that wait;
+ * returns SPHKV_EPAGE when the count is non-zero (the output is still written,
+ * without the skipped pages).  Neither has a reference counterpart: the
+ * reference launches without any check (decode_kernel.cu:262-288).
+ */
+int sphkv_decode_paged_status(const void* workspace, int64_t workspace_bytes, int32_t num_items, int32_t gqa,
+                              int32_t dh, int32_t* malformed, void* stream);
+int sphkv_decode_paged_checked(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                               const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                               const uint16_t* v_pool, int64_t num_vpages,
+                               const float* cb1, const float* cb2, const float* cb3,
+                               const int32_t* work, int32_t num_items, const int32_t* work_start,
+                               int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                               const uint16_t* q, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                               int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                               void* stream);
 
 /*
  * The two phases of sphkv_decode_paged as separate calls, for callers that

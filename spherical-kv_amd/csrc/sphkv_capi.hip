@@ -12,10 +12,15 @@ namespace {
 
 thread_local char g_err[512] = "";
 
+int fail_v(int code, const char* fmt, va_list ap) {
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  return code;
+}
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  fail_v(code, fmt, ap);
   va_end(ap);
   return code;
 }
@@ -66,7 +71,7 @@ int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int6
 
 int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32_t dh) {
   if (num_items < 0 || !gqa_ok(gqa) || !dh_ok(dh)) return -1;
-  return (int64_t)num_items * sphkv::partial_floats(gqa, dh) * (int64_t)sizeof(float);
+  return sphkv::decode_workspace_bytes(num_items, gqa, dh);
 }
 
 }  // extern "C"
@@ -90,11 +95,15 @@ int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_
   if ((phases & sphkv::kPhasePartials) &&
       (pages_bytes < 0 || pages_bytes > 0x7FFFFF00LL || (int64_t)num_rows * 64 > 0x7FFFFF00LL))
     return fail(SPHKV_EINVAL, "%s: byte pool and pointer table must stay below 2 GiB", fn);
+  // V pages are addressed with 64-bit offsets; vslot is int32, so a larger
+  // pool could not be indexed in full
+  if ((phases & sphkv::kPhasePartials) && (num_vpages < 0 || num_vpages > (int64_t)1 << 31))
+    return fail(SPHKV_EINVAL, "%s: num_vpages must be in [0, 2^31] (int32 vslot)", fn);
+  if (num_seqs == 0) return ok();
   const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
   if (workspace_bytes < need)
     return fail(SPHKV_EINVAL, "%s: workspace too small (%lld < %lld bytes)", fn,
                 (long long)workspace_bytes, (long long)need);
-  if (num_seqs == 0) return ok();
   if (num_items < num_seqs * num_kv)
     return fail(SPHKV_EINVAL, "%s: need at least one work item per (seq, head)", fn);
   if (!work_start || !workspace) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
@@ -125,6 +134,46 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
                      ptable, vslot, positions, num_rows, v_pool, num_vpages, cb1, cb2, cb3, work,
                      num_items, work_start, num_seqs, num_kv, gqa, q, out, workspace, workspace_bytes,
                      dh, page_size, sm_scale, rope_theta, stream);
+}
+
+int sphkv_decode_paged_status(const void* workspace, int64_t workspace_bytes, int32_t num_items, int32_t gqa,
+                              int32_t dh, int32_t* malformed, void* stream) {
+  const char* fn = "sphkv_decode_paged_status";
+  if (!malformed) return fail(SPHKV_EINVAL, "%s: null output", fn);
+  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
+  if (need < 0 || workspace_bytes < need || !workspace)
+    return fail(SPHKV_EINVAL, "%s: workspace of %lld bytes does not hold %d items", fn,
+                (long long)workspace_bytes, num_items);
+  uint32_t st = 0;
+  const uint8_t* src = static_cast<const uint8_t*>(workspace) + need - sphkv::kDecodeStatusBytes + 4;
+  hipError_t e = hipMemcpyAsync(&st, src, 4, hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return fail(SPHKV_ELAUNCH, "%s: %s", fn, hipGetErrorString(e));
+  *malformed = (int32_t)(st > 0x7FFFFFFFu ? 0x7FFFFFFFu : st);
+  return ok();
+}
+
+int sphkv_decode_paged_checked(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                               const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                               const uint16_t* v_pool, int64_t num_vpages,
+                               const float* cb1, const float* cb2, const float* cb3,
+                               const int32_t* work, int32_t num_items, const int32_t* work_start,
+                               int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                               const uint16_t* q, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                               int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                               void* stream) {
+  const char* fn = "sphkv_decode_paged_checked";
+  int rc = decode_call(fn, sphkv::kPhasePartials | sphkv::kPhaseMerge, pages, pages_bytes, ptable, vslot,
+                       positions, num_rows, v_pool, num_vpages, cb1, cb2, cb3, work, num_items, work_start,
+                       num_seqs, num_kv, gqa, q, out, workspace, workspace_bytes, dh, page_size, sm_scale,
+                       rope_theta, stream);
+  if (rc != SPHKV_OK || num_seqs == 0) return rc;
+  int32_t bad = 0;
+  rc = sphkv_decode_paged_status(workspace, workspace_bytes, num_items, gqa, dh, &bad, stream);
+  if (rc != SPHKV_OK) return rc;
+  if (bad != 0)
+    return fail(SPHKV_EPAGE, "%s: %d malformed pointer-table rows or pages were skipped", fn, bad);
+  return ok();
 }
 
 int sphkv_decode_paged_partials(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,

@@ -64,6 +64,7 @@ struct DecodeArgs {
   const _Float16* q;
   _Float16* out;
   float* partials;
+  uint32_t* status;      // [0]: malformed rows / pages seen (accumulates until a merge)
   int32_t num_kv;
   int32_t num_rows;
   int32_t num_sh;        // num_seqs * num_kv
@@ -95,7 +96,8 @@ __device__ __forceinline__ Res make_res(const DecodeArgs& a) {
 struct RowLd { int x, y; };
 struct Row {
   int page_off, th_off, rad_off, vs;
-  bool ok;
+  bool ok;         // the row is present and addresses the pools
+  bool present;    // the row is one of the item's (p < end)
 };
 
 __device__ __forceinline__ RowLd row_issue(const Res& rs, int p, int re, int lane) {
@@ -112,6 +114,7 @@ __device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int
   r.th_off = __builtin_amdgcn_readlane(l.x, 1);
   r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
   r.vs = __builtin_amdgcn_readlane(l.y, 3);
+  r.present = p < re;
   r.ok = p < re && r.page_off >= 0 && (int64_t)r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
          r.vs >= 0 && r.vs < a.num_vpages;
   if (!r.ok) { r.page_off = 0; r.th_off = 0; r.rad_off = 0; r.vs = 0; }
@@ -144,7 +147,8 @@ __device__ __forceinline__ int load_pos(const Res& rs, const Row& r, int p, int 
 // 4x4x4 PV MFMA.
 template <int DH>
 __device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int lane, half8 (&vreg)[DH / 32]) {
-  const rsrc_t rs = make_rsrc(a.v_pool + r.vs * DH * kTile, r.ok ? DH * kTile * 2 : 0);
+  // 64-bit element offset: vslot * DH * 16 exceeds 2^31 from vslot 2^20 (DH 128)
+  const rsrc_t rs = make_rsrc(a.v_pool + (int64_t)r.vs * (DH * kTile), r.ok ? DH * kTile * 2 : 0);
 #pragma unroll
   for (int hf = 0; hf < DH / 64; ++hf)
 #pragma unroll
@@ -516,6 +520,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
 
   int pages_done = 0;                                   // pages of this wave processed so far
+  int nbad = 0;                                         // malformed rows / pages of this wave
   // One page of the pipeline.  The staging window and positions of the next
   // page are loaded into the other register set of a pair, and the pointer-
   // table rows into the other slot of a pair, so the loop (unrolled by two)
@@ -551,9 +556,44 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     uint32_t hw = rel == 0 ? stg_c.x : (rel == 4 ? stg_c.y : (rel == 8 ? stg_c.z : stg_c.w));
     hw = (uint32_t)__builtin_amdgcn_readfirstlane((int)hw);
     int tid = row_c.ok ? (int)(hw & 0xFF) : 0;
-    // a dense page whose rows were not prefetched (not 16-byte aligned) is skipped
-    if (tid == kDenseTier && !row_looks_dense<DH>(row_c)) tid = 0;
-    const int n = (tid == 0) ? 0 : min((int)((hw >> 8) & 0xFF), kTile);
+    const int cnt = (int)((hw >> 8) & 0xFF);
+    // A malformed row or page contributes no token and is counted: a row that
+    // does not address the pools, an unknown tier id, a count above 16, a
+    // dense page whose K rows are not 16-byte aligned inside its section and
+    // the pool, a compressed page whose sections leave its 512-byte staging
+    // window or the pool.
+    bool bad = row_c.present && !row_c.ok;
+    if (!(tid == kDenseTier || (tid >= 1 && tid <= 3))) {
+      bad = bad || row_c.ok;
+      tid = 0;
+    }
+    if (tid != 0 && cnt > kTile) bad = true;
+    int n = (tid == 0) ? 0 : min(cnt, kTile);
+    if (tid == kDenseTier &&
+        !(row_looks_dense<DH>(row_c) && (int64_t)row_c.th_off + (int64_t)n * DH * 2 <= row_c.rad_off &&
+          (int64_t)row_c.th_off + (int64_t)n * DH * 2 <= a.pages_bytes)) {
+      bad = true;
+      tid = 0;
+      n = 0;
+    }
+    int thr = 0, rdr = 0;                       // section offsets in the staging window
+    if (tid >= 1 && tid <= 3) {
+      const int base = row_c.page_off & ~15;
+      const int thr0 = row_c.th_off - base, rdr0 = row_c.rad_off - base;   // offsets are < 2^31
+      const int G = DH / tier_g(tid);
+      const int tb = (n * G * tier_b(tid) + 7) / 8;
+      const bool sec_ok = row_c.th_off >= base && row_c.rad_off >= base && thr0 + tb + 2 < 512 &&
+                          rdr0 + n * G <= 512 && (int64_t)row_c.th_off + tb <= a.pages_bytes &&
+                          (int64_t)row_c.rad_off + n * G <= a.pages_bytes;
+      if (sec_ok) {
+        thr = thr0;
+        rdr = rdr0;
+      } else {
+        bad = true;
+        n = 0;
+      }
+    }
+    nbad += bad ? 1 : 0;
     if (!row_c.ok) pos_c = -1;
     const bool valid = (t < n) && (pos_c >= 0);
 
@@ -607,16 +647,9 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     if (tid >= 1 && tid <= 3) {
       if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
       wave_lds_sync();
-      const int base = row_c.page_off & ~15;
-      const int thr0 = row_c.th_off - base, rdr0 = row_c.rad_off - base;   // offsets are < 2^31
-      const int g = tier_g(tid), b = tier_b(tid);
-      const int G = DH / g;
-      const bool ok = row_c.th_off >= base && row_c.rad_off >= base && thr0 <= 512 && rdr0 <= 512 &&
-                      rdr0 + n * G <= 512 && thr0 + (n * G * b + 7) / 8 + 2 < 512;
-      const int thr = ok ? thr0 : 0, rdr = ok ? rdr0 : 0;
-      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
-      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
-      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, ok, cofs, rh);
+      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
+      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
+      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
     }
     wave_lds_sync();
 
@@ -843,6 +876,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   }
 
   __builtin_amdgcn_s_setprio(0);
+  if (nbad != 0 && lane == 0) __hip_atomic_fetch_add(a.status, (uint32_t)nbad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // ---- merge the waves' states in LDS, write this item's partial ----------
   constexpr int PS = partial_stride<DH, GQA>();
   __syncthreads();
@@ -905,7 +939,7 @@ template <int DH, int GQA>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ partials,
                                                            const int32_t* __restrict__ work_start,
                                                            int32_t num_items, int32_t num_kv,
-                                                           _Float16* __restrict__ out) {
+                                                           _Float16* __restrict__ out, uint32_t* status) {
   constexpr int PS = partial_stride<DH, GQA>();
   constexpr int SL = GQA * DH < 128 ? GQA * DH : 128; // floats per output slice
   constexpr int NSL = (GQA * DH) / SL;                // slices per (seq, kv head)
@@ -914,6 +948,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   __shared__ float4 red_v[IL][32];
   __shared__ float red_m[IL][32], red_l[IL][32];
   const int sh = blockIdx.x / NSL, slice = blockIdx.x % NSL;
+  // the malformed-page count of the decode calls since the last merge becomes
+  // this merge's result, and the counter restarts (stream order: every
+  // decode workgroup has finished)
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    status[1] = status[0];
+    status[0] = 0u;
+  }
   // item range of this (seq, head), clamped to the partials that exist
   const int ib = min(max(work_start[sh], 0), num_items);
   const int ni = min(max(work_start[sh + 1], ib), num_items) - ib;
@@ -984,6 +1025,7 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.num_vpages = L.num_vpages; a.cb[0] = nullptr; a.cb[1] = L.cb1; a.cb[2] = L.cb2; a.cb[3] = L.cb3;
   a.work = L.work; a.work_start = L.work_start; a.q = reinterpret_cast<const _Float16*>(L.q);
   a.out = reinterpret_cast<_Float16*>(L.out); a.partials = L.partials;
+  a.status = reinterpret_cast<uint32_t*>(L.partials + (int64_t)L.num_items * partial_stride<DH, GQA>());
   a.num_kv = L.num_kv; a.num_rows = L.num_rows; a.num_sh = L.num_seqs * L.num_kv;
   a.scale_log2 = L.sm_scale * 1.4426950408889634f;
   a.log2_theta = __builtin_log2(L.rope_theta);
@@ -995,7 +1037,7 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
     if ((phases & kPhaseMerge) && nsh > 0)
       hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
                          dim3(256), 0, stream, L.partials, L.work_start, L.num_items, L.num_kv,
-                         reinterpret_cast<_Float16*>(L.out));
+                         reinterpret_cast<_Float16*>(L.out), a.status);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

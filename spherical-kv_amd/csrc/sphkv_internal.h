@@ -122,6 +122,13 @@ int launch_ragged(const RaggedLaunch& L, hipStream_t stream);
 
 // fp32 elements of one work item's partial: 16 (m, l, padding) + gqa * dh
 inline int64_t partial_floats(int gqa, int dh) { return 16 + (int64_t)gqa * dh; }
+// The decode workspace ends with 16 status bytes after the partials: uint32
+// [0] malformed rows / pages counted by the decode kernel since the last
+// merge, [1] the count the last merge saw.
+constexpr int64_t kDecodeStatusBytes = 16;
+inline int64_t decode_workspace_bytes(int num_items, int gqa, int dh) {
+  return (int64_t)num_items * partial_floats(gqa, dh) * 4 + kDecodeStatusBytes;
+}
 
 
 }  // namespace sphkv

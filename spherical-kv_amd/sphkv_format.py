@@ -124,7 +124,7 @@ class PagePlan:
 def plan_pages(tier_of: Sequence[np.ndarray], positions_of: Optional[Sequence[np.ndarray]],
                num_seqs: int, num_kv: int, dh: int, page_size: int = 16,
                rng: Optional[np.random.Generator] = None,
-               num_vpages: Optional[int] = None) -> PagePlan:
+               num_vpages: Optional[int] = None, byte_spread: float = 1.0) -> PagePlan:
     """Group tokens by (seq, head, tier), sort, chunk into pages and place them.
 
     tier_of[s*num_kv + h] is an int array over the sequence's tokens giving the
@@ -132,7 +132,10 @@ def plan_pages(tier_of: Sequence[np.ndarray], positions_of: Optional[Sequence[np
     positions_of[s] gives each token's absolute position (default 0..L-1).
     If rng is given, pages are placed in a random physical order (random byte
     offsets and random V slots drawn from num_vpages >= P slots); otherwise in
-    logical order.
+    logical order.  byte_spread > 1 (with rng) leaves a random gap after each
+    page, uniform in [0, 2 (byte_spread - 1) x the page's bytes], so the pages
+    are scattered over a byte pool about byte_spread times their total size
+    (a shared pool that holds other sequences' pages too).
     """
     tiers_l, counts_l, toks_l, pos_l, sh_l = [], [], [], [], []
     row_start = [0]
@@ -177,7 +180,10 @@ def plan_pages(tier_of: Sequence[np.ndarray], positions_of: Optional[Sequence[np
         else:
             off = ((off + PAGE_ALIGN - 1) // PAGE_ALIGN) * PAGE_ALIGN
         ptable[p] = ptable_row(off, tid, n, dh)
-        off += page_nbytes(tid, n, dh)
+        nb = page_nbytes(tid, n, dh)
+        off += nb
+        if rng is not None and byte_spread > 1.0:
+            off += int(rng.integers(0, int(2 * (byte_spread - 1.0) * nb) + 1))
     pages_bytes = ((off + PAGE_ALIGN - 1) // PAGE_ALIGN) * PAGE_ALIGN + PAGE_ALIGN
     if pages_bytes >= 2 ** 31:
         raise ValueError("page byte pool exceeds int32 offsets")

@@ -16,6 +16,8 @@ import torch
 import sphkv_format as fmt
 from sphkv_lib import check, load
 
+_check_rc = check      # decode_paged's `check` argument shadows the name there
+
 ROWS_PER_ITEM = 64     # pointer-table rows per decode work item (8 pages per wave, 8 waves)
 
 
@@ -259,9 +261,11 @@ def encode_pages(pool: PagedPool, k: torch.Tensor, v: torch.Tensor, src_rows: to
 
 
 def _decode_workspace(pool: PagedPool, gqa: int, workspace: Optional[torch.Tensor]) -> torch.Tensor:
+    """A caller's workspace, or a new zeroed one (its trailing status words
+    must start at zero)."""
     wsb = pool.workspace_bytes(gqa)
     if workspace is None:
-        workspace = torch.empty(max(wsb, 4), dtype=torch.uint8, device=pool.device)
+        workspace = torch.zeros(max(wsb, 4), dtype=torch.uint8, device=pool.device)
     _need(workspace, torch.uint8, "workspace", pool.device)
     if workspace.numel() < wsb:
         raise ValueError(f"workspace needs {wsb} bytes, got {workspace.numel()}")
@@ -278,9 +282,12 @@ def _check_q(pool: PagedPool, q: torch.Tensor, gqa: int) -> None:
 
 def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 workspace: Optional[torch.Tensor] = None, check: bool = False) -> torch.Tensor:
     """Angle-domain paged attention decode.  q fp16 [num_seqs, num_kv*gqa, dh]
-    -> out fp16 of the same shape."""
+    -> out fp16 of the same shape.  check=True waits for the decode and raises
+    SphkvError if it skipped malformed pointer-table rows or pages
+    (sphkv_decode_paged_checked); the default call is asynchronous and leaves
+    that count in the workspace (decode_status)."""
     plan = pool.plan
     _check_q(pool, q, gqa)
     if out is None:
@@ -292,14 +299,28 @@ def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(plan.dh)
     c1, c2, c3 = pool.cb_ptrs()
-    rc = load().sphkv_decode_paged(
+    lib = load()
+    fn, name = ((lib.sphkv_decode_paged_checked, "sphkv_decode_paged_checked") if check
+                else (lib.sphkv_decode_paged, "sphkv_decode_paged"))
+    rc = fn(
         pool.pages.data_ptr(), plan.pages_bytes, pool.ptable.data_ptr(), pool.vslot.data_ptr(),
         pool.positions.data_ptr(), plan.num_rows, pool.v_pool.data_ptr(), plan.num_vpages,
         c1, c2, c3, pool.work.data_ptr(), pool.num_items, pool.work_start.data_ptr(),
         plan.num_seqs, plan.num_kv, gqa, q.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         workspace.numel(), plan.dh, plan.page_size, float(sm_scale), float(rope_theta), _stream())
-    check(rc, "sphkv_decode_paged")
+    _check_rc(rc, name)
     return out
+
+
+def decode_status(pool: PagedPool, workspace: torch.Tensor, gqa: int) -> int:
+    """Malformed rows / pages skipped by the last merged decode on this
+    workspace (waits for the current stream)."""
+    import ctypes
+    n = ctypes.c_int32(0)
+    rc = load().sphkv_decode_paged_status(workspace.data_ptr(), workspace.numel(), pool.num_items, gqa,
+                                          pool.plan.dh, ctypes.byref(n), _stream())
+    check(rc, "sphkv_decode_paged_status")
+    return int(n.value)
 
 
 def decode_paged_partials(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,

@@ -11,6 +11,16 @@ codebooks -> K scale -> K -> tiers -> V -> q -> page permutation.
   (layer, head, token) TokenState.
 * Positions are token indices (each sequence uses its own 0..L-1).
 * RoPE: default (no scaling), theta = 500000, HF rotate_half pairing.
+* Config 4 scatters its pages over one shared pool of POOL_PAGES_C4 (~1.2M)
+  16-token pages: V slots drawn from that many slots, K pages placed with
+  random gaps over a byte pool of the same proportion (reduced-size variants
+  keep the ratio).
+
+kv_device: K and V are drawn on that torch device instead (torch's Philox
+generator seeded from the config seed; K = N(0,1) x the host-drawn channel
+scale, rounded to fp16), for full-size workloads whose host draws take
+minutes.  The host generator then skips the K and V draws, so the tiers, q
+and placement are a different (equally deterministic) instance.
 """
 from __future__ import annotations
 
@@ -22,6 +32,14 @@ import sys
 import numpy as np
 
 import sphkv_format as fmt
+
+
+POOL_PAGES_C4 = 1_200_000      # one shared pool of ~1.2M 16-token pages
+FULL_ROWS_C4 = 571_036         # rows of the full config-4 instance (seed 4, host draws)
+
+
+def _is_torch(x) -> bool:
+    return type(x).__module__.startswith("torch")
 
 
 @dataclass
@@ -40,18 +58,46 @@ class Workload:
     tier_of: List[np.ndarray]       # per (seq*num_kv + head): [L] tier ids
     plan: fmt.PagePlan
     page_size: int = 16
+    positions: Optional[List[np.ndarray]] = None   # per seq: absolute position of each token (None: index)
 
     @property
     def num_q(self) -> int:
         return self.num_kv * self.gqa
 
-    def k_rows(self) -> np.ndarray:
-        """K of all sequences as one [rows, dh] fp16 matrix; row of
-        (seq s, head h, token t) = row_base[s*num_kv+h] + t."""
+    def k_rows(self):
+        """K of all sequences as one [rows, dh] fp16 matrix (a torch tensor on
+        the device for device-drawn workloads); row of (seq s, head h, token
+        t) = row_base[s*num_kv+h] + t."""
+        if _is_torch(self.K[0]):
+            import torch
+            return torch.cat([k.reshape(-1, self.dh) for k in self.K], dim=0)
         return np.concatenate([k.reshape(-1, self.dh) for k in self.K], axis=0)
 
-    def v_rows(self) -> np.ndarray:
+    def v_rows(self):
+        if _is_torch(self.V[0]):
+            import torch
+            return torch.cat([v.reshape(-1, self.dh) for v in self.V], dim=0)
         return np.concatenate([v.reshape(-1, self.dh) for v in self.V], axis=0)
+
+    def head_kv(self, s: int, h: int):
+        """(K [L, dh], V [L, dh]) fp16 numpy arrays of one (seq, kv head)."""
+        k, v = self.K[s][h], self.V[s][h]
+        if _is_torch(k):
+            return k.cpu().numpy(), v.cpu().numpy()
+        return np.asarray(k), np.asarray(v)
+
+    def head_workload(self, s: int, h: int) -> "Workload":
+        """The workload of one (seq, kv head) alone -- one sequence, one kv
+        head, its codebooks, K, V, tiers and queries -- with a logical-order
+        plan (the grouping of a (seq, head) does not depend on the others)."""
+        k, v = self.head_kv(s, h)
+        t_of = [self.tier_of[s * self.num_kv + h]]
+        plan = fmt.plan_pages(t_of, None, 1, 1, self.dh, self.page_size)
+        return Workload(name=f"{self.name}[s{s}h{h}]", dh=self.dh, num_kv=1, gqa=self.gqa, num_seqs=1,
+                        lengths=[self.lengths[s]], rope_theta=self.rope_theta,
+                        codebooks={t: c[h:h + 1] for t, c in self.codebooks.items()},
+                        K=[k[None]], V=[v[None]], q=self.q[s:s + 1, h * self.gqa:(h + 1) * self.gqa],
+                        tier_of=t_of, plan=plan, page_size=self.page_size)
 
     def row_base(self) -> np.ndarray:
         base, acc = [], 0
@@ -95,9 +141,11 @@ def _assign_tiers(rng, L: int, fracs, sink: int = 0, recent: int = 0) -> np.ndar
 
 
 def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: Optional[int] = None,
-                         num_seqs_override: Optional[int] = None, layout: str = "default") -> Workload:
+                         num_seqs_override: Optional[int] = None, layout: str = "default",
+                         kv_device=None) -> Workload:
     """Decode configs 1, 2, 4, 5.  ctx_override shrinks
-    the context (for oracle-sized parity cases) keeping everything else."""
+    the context (for oracle-sized parity cases) keeping everything else;
+    kv_device draws K and V on that torch device (see the module docstring)."""
     D = fmt.DENSE_TIER_ID
     if config == 1:
         dh, num_kv, gqa, num_seqs, theta = 64, 8, 4, 1, 500000.0
@@ -136,9 +184,23 @@ def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: 
             print(f"[synth] config{config}: {what}" + ("" if i is None else f" {i + 1}/{len(lengths)}"),
                   file=sys.stderr, flush=True)
 
+    gen = None
+    if kv_device is not None:
+        import torch
+        gen = torch.Generator(device=kv_device)
+        gen.manual_seed(1_000_003 * (seed_d if seed is None else seed) + 17)
+        scale_t = torch.as_tensor(scale, dtype=torch.float32, device=kv_device)
+
+    def draw(L, scaled):
+        if gen is None:
+            x = rng.standard_normal((num_kv, L, dh))
+            return (x * scale[:, None, :] if scaled else x).astype(np.float16)
+        x = torch.randn((num_kv, L, dh), generator=gen, device=kv_device, dtype=torch.float32)
+        return (x * scale_t[:, None, :] if scaled else x).to(torch.float16)
+
     K = []
     for i, L in enumerate(lengths):
-        K.append((rng.standard_normal((num_kv, L, dh)) * scale[:, None, :]).astype(np.float16))
+        K.append(draw(L, True))
         progress("K", i)
     tier_of = []
     for L in lengths:
@@ -147,13 +209,20 @@ def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: 
     progress("tiers")
     V = []
     for i, L in enumerate(lengths):
-        V.append(rng.standard_normal((num_kv, L, dh)).astype(np.float16))
+        V.append(draw(L, False))
         progress("V", i)
     q = rng.standard_normal((num_seqs, num_kv * gqa, dh)).astype(np.float16)
     # config 1 uses an identity page table, the others a random placement;
     # layout="sequential" forces the identity placement (for locality studies)
     permute = config != 1 and layout != "sequential"
-    plan = fmt.plan_pages(tier_of, None, num_seqs, num_kv, dh, 16, rng=rng if permute else None)
+    nv, spread = None, 1.0
+    if config == 4 and permute:
+        rows = sum(-(-int(np.count_nonzero(t == tid)) // 16) for t in tier_of for tid in np.unique(t) if tid != 0)
+        full = ctx_override is None and num_seqs_override is None
+        nv = max(POOL_PAGES_C4, rows) if full else int(np.ceil(rows * POOL_PAGES_C4 / FULL_ROWS_C4))
+        spread = nv / max(rows, 1)
+    plan = fmt.plan_pages(tier_of, None, num_seqs, num_kv, dh, 16, rng=rng if permute else None,
+                          num_vpages=nv, byte_spread=spread)
     progress("page plan")
     return Workload(name=f"config{config}", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=num_seqs,
                     lengths=lengths, rope_theta=theta, codebooks=cbs, K=K, V=V, q=q,

@@ -52,8 +52,9 @@ def test_version_string():
 
 def test_workspace_bytes():
     lib = sphkv_lib.load()
-    assert lib.sphkv_decode_paged_workspace_bytes(256, 4, 128) == 256 * (16 + 4 * 128) * 4
-    assert lib.sphkv_decode_paged_workspace_bytes(0, 8, 64) == 0
+    # one (m, l, acc) partial per item, then 16 status bytes
+    assert lib.sphkv_decode_paged_workspace_bytes(256, 4, 128) == 256 * (16 + 4 * 128) * 4 + 16
+    assert lib.sphkv_decode_paged_workspace_bytes(0, 8, 64) == 16
     assert lib.sphkv_decode_paged_workspace_bytes(4, 3, 128) == -1      # gqa not supported
     assert lib.sphkv_decode_paged_workspace_bytes(4, 4, 96) == -1       # dh not supported
     assert lib.sphkv_decode_paged_workspace_bytes(-1, 4, 128) == -1
@@ -82,6 +83,25 @@ def test_decode_argument_errors(kw, msg):
     rc = lib.sphkv_decode_paged(*_decode_args(**kw))
     assert rc == -1
     assert msg in lib.sphkv_last_error().decode()
+
+
+def test_decode_rejects_unaddressable_v_pool():
+    lib = sphkv_lib.load()
+    rc = lib.sphkv_decode_paged(*_decode_args(num_vpages=(1 << 31) + 1, num_items=8, workspace_bytes=10 ** 9))
+    assert rc == -1 and "num_vpages" in lib.sphkv_last_error().decode()
+
+
+def test_decode_status_argument_errors():
+    lib = sphkv_lib.load()
+    n = ctypes.c_int32(7)
+    assert lib.sphkv_decode_paged_status(None, 0, 8, 4, 128, ctypes.byref(n), None) == -1
+    assert "does not hold" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_decode_paged_status(None, 10 ** 9, 8, 4, 128, None, None) == -1
+    assert "null output" in lib.sphkv_last_error().decode()
+    # the checked entry validates like sphkv_decode_paged before it launches
+    rc = lib.sphkv_decode_paged_checked(*_decode_args(dh=96))
+    assert rc == -1 and "dh must be 64 or 128" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_decode_paged_checked(*_decode_args(num_seqs=0)) == 0
 
 
 def test_decode_zero_sequences_is_a_no_op():

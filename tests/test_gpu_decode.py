@@ -20,7 +20,7 @@ TOL = 2e-3
 
 def _decode(pool, wl, gpu):
     q = torch.as_tensor(wl.q, device=gpu)
-    out = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta)
+    out = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta, check=True)     # raises on a skipped page
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
@@ -120,7 +120,7 @@ def test_decode_edge_cases(gpu):
     pos = [np.sort(rng.choice(120000, size=L, replace=False))]
     plan = fmt.plan_pages(tier_of, pos, 1, num_kv, dh, 16, rng=rng)
     wl = synth.Workload(name="edge", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=1, lengths=[L],
-                        rope_theta=5e5, codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan)
+                        rope_theta=5e5, codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan, positions=pos)
     pool, cpu = pool_from_oracle(wl, gpu)
     got = _decode(pool, wl, gpu)
     want = oracle.decode_mode_b(cpu, plan, cbs, q, gqa, 5e5)
@@ -229,7 +229,7 @@ def test_decode_split_phases_equal_fused_call(gpu):
     pool, _ = pool_from_oracle(wl, gpu, rows_per_item=24)
     q = torch.as_tensor(wl.q, device=gpu)
     ref = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta)
-    ws = torch.empty(pool.workspace_bytes(wl.gqa), dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(pool.workspace_bytes(wl.gqa), dtype=torch.uint8, device=gpu)
     part = ops.decode_paged_partials(pool, q, wl.gqa, wl.rope_theta, ws)
     out = ops.merge_partials(pool, ws, wl.gqa, torch.empty_like(q))
     torch.cuda.synchronize()
@@ -245,3 +245,72 @@ def test_decode_split_phases_equal_fused_call(gpu):
         f = np.where(np.isfinite(m), np.exp2(m - M), 0.0)
         host[sh * G:(sh + 1) * G] = (f[:, :, None] * acc).sum(0) / (f * l).sum(0)[:, None]
     assert max_err(out[0].float().cpu().numpy(), host) < 1e-3
+
+
+def _drop_rows(plan, drop):
+    """The plan without the given rows (page bytes stay where they are)."""
+    keep = np.setdiff1d(np.arange(plan.num_rows), np.asarray(sorted(drop)))
+    sh = plan.seq_head[keep]
+    rs = np.searchsorted(sh, np.arange(plan.num_seqs * plan.num_kv + 1), side="left").astype(np.int32)
+    return fmt.PagePlan(dh=plan.dh, page_size=plan.page_size, num_seqs=plan.num_seqs, num_kv=plan.num_kv,
+                        tier=plan.tier[keep], count=plan.count[keep], tokens=plan.tokens[keep],
+                        positions=plan.positions[keep], seq_head=sh, row_start=rs, ptable=plan.ptable[keep],
+                        vslot=plan.vslot[keep], pages_bytes=plan.pages_bytes, num_vpages=plan.num_vpages)
+
+
+def test_decode_v_slots_beyond_2_pow_20(gpu):
+    # regression of the 64-bit V-page offset: every row's V page sits at a
+    # slot >= 2^20 (element offset >= 2^31 at dh 128) in a 1.31M-page pool;
+    # the decode must equal the same pool with compact slots, bit for bit,
+    # and the oracle within 2e-3
+    wl = synth.make_decode_workload(2, ctx_override=4096)
+    P = wl.plan.num_rows
+    rng = np.random.default_rng(21)
+    hi_slots = ((1 << 20) + rng.choice(1 << 18, size=P, replace=False)).astype(np.int32)
+    plan_hi = fmt.PagePlan(**{**wl.plan.__dict__, "vslot": hi_slots, "num_vpages": (1 << 20) + (1 << 18)})
+    log(f"vslots in [{int(hi_slots.min())}, {int(hi_slots.max())}], pool {plan_hi.num_vpages} pages")
+    pool_hi, _, _ = ops.build_pool_gpu(synth.Workload(**{**wl.__dict__, "plan": plan_hi}), gpu)
+    pool_lo, cpu = pool_from_oracle(wl, gpu)
+    q = torch.as_tensor(wl.q, device=gpu)
+    a = ops.decode_paged(pool_hi, q, wl.gqa, wl.rope_theta, check=True)
+    b = ops.decode_paged(pool_lo, q, wl.gqa, wl.rope_theta, check=True)
+    assert torch.equal(a, b)
+    want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+    assert max_err(a.float().cpu().numpy(), want) <= TOL
+    del pool_hi
+
+
+def test_decode_malformed_rows_are_skipped_and_counted(gpu):
+    # five malformed rows of different kinds: each contributes no token, the
+    # checked entry reports all five, the output equals the oracle over the
+    # other rows, and a clean decode on the same workspace reports zero again
+    wl = synth.make_decode_workload(2, ctx_override=3000)
+    pool, cpu = pool_from_oracle(wl, gpu)
+    plan = wl.plan
+    rs = plan.row_start
+    dense = [p for p in range(rs[0], rs[1]) if plan.tier[p] == fmt.DENSE_TIER_ID]
+    comp = [p for p in range(rs[2], rs[3]) if plan.tier[p] == 1]
+    r_off, r_vs, r_tier, r_dense, r_sec = int(rs[1]) + 3, int(rs[4]) + 1, int(rs[5]) + 2, dense[1], comp[4]
+    pt = plan.ptable.copy()
+    vs = plan.vslot.copy()
+    pt[r_off, 0] = -16                                 # page offset outside the pool
+    vs[r_vs] = plan.num_vpages + 5                     # V slot outside the V pool
+    pt[r_dense, 1] += 2                                # dense K rows not 16-byte aligned
+    pt[r_sec, 2] += 600                                # radius section beyond the 512-byte window
+    pages = pool.pages.clone()
+    pages[int(plan.ptable[r_tier, 0])] = 7             # unknown tier id
+    bad = ops.PagedPool(**{**pool.__dict__, "ptable": torch.as_tensor(pt, device=gpu),
+                           "vslot": torch.as_tensor(vs, device=gpu), "pages": pages})
+    q = torch.as_tensor(wl.q, device=gpu)
+    ws = torch.zeros(pool.workspace_bytes(wl.gqa), dtype=torch.uint8, device=gpu)
+    out = ops.decode_paged(bad, q, wl.gqa, wl.rope_theta, workspace=ws)
+    assert ops.decode_status(bad, ws, wl.gqa) == 5
+    with pytest.raises(Exception, match="5 malformed"):
+        ops.decode_paged(bad, q, wl.gqa, wl.rope_theta, workspace=ws, check=True)
+    want = oracle.decode_mode_b(cpu, _drop_rows(plan, [r_off, r_vs, r_tier, r_dense, r_sec]), wl.codebooks,
+                                wl.q, wl.gqa, wl.rope_theta)
+    err = max_err(out.float().cpu().numpy(), want)
+    log(f"  malformed rows skipped: max abs err {err:.3e} against the oracle without them")
+    assert err <= TOL and torch.isfinite(out).all()
+    ops.decode_paged(pool, q, wl.gqa, wl.rope_theta, workspace=ws)
+    assert ops.decode_status(pool, ws, wl.gqa) == 0
