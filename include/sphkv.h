@@ -126,6 +126,30 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
                        void* stream);
 
 /*
+ * sphkv_decode_paged without the workspace arguments, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc).  No reference counterpart.  The partials and status words
+ * live in a device array of the library (SPHKV_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends); the call allocates nothing and returns
+ * SPHKV_EINVAL when sphkv_decode_paged_workspace_bytes(num_items, gqa, dh)
+ * exceeds that size (8 MiB: 3,970 work items at gqa 4 / dh 128, 2,016 at
+ * gqa 8).  All calls on one GPU share that GPU's array: calls that overlap
+ * on one GPU (several streams or threads) race.  Results equal
+ * sphkv_decode_paged's on the same inputs.  Malformed pages are skipped as
+ * there, without a report (sphkv_decode_paged_checked reports them).
+ */
+#define SPHKV_NOALLOC_SCRATCH_BYTES (8 << 20)
+int sphkv_decode_paged_noalloc(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                               const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                               const uint16_t* v_pool, int64_t num_vpages,
+                               const float* cb1, const float* cb2, const float* cb3,
+                               const int32_t* work, int32_t num_items, const int32_t* work_start,
+                               int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                               const uint16_t* q, uint16_t* out,
+                               int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                               void* stream);
+
+/*
  * Malformed input.  The decode never reads outside the buffers it is given;
  * a pointer-table row that does not address the pools, a page whose tier id
  * is not 1, 2, 3 or 0xFF, a count above page_size, a dense page whose K rows

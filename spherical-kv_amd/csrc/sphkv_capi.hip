@@ -119,6 +119,29 @@ int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_
 
 }  // namespace
 
+// Shared with sphkv_noalloc.hip (its entry point validates and launches as
+// sphkv_decode_paged does, on its own scratch).
+namespace sphkv {
+int noalloc_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  fail_v(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+int noalloc_decode(const char* fn, const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                   const int32_t* vslot, const int32_t* positions, int32_t num_rows, const uint16_t* v_pool,
+                   int64_t num_vpages, const float* cb1, const float* cb2, const float* cb3,
+                   const int32_t* work, int32_t num_items, const int32_t* work_start, int32_t num_seqs,
+                   int32_t num_kv, int32_t gqa, const uint16_t* q, uint16_t* out, void* workspace,
+                   int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale, double rope_theta,
+                   void* stream) {
+  return decode_call(fn, kPhasePartials | kPhaseMerge, pages, pages_bytes, ptable, vslot, positions, num_rows,
+                     v_pool, num_vpages, cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q,
+                     out, workspace, workspace_bytes, dh, page_size, sm_scale, rope_theta, stream);
+}
+}  // namespace sphkv
+
 extern "C" {
 
 int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,

@@ -33,6 +33,8 @@ SIGNATURES = {
                                                    I32, I32, I32, P, P, I64, I32, I32, F32, F64, P]),
     "sphkv_decode_merge_partials": (ctypes.c_int, [P, I64, I32, P, I32, I32, I32, I32, P, P]),
     "sphkv_decode_paged_status": (ctypes.c_int, [P, I64, I32, I32, I32, P, P]),
+    "sphkv_decode_paged_noalloc": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P,
+                                                  I32, I32, I32, P, P, I32, I32, F32, F64, P]),
     "sphkv_decode_paged_checked": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P,
                                                   I32, I32, I32, P, P, P, I64, I32, I32, F32, F64, P]),
     "sphkv_fused_decode_ragged": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,

@@ -213,3 +213,17 @@ def test_omega_ema_argument_errors():
     assert lib.sphkv_omega_ema(None, None, 130, 2, None, None, 8, 4, 64, 0.9, None) == -1
     assert "null pointer" in lib.sphkv_last_error().decode()
     assert lib.sphkv_omega_ema(None, None, 130, 2, None, None, 8, 4, 0, 0.9, None) == 0
+
+
+def test_noalloc_refuses_work_beyond_its_scratch():
+    # the size check runs before any device access
+    lib = sphkv_lib.load()
+    per_item = lib.sphkv_decode_paged_workspace_bytes(1, 8, 128) - lib.sphkv_decode_paged_workspace_bytes(0, 8, 128)
+    n = (8 << 20) // per_item + 1
+    args = _decode_args(num_items=n, gqa=8)
+    del args[19:21]                                  # no workspace arguments
+    assert lib.sphkv_decode_paged_noalloc(*args) == -1
+    assert "more than its" in lib.sphkv_last_error().decode()
+    args = _decode_args(num_seqs=0)
+    del args[19:21]
+    assert lib.sphkv_decode_paged_noalloc(*args) == 0
