@@ -184,10 +184,13 @@ __device__ __forceinline__ void load_dense(const Res& rs, const Row& r, int t, i
   }
 }
 
-// Waves per decode workgroup: 16 (4 per SIMD) where the register and LDS
-// budgets allow it (GQA <= 4), else 12 (3 per SIMD).
+// Waves per decode workgroup: 12 (3 per SIMD, up to 168 VGPRs each), which
+// leaves room to keep the lane-derived addresses of the page loop in
+// registers for GQA <= 4 (decode_hoist); GQA 8 recomputes them per page.
 template <int GQA>
-__host__ __device__ constexpr int decode_waves() { return GQA <= 4 ? 16 : 12; }
+__host__ __device__ constexpr int decode_waves() { return 12; }
+template <int GQA>
+__host__ __device__ constexpr bool decode_hoist() { return GQA <= 4; }
 constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| < kDelta
 
 __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
@@ -208,6 +211,8 @@ template <int DH, int GQA>
 struct DecodeLds {
   static constexpr int kWaves = decode_waves<GQA>();
   static constexpr int NJ = DH / 2;
+  static constexpr int NPAIR = DH / 8;          // RoPE pairs (j, j + DH/2) per lane
+  static constexpr int MQ = NPAIR / 4;          // float4 groups of pairs per lane
   __host__ __device__ static constexpr int cb_pad(int g) { return g + 4; }
   static constexpr int cb_n1 = (DH / 16) * 64 * 20;
   static constexpr int cb_n2 = (DH / 16) * 16 * 20;
@@ -222,23 +227,21 @@ struct DecodeLds {
   static constexpr int o_stage = o_ftab + NJ * 8;
   static constexpr int PR = GQA < 4 ? 4 : GQA;                   // heads padded to 4 (slots)
   static constexpr int NHS = PR / 4;                             // sets of 4 head slots
-  // rotated query, fp32, per set of 4 head slots: float4 group kq (dims kk =
-  // 4 kq .. 4 kq + 3 of a lane quarter's 32) x (quarter u, slot j), groups
-  // kq_stride floats apart: the MFMA operand reads (16 float4s of one group)
-  // and the per-frequency writes (one float per lane) are both conflict-free
-  static constexpr int kq_stride = 68;
-  static constexpr int qs_floats = (DH / 16) * kq_stride;
+  // rotated query, fp32, per set of 4 head slots: block (half hf, group m)
+  // of 68 floats = [quarter u][slot][4 pairs e] + 4 padding floats, the
+  // float4 of (u, slot) holding pairs 4m .. 4m + 3 of quarter u's RoPE
+  // frequencies, first (hf = 0) or second (hf = 1) half.  The A-operand
+  // reads (16 float4s of one block) and the per-frequency writes (one float
+  // per lane, banks (4 m + e + 16 u) mod 64 distinct) are conflict-free.
+  static constexpr int kQBlk = 68;
+  static constexpr int qset = 2 * MQ * kQBlk;                    // floats per head-slot set
   static constexpr int o_qr = o_stage + kWaves * 512;
-  // GQA > 4 keeps QK on the fp16 16x16x32 MFMA (16 output columns hold 8
-  // heads at once): query rows split hi + lo, [2][GQA][DH + 8] halves
-  static constexpr bool kF32QK = GQA <= 4;
-  static constexpr int qrow = DH + 8;
-  static constexpr int qr_wave = kF32QK ? NHS * qs_floats * 4 : 2 * GQA * qrow * 2;   // bytes per wave
+  static constexpr int qr_wave = NHS * qset * 4;                 // bytes per wave
   static constexpr int o_pt = o_qr + kWaves * qr_wave;
   static constexpr int total = o_pt + kWaves * PR * 32;
   // the end-of-item wave merge reuses the space: [kWaves][GQA][DH] acc,
-  // [kWaves][GQA][2] (m, l), [GQA][kWaves] weights
-  static constexpr int merge_bytes = kWaves * GQA * (DH + 3) * 4;
+  // [kWaves][GQA][2] (m, l)
+  static constexpr int merge_bytes = kWaves * GQA * (DH + 2) * 4;
   static_assert(merge_bytes <= total, "merge buffer exceeds the workgroup's LDS");
   static_assert(total <= 160 * 1024, "LDS budget");
 };
@@ -248,11 +251,11 @@ struct DecodeLds {
 // the radius r_hat = int8 / 127 * scale (pagebuilder.py:17-21).
 template <int DH, int GQA, int TID>
 __device__ __forceinline__ void locate_k(const uint8_t* st, int rel, int thr, int rdr, int t, int u, int n,
-                                         bool ok, int (&cofs)[2], float (&rh)[2]) {
+                                         int (&cofs)[2], float (&rh)[2]) {
   constexpr int g = tier_g(TID), b = tier_b(TID), C = tier_C(TID);
   constexpr int G = DH / g;
   using L = DecodeLds<DH, GQA>;
-  const bool live = ok && t < n;
+  const bool live = t < n;
   uint64_t bits = 0;
   uint32_t rad[2] = {0u, 0u};
   if (live) {
@@ -312,59 +315,30 @@ __device__ __forceinline__ float2 turn_phasor(double x) {
   return float2{__builtin_amdgcn_cosf(ph), __builtin_amdgcn_sinf(ph)};
 }
 
-// x = hi + lo with hi, lo fp16: hi = x rounded toward zero (v_cvt_pkrtz), lo =
-// fp16(x - hi) formed by one mixed-precision FMA per half (fp32 x, fp16 hi)
-// that writes that half of the packed result.  The pair carries x to about
-// 2^-22 relative, so products on the fp16 MFMA lose nothing that matters
-// against the 2e-3 tolerance.  The FMAs are inline asm (the compiler forms
-// them only when fp32 denormals are flushed); the s_nop after each covers the
-// forwarding hazard of a partial (one-half) VGPR write, which the compiler's
-// hazard recognizer does not track through inline asm.  Inputs are never the
-// direct result of a transcendental instruction.
-__device__ __forceinline__ uint32_t pk_rtz(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
-__device__ __forceinline__ uint32_t pk_rest(float a, float b, uint32_t hi) {
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
-      "s_nop 0\n\t"
-      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
-      "s_nop 0"
-      : "=&v"(d) : "v"(a), "v"(b), "v"(hi));
-  return d;
-}
-__device__ __forceinline__ void split_f16(const float (&x)[8], half8& hi, half8& lo) {
-  uint4 h, l;
-  h.x = pk_rtz(x[0], x[1]); h.y = pk_rtz(x[2], x[3]); h.z = pk_rtz(x[4], x[5]); h.w = pk_rtz(x[6], x[7]);
-  l.x = pk_rest(x[0], x[1], h.x); l.y = pk_rest(x[2], x[3], h.y);
-  l.z = pk_rest(x[4], x[5], h.z); l.w = pk_rest(x[6], x[7], h.w);
-  hi = __builtin_bit_cast(half8, h);
-  lo = __builtin_bit_cast(half8, l);
-}
-
 // Rotation by N lanes within each 16-lane row (DPP row_ror).
 template <int N>
 __device__ __forceinline__ float row_ror(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, true));
 }
 
-// Max / sum over the 16 lanes l' with l' = l (mod 4): the four lanes of each
-// row (row_ror 4, 8), then the four rows.
-__device__ __forceinline__ float head_max(float x) {
-  x = fmaxf(x, row_ror<4>(x));
+// Max / sum over the 16 lanes of each row (every lane gets its row's result).
+__device__ __forceinline__ float row_max16(float x) {
   x = fmaxf(x, row_ror<8>(x));
-  return rows_max(x);
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<2>(x));
+  return fmaxf(x, row_ror<1>(x));
 }
-__device__ __forceinline__ float head_sum(float x) {
-  x += row_ror<4>(x);
+__device__ __forceinline__ float row_sum16(float x) {
   x += row_ror<8>(x);
-  return rows_sum(x);
+  x += row_ror<4>(x);
+  x += row_ror<2>(x);
+  return x + row_ror<1>(x);
 }
 
-// Sums the four lane quarters' partials of a 4x4x1 MFMA result: element i of
-// lane l holds (token 4 ((l >> 2) & 3) + i, head slot l & 3) summed over the
-// 32 dimensions of quarter l >> 4.  Two row-swap rounds pair the quarters and
-// leave lane l with the full sum of element {0, 2, 1, 3}[l >> 4].
+// Sums the four lane quarters' partials of a head set: element i of lane l
+// holds head slot i of lane l's token summed over the dimensions of quarter
+// l >> 4.  Two row-swap rounds pair the quarters and leave lane l with the
+// full sum of head slot {0, 2, 1, 3}[l >> 4].
 __device__ __forceinline__ float quarter_sum(floatx4 s) {
   float a0 = s[0], a1 = s[1], b0 = s[2], b1 = s[3];
   swap32(a0, a1);
@@ -373,6 +347,8 @@ __device__ __forceinline__ float quarter_sum(floatx4 s) {
   swap16(a, b);
   return a + b;
 }
+__host__ __device__ constexpr int row_slot(int row) { return (0xD8 >> (2 * row)) & 3; }   // {0, 2, 1, 3}
+__host__ __device__ constexpr int slot_row(int slot) { return (0xD8 >> (2 * slot)) & 3; }  // its inverse
 
 template <int DH, int GQA>
 __global__ __launch_bounds__(decode_waves<GQA>() * 64)
@@ -382,10 +358,10 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // kernel-argument dwords into SGPRs, so the work item's load is issued at
   // wave start instead of after two dependent argument loads
   constexpr int kWaves = decode_waves<GQA>();
-  constexpr int NC = DH / 32;        // 32-dim chunks per lane-token
-  constexpr int NP = NC / 2;         // chunks holding the first RoPE half
+  constexpr int NC = DH / 32;        // 8-dim chunks of dense K per lane-token
   constexpr int NJ = DH / 2;         // RoPE frequencies
   using L = DecodeLds<DH, GQA>;
+  constexpr int NPAIR = L::NPAIR, MQ = L::MQ;
   __shared__ __attribute__((aligned(16))) uint8_t smem[L::total];
   float* cb_s = reinterpret_cast<float*>(smem + L::o_cb);
   const uint8_t* dtab = smem + L::o_dtab;
@@ -413,7 +389,6 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int u = lane >> 4;
   uint8_t* st = smem + L::o_stage + wave * 512;
   float* qr = reinterpret_cast<float*>(smem + L::o_qr + wave * L::qr_wave);
-  _Float16* qrh = reinterpret_cast<_Float16*>(qr);   // the fp16 form's [hi, lo][GQA][qrow]
 
   int p = rb + wave * rstride;
   const Res rs = make_res(a);
@@ -441,17 +416,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       }
     }
   }
-  // this lane's query pair (j, j + NJ) of every head of the item, packed fp16
-  uint32_t qv[GQA];
+  // this lane's query pair (j, j + NJ) of every head of the item, fp32
+  float qf[GQA][2];
   {
     const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
     const int j = lane % NJ;
 #pragma unroll
     for (int hh = 0; hh < GQA; ++hh) {
-      half2v v;
-      v[0] = qh[hh * DH + j];
-      v[1] = qh[hh * DH + j + NJ];
-      qv[hh] = __builtin_bit_cast(uint32_t, v);
+      qf[hh][0] = (float)qh[hh * DH + j];
+      qf[hh][1] = (float)qh[hh * DH + j + NJ];
     }
   }
   if (GQA < 4) {
@@ -461,8 +434,8 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.f;
       *reinterpret_cast<half8*>(reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile + GQA * kTile + 8 * lane) = z;
     }
-    for (int i = lane; i < DH; i += 64)              // i = (kq, u, slot j)
-      if ((i & 3) >= GQA) *reinterpret_cast<floatx4*>(qr + (i >> 4) * L::kq_stride + 4 * (i & 15)) = (floatx4){0.f, 0.f, 0.f, 0.f};
+    for (int i = lane; i < 2 * MQ * 16; i += 64)          // i = (block, u, slot)
+      if ((i & 3) >= GQA) *reinterpret_cast<floatx4*>(qr + (i >> 4) * L::kQBlk + 4 * (i & 15)) = (floatx4){0.f, 0.f, 0.f, 0.f};
   }
   // first page's data and the next page's row
   Row row_c = row_take(a, rl_c, p, re);
@@ -504,12 +477,16 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // no wait inside the loop has to account for it
   __builtin_amdgcn_s_waitcnt(0);
 
-  // online-softmax state of head 4 hs + (lane % 4) (the same in all 16 lanes
-  // of that head; slots >= GQA hold zero logits and are never written out)
+  // Online-softmax state.  After a page's quarter sums, lane (row r, token t)
+  // holds the logit of head 4 hs + row_slot(r) for token t; the running
+  // reference max m_run of that head is the same in all 16 lanes of the row,
+  // and l_part is this lane's share (token slot t) of the head's sum of
+  // weights, reduced over the row once the item is done.
   constexpr int NHS = L::NHS, NHF = DH / 64;
-  float m_run[NHS], l_run[NHS];
+  const int hr = row_slot(u);
+  float m_run[NHS], l_part[NHS];
 #pragma unroll
-  for (int hs = 0; hs < NHS; ++hs) { m_run[hs] = -INFINITY; l_run[hs] = 0.f; }
+  for (int hs = 0; hs < NHS; ++hs) { m_run[hs] = -INFINITY; l_part[hs] = 0.f; }
   // PV accumulators of the 4x4x4 MFMA: acc[hs][hf] lane l, element i =
   // O[head 4 hs + i][dim 64 hf + l]
   floatx4 acc[NHS][NHF];
@@ -528,11 +505,11 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // wait for that load.
   auto step = [&](const int p, uint4& stg_c, int& pos_c, uint4& stg_n, int& pos_n, RowLd& rl_issue,
                   RowLd& rl_take) __attribute__((always_inline)) {
-    // Lane-derived addresses are recomputed each iteration (a few VALU ops)
-    // instead of being hoisted out of the loop, where they would not fit in
-    // the register budget of 3 waves per SIMD and would be spilled.
+    // Without hoisting, lane-derived addresses are recomputed each iteration
+    // (a few VALU ops): the opaque copy of the lane id keeps the compiler from
+    // hoisting them into registers the budget does not have.
     int lane_v = lane;
-    asm volatile("" : "+v"(lane_v));
+    if constexpr (!decode_hoist<GQA>()) asm volatile("" : "+v"(lane_v));
     const int t = lane_v & 15;
     const int u = lane_v >> 4;
     // ---- issue priority from this wave's share of pages still to do: a
@@ -602,229 +579,155 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     int t_lo = __builtin_amdgcn_readlane(pos_c, 0);
     int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
     const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
-    if (lane < NJ) {
-      // lane = frequency j: dims j and j + NJ are element kk = j mod (DH/8)
-      // and kk + DH/8 of quarter j / (DH/8) (loop-invariant addresses, kept
-      // in registers)
-      const int j = lane % NJ;
+    if (lane_v < NJ) {
+      // lane = frequency j: pair e = j mod 4 of group m of quarter j / NPAIR
+      const int j = lane_v;
       const float2 z = turn_phasor((double)t_mid * ftab[j]);
-      if constexpr (L::kF32QK) {
-        const int kk = j % (DH / 8), uq = j / (DH / 8);
-        float* q0 = qr + (kk >> 2) * L::kq_stride + uq * 16 + (kk & 3);
-        float* q1 = q0 + (DH / 32) * L::kq_stride;
+      const int s = j % NPAIR;
+      float* w0 = qr + (s >> 2) * L::kQBlk + (j / NPAIR) * 16 + (s & 3);
+      float* w1 = w0 + MQ * L::kQBlk;
 #pragma unroll
-        for (int hh = 0; hh < GQA; ++hh) {
-          const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
-          const float a0 = (float)qp[0], a1 = (float)qp[1];
-          const int o = (hh >> 2) * L::qs_floats + (hh & 3) * 4;
-          q0[o] = a0 * z.x + a1 * z.y;
-          q1[o] = a1 * z.x - a0 * z.y;
-        }
-      } else {
-#pragma unroll
-        for (int hh = 0; hh < GQA; ++hh) {
-          const half2v qp = __builtin_bit_cast(half2v, qv[hh]);
-          const float a0 = (float)qp[0], a1 = (float)qp[1];
-          const float r0 = a0 * z.x + a1 * z.y;
-          const float r1 = a1 * z.x - a0 * z.y;
-          const uint32_t hp = pk_rtz(r0, r1);
-          const half2v hi = __builtin_bit_cast(half2v, hp);
-          const half2v lo = __builtin_bit_cast(half2v, pk_rest(r0, r1, hp));
-          _Float16* qh = qrh + hh * L::qrow;
-          _Float16* ql = qrh + (GQA + hh) * L::qrow;
-          qh[j] = hi[0];
-          qh[j + NJ] = hi[1];
-          ql[j] = lo[0];
-          ql[j + NJ] = lo[1];
-        }
+      for (int hh = 0; hh < GQA; ++hh) {
+        const int o = (hh >> 2) * L::qset + (hh & 3) * 4;
+        w0[o] = qf[hh][0] * z.x + qf[hh][1] * z.y;
+        w1[o] = qf[hh][1] * z.x - qf[hh][0] * z.y;
       }
     }
 
     // ---- locate this page's keys: centroid offsets + radii (compressed) ---
     const bool dense = tid == kDenseTier;
     int cofs[2] = {0, 0};
-    float rh[2] = {0.f, 0.f};
+    float rh[2] = {1.f, 1.f};                   // dense K enters unscaled
     if (tid >= 1 && tid <= 3) {
-      if (lane < 32) *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
+      if (lane_v < 32) *reinterpret_cast<uint4*>(st + 16 * lane_v) = stg_c;
       wave_lds_sync();
-      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
-      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
-      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, true, cofs, rh);
+      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, cofs, rh);
+      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, cofs, rh);
+      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, cofs, rh);
     }
     wave_lds_sync();
 
-    // ---- k_rot = R(pos - t_mid) k_hat per chunk pair (c, c + NP), fp32.
-    //      Phasors from the delta table (sine negated for pos < t_mid), or
-    //      formed directly when |pos - t_mid| >= kDelta.  Each chunk pair
-    //      feeds the fp32 4x4x1 MFMA as soon as it is formed: block b = lane /
-    //      4 = (quarter u, token group), A = k_rot of token t (row t % 4),
-    //      B = the rotated query of head slot lane % 4 (column), one
-    //      dimension per instruction; chunks c and c + NP accumulate apart.
-    //      (GQA > 4: split hi + lo fp16 and S^T = K_rot q_rot^T on the
-    //      16x16x32 MFMA as hi*hi + lo*hi + hi*lo; lane (u, hl) gets head hl,
-    //      tokens 4u..4u+3.)
-    floatx4 Sa[NHS], Sb[NHS];
+    // ---- QK.  k_hat = (r1 c1, r2 c2) on the lane's pairs (j, j + DH/2) (c1,
+    //      c2 the centroid runs of the two codebook groups, or the dense K
+    //      halves with r1 = r2 = 1), d = pos - t_mid, cs = cos(2 pi f_j |d|),
+    //      sn = sin(2 pi f_j |d|), sg = sign d, q_c = R(-t_mid) q.  With k1 =
+    //      r1 c1 and k2 = sg r2 c2 (dense: sg K2),
+    //        x0 = k1 cs - k2 sn,  x1' = k2 cs + k1 sn,
+    //      R(d) k_hat = (x0, sg x1'), so <q_c, R(d) k_hat> = sum q0 x0 + sg sum q1 x1'.
+    //      Both sums run on the fp32 MFMA (4x4x1, 16 blocks = 4 lane quarters
+    //      x 4 token groups; A = the rotated query of head slot i (row), B =
+    //      x0 or x1' of the lane's own token (column), one pair per
+    //      instruction), so every lane's accumulators hold its own token's
+    //      sums for head slots 0..3 and sg applies per lane afterwards.
+    //      Phasors come from the LDS delta table, or are formed directly when
+    //      |d| >= kDelta.
+    const int dl = valid ? pos_c - t_mid : 0;
+    const int ad = dl < 0 ? -dl : dl;
+    const bool near = ad < kDelta;
+    const bool any_far = __ballot(!near) != 0;
+    const float* drw = reinterpret_cast<const float*>(dtab + (near ? ad : 0) * L::drow) + 2 * NPAIR * u;
+    const float* qb = qr + u * 16 + (lane_v & 3) * 4;
+    const float sg = dl < 0 ? -1.f : 1.f;
+    const float r1 = rh[0], r2 = sg * rh[1];
+    const uint32_t kneg = dl < 0 ? 0x80008000u : 0u;  // dense: sg applied to K2's fp16 sign bits
+    floatx4 qk[NHS][2];
 #pragma unroll
-    for (int hs = 0; hs < NHS; ++hs) { Sa[hs] = (floatx4){0.f, 0.f, 0.f, 0.f}; Sb[hs] = Sa[hs]; }
-    floatx4 S = {0.f, 0.f, 0.f, 0.f};
-    const int hl = lane_v & 15;
-    {
-      const float* qb = qr + (u * 4 + (lane_v & 3)) * 4;
-      const _Float16* qh = qrh + (hl % GQA) * L::qrow;
-      const _Float16* ql = qh + GQA * L::qrow;
-      const int dl = valid ? pos_c - t_mid : 0;
-      const int ad = dl < 0 ? -dl : dl;
-      const bool near = ad < kDelta;
-      const float sg = dl < 0 ? -1.f : 1.f;
-      const bool any_far = __ballot(!near) != 0;
-      const float* drw = reinterpret_cast<const float*>(dtab + (near ? ad : 0) * L::drow) + 2 * (DH / 8) * u;
+    for (int hs = 0; hs < NHS; ++hs) { qk[hs][0] = (floatx4){0.f, 0.f, 0.f, 0.f}; qk[hs][1] = qk[hs][0]; }
 #pragma unroll
-      for (int c = 0; c < NP; ++c) {
-        float k0[8], k1[8];                      // chunks c and c + NP
-        if (dense) {
-          const half8 h0 = __builtin_bit_cast(half8, kd[c]), h1 = __builtin_bit_cast(half8, kd[c + NP]);
+    for (int m = 0; m < MQ; ++m) {
+      float k1[4], k2[4];                        // k1 = r1 c1, k2 = sg r2 c2 on pairs 4m .. 4m + 3
+      if (dense) {
+        const uint4 w0 = kd[m >> 1], w1 = kd[NC / 2 + (m >> 1)];
+        const uint32_t a0 = (m & 1) ? w0.z : w0.x, a1 = (m & 1) ? w0.w : w0.y;
+        const uint32_t b0 = ((m & 1) ? w1.z : w1.x) ^ kneg, b1 = ((m & 1) ? w1.w : w1.y) ^ kneg;
+        const half2v ha0 = __builtin_bit_cast(half2v, a0), ha1 = __builtin_bit_cast(half2v, a1);
+        const half2v hb0 = __builtin_bit_cast(half2v, b0), hb1 = __builtin_bit_cast(half2v, b1);
+        k1[0] = (float)ha0[0]; k1[1] = (float)ha0[1]; k1[2] = (float)ha1[0]; k1[3] = (float)ha1[1];
+        k2[0] = (float)hb0[0]; k2[1] = (float)hb0[1]; k2[2] = (float)hb1[0]; k2[3] = (float)hb1[1];
+      } else {
+        const float4 c0 = *reinterpret_cast<const float4*>(cb_s + cofs[0] + 4 * m);
+        const float4 c1 = *reinterpret_cast<const float4*>(cb_s + cofs[1] + 4 * m);
+        k1[0] = r1 * c0.x; k1[1] = r1 * c0.y; k1[2] = r1 * c0.z; k1[3] = r1 * c0.w;
+        k2[0] = r2 * c1.x; k2[1] = r2 * c1.y; k2[2] = r2 * c1.z; k2[3] = r2 * c1.w;
+      }
+      float pc[4], ps[4];
+      {
+        const float4 c03 = *reinterpret_cast<const float4*>(drw + 8 * m);
+        const float4 s03 = *reinterpret_cast<const float4*>(drw + 8 * m + 4);
+        pc[0] = c03.x; pc[1] = c03.y; pc[2] = c03.z; pc[3] = c03.w;
+        ps[0] = s03.x; ps[1] = s03.y; ps[2] = s03.z; ps[3] = s03.w;
+      }
+      if (any_far && !near) {
 #pragma unroll
-          for (int s = 0; s < 8; ++s) { k0[s] = (float)h0[s]; k1[s] = (float)h1[s]; }
-        } else {
-          const float4* c0 = reinterpret_cast<const float4*>(cb_s + cofs[0] + 8 * c);
-          const float4* c1 = reinterpret_cast<const float4*>(cb_s + cofs[1] + 8 * c);
-          const float4 a0 = c0[0], a1 = c0[1], b0 = c1[0], b1 = c1[1];
-          const float r0 = rh[0], r1 = rh[1];
-          k0[0] = r0 * a0.x; k0[1] = r0 * a0.y; k0[2] = r0 * a0.z; k0[3] = r0 * a0.w;
-          k0[4] = r0 * a1.x; k0[5] = r0 * a1.y; k0[6] = r0 * a1.z; k0[7] = r0 * a1.w;
-          k1[0] = r1 * b0.x; k1[1] = r1 * b0.y; k1[2] = r1 * b0.z; k1[3] = r1 * b0.w;
-          k1[4] = r1 * b1.x; k1[5] = r1 * b1.y; k1[6] = r1 * b1.z; k1[7] = r1 * b1.w;
+        for (int e = 0; e < 4; ++e) {
+          const float2 z = turn_phasor((double)ad * ftab[NPAIR * u + 4 * m + e]);
+          pc[e] = z.x;
+          ps[e] = z.y;
         }
-        float pc[8], ps[8];                     // phasor cos / sin
-        {
-          const float4* dq = reinterpret_cast<const float4*>(drw + 16 * c);
-          const float4 c03 = dq[0], s03 = dq[1], c47 = dq[2], s47 = dq[3];
-          pc[0] = c03.x; pc[1] = c03.y; pc[2] = c03.z; pc[3] = c03.w;
-          pc[4] = c47.x; pc[5] = c47.y; pc[6] = c47.z; pc[7] = c47.w;
-          ps[0] = sg * s03.x; ps[1] = sg * s03.y; ps[2] = sg * s03.z; ps[3] = sg * s03.w;
-          ps[4] = sg * s47.x; ps[5] = sg * s47.y; ps[6] = sg * s47.z; ps[7] = sg * s47.w;
-        }
-        if (any_far && !near) {
+      }
+      floatx4 q0[NHS], q1[NHS];
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const float2 z = turn_phasor((double)dl * ftab[chunk_dim<DH>(c, 0) + (DH / 8) * u + s]);
-            pc[s] = z.x;
-            ps[s] = z.y;
-          }
-        }
-        float x0[8], x1[8];
+      for (int hs = 0; hs < NHS; ++hs) {
+        q0[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + m * L::kQBlk);
+        q1[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + (MQ + m) * L::kQBlk);
+      }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          x0[s] = k0[s] * pc[s] - k1[s] * ps[s];
-          x1[s] = k1[s] * pc[s] + k0[s] * ps[s];
-        }
-        if constexpr (!L::kF32QK) {
-          half8 kh0, kl0, kh1, kl1;
-          split_f16(x0, kh0, kl0);
-          split_f16(x1, kh1, kl1);
-          const int d0 = chunk_dim<DH>(c, 0) + (DH / 8) * u, d1 = chunk_dim<DH>(c + NP, 0) + (DH / 8) * u;
-          const half8 qa0 = *reinterpret_cast<const half8*>(qh + d0);
-          const half8 qb0 = *reinterpret_cast<const half8*>(ql + d0);
-          const half8 qa1 = *reinterpret_cast<const half8*>(qh + d1);
-          const half8 qb1 = *reinterpret_cast<const half8*>(ql + d1);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qa0, S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qa0, S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qb0, S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qa1, S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qa1, S, 0, 0, 0);
-          S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qb1, S, 0, 0, 0);
-        } else {
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = k1[e] * pc[e] - k2[e] * ps[e];
+        const float x1 = k2[e] * pc[e] + k1[e] * ps[e];
 #pragma unroll
-          for (int hs = 0; hs < NHS; ++hs) {
-            const float* qs = qb + hs * L::qs_floats;
-            const floatx4 qa0 = *reinterpret_cast<const floatx4*>(qs + (2 * c) * L::kq_stride);
-            const floatx4 qa1 = *reinterpret_cast<const floatx4*>(qs + (2 * c + 1) * L::kq_stride);
-            const floatx4 qc0 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP)) * L::kq_stride);
-            const floatx4 qc1 = *reinterpret_cast<const floatx4*>(qs + (2 * (c + NP) + 1) * L::kq_stride);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[s], qa0[s], Sa[hs], 0, 0, 0);
-              Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[s], qc0[s], Sb[hs], 0, 0, 0);
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              Sa[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[4 + s], qa1[s], Sa[hs], 0, 0, 0);
-              Sb[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[4 + s], qc1[s], Sb[hs], 0, 0, 0);
-            }
-          }
+        for (int hs = 0; hs < NHS; ++hs) {
+          qk[hs][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(q0[hs][e], x0, qk[hs][0], 0, 0, 0);
+          qk[hs][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(q1[hs][e], x1, qk[hs][1], 0, 0, 0);
         }
       }
     }
 
-    const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
-    if constexpr (L::kF32QK) {
-      // ---- online softmax over the page, per head, in the log2 domain:
-      //      after the quarter sum lane l holds token tk, head slot 4 hs + l % 4
-      const int tk = 4 * ((lane_v >> 2) & 3) + ((0xD8 >> (2 * (lane_v >> 4))) & 3);
-      const bool tv = (vmask >> tk) & 1u;
+    // ---- logits and online softmax in the log2 domain: lane (row r, token
+    //      t) ends with head 4 hs + row_slot(r)'s logit of token t ----------
+    float x[NHS];
+    bool exceed = false;
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) {
+      floatx4 s;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = sg * qk[hs][1][i] + qk[hs][0][i];
+      const float lg = quarter_sum(s);            // the cross-lane sum runs on every lane
+      x[hs] = (valid && 4 * hs + hr < GQA) ? lg * a.scale_log2 : -INFINITY;
+      exceed |= x[hs] > m_run[hs] + kRescaleLog2;
+    }
+    // The running reference max of a head moves only when one of its logits
+    // exceeds it by more than 2^8, so p = 2^(x - m) <= 256 stays finite in
+    // fp16; the max over the row is taken only then.
+    if (__ballot(exceed) != 0) {
       float alpha[NHS];
-      bool upd_any = false;
 #pragma unroll
       for (int hs = 0; hs < NHS; ++hs) {
-        // the cross-lane sum runs on every lane (never under the token mask)
-        const float lg = quarter_sum(Sa[hs] + Sb[hs]);
-        const float x = tv ? lg * a.scale_log2 : -INFINITY;
-        const float mx = head_max(x);
-        const bool upd = mx > m_run[hs] + kRescaleLog2;
-        const float m_new = upd ? mx : m_run[hs];
-        alpha[hs] = upd ? __builtin_amdgcn_exp2f(m_run[hs] - m_new) : 1.f;
-        const _Float16 ph = (_Float16)(tv ? __builtin_amdgcn_exp2f(x - m_new) : 0.f);
-        l_run[hs] = alpha[hs] * l_run[hs] + head_sum((float)ph);
+        const float mx = row_max16(x[hs]);
+        const float m_new = mx > m_run[hs] + kRescaleLog2 ? mx : m_run[hs];
+        alpha[hs] = m_new == m_run[hs] ? 1.f : __builtin_amdgcn_exp2f(m_run[hs] - m_new);
+        l_part[hs] *= alpha[hs];
         m_run[hs] = m_new;
-        upd_any |= upd;
-        // ---- P[head][token] for the PV MFMA's A operand
-        if (4 * hs + (lane_v & 3) < GQA) pt[(4 * hs + (lane_v & 3)) * kTile + tk] = ph;
       }
-      if (__ballot(upd_any) != 0) {
-        // head 4 hs + i's factor lives in lane i; accumulators hold heads
-        // 4 hs + i in element i
+      // head slot i's factor lives in row slot_row(i); accumulators hold
+      // head slot i in element i
 #pragma unroll
-        for (int hs = 0; hs < NHS; ++hs)
+      for (int hs = 0; hs < NHS; ++hs)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[hs]), i));
+        for (int i = 0; i < 4; ++i) {
+          const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[hs]),
+                                                                            16 * slot_row(i)));
 #pragma unroll
-            for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
-          }
-      }
-    } else {
-      // ---- (GQA > 4) lane (u, hl): head hl, tokens 4u..4u+3; state m_run[0]
-      float x[4];
+          for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
+        }
+    }
+    // p rounded to fp16 for the PV MFMA, and the same rounded p summed into
+    // l, so the output stays an exact convex combination of V rows
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        x[s] = ((vmask >> (4 * u + s)) & 1u) ? S[s] * a.scale_log2 : -INFINITY;
-      const float mx = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-      const bool upd = mx > m_run[0] + kRescaleLog2;
-      const float m_new = upd ? mx : m_run[0];
-      const float alpha = upd ? __builtin_amdgcn_exp2f(m_run[0] - m_new) : 1.f;
-      half4 pa;
-      float es = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float e = (x[s] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[s] - m_new);
-        pa[s] = (_Float16)e;
-        es += (float)pa[s];
-      }
-      l_run[0] = alpha * l_run[0] + rows_sum(es);
-      m_run[0] = m_new;
-      if (__ballot(upd) != 0) {
-        // head h's factor lives in lane h (row u = 0); accumulators hold heads
-        // 4 hs + i in element i
-#pragma unroll
-        for (int hs = 0; hs < NHS; ++hs)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 * hs + i));
-#pragma unroll
-            for (int hf = 0; hf < NHF; ++hf) acc[hs][hf][i] *= f;
-          }
-      }
-      if (hl < GQA) *reinterpret_cast<half4*>(pt + hl * kTile + 4 * u) = pa;
+    for (int hs = 0; hs < NHS; ++hs) {
+      const _Float16 ph = (_Float16)(x[hs] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x[hs] - m_run[hs]));
+      l_part[hs] += (float)ph;
+      if (4 * hs + hr < GQA) pt[(4 * hs + hr) * kTile + t] = ph;
     }
 
     // ---- O += P V on the 4x4x4 MFMA (16 blocks = 16 groups of 4 dims):
@@ -832,6 +735,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     //      B = V[4 tokens][dim 64 hf + l] (lane l's own dim) -----------------
     // slots without a token get V = 0 (their p is already 0; this keeps
     // whatever bytes an unused slot holds out of the sum)
+    const uint32_t vmask = (uint32_t)__ballot(valid) & 0xFFFFu;
     if (vmask != 0xFFFFu) {
 #pragma unroll
       for (int v = 0; v < DH / 32; ++v)
@@ -877,6 +781,9 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 
   __builtin_amdgcn_s_setprio(0);
   if (nbad != 0 && lane == 0) __hip_atomic_fetch_add(a.status, (uint32_t)nbad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float l_run[NHS];
+#pragma unroll
+  for (int hs = 0; hs < NHS; ++hs) l_run[hs] = row_sum16(l_part[hs]);
   // ---- merge the waves' states in LDS, write this item's partial ----------
   constexpr int PS = partial_stride<DH, GQA>();
   __syncthreads();
@@ -889,17 +796,12 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       if (4 * hs + i < GQA)
 #pragma unroll
         for (int hf = 0; hf < NHF; ++hf) mrg[(wave * GQA + 4 * hs + i) * DH + 64 * hf + lane] = acc[hs][hf][i];
-  if constexpr (L::kF32QK) {
 #pragma unroll
-    for (int hs = 0; hs < NHS; ++hs)
-      if (lane < 4 && 4 * hs + lane < GQA) {
-        mrg_ml[(wave * GQA + 4 * hs + lane) * 2] = m_run[hs];
-        mrg_ml[(wave * GQA + 4 * hs + lane) * 2 + 1] = l_run[hs];
-      }
-  } else if ((lane & 15) < GQA && lane < 16) {
-    mrg_ml[(wave * GQA + lane) * 2] = m_run[0];
-    mrg_ml[(wave * GQA + lane) * 2 + 1] = l_run[0];
-  }
+  for (int hs = 0; hs < NHS; ++hs)
+    if (t == 0 && 4 * hs + hr < GQA) {
+      mrg_ml[(wave * GQA + 4 * hs + hr) * 2] = m_run[hs];
+      mrg_ml[(wave * GQA + 4 * hs + hr) * 2 + 1] = l_run[hs];
+    }
   __syncthreads();
   // every output thread derives its head's wave weights 2^(m_w - M) itself
   // (the kWaves reads of a head hit one LDS address each: broadcasts), so
