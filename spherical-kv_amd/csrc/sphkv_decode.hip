@@ -68,16 +68,20 @@ struct DecodeArgs {
   int32_t num_kv;
   int32_t num_rows;
   int32_t num_sh;        // num_seqs * num_kv
-  float scale_log2;      // sm_scale * log2(e)
+  int32_t pages32;       // pages_bytes (< 2^31)
+  int32_t pages_m8;      // pages_bytes - 8: last offset a page header fits at
+  int32_t nvp32;         // num_vpages clamped to 2^31 - 1
+  float scale_log2;      // sm_scale * log2(e): logit scale of dense pages
+  float scale_log2_c;    // scale_log2 / 127: compressed pages' radii carry the int8 code
   double log2_theta;
 };
 
 constexpr float kRescaleLog2 = 8.0f;   // reference-max hysteresis (log2 units)
 
 // Buffer resources of the kernel-wide arrays, built once per wave (scalar
-// registers).  Loads of absent data use an offset beyond every resource
-// (kOOB) and return zeros.  The byte pool, pointer table and positions are
-// below 2 GiB (checked by the host), so 32-bit offsets address them.
+// registers).  A load of absent data adds kOOB to its offset, which puts it
+// beyond every resource (the host keeps the byte pool and the position table
+// below kOOB bytes), so it returns zeros without touching memory.
 struct Res {
   rsrc_t pages, ptab, vslot, pos;
 };
@@ -91,73 +95,6 @@ __device__ __forceinline__ Res make_res(const DecodeArgs& a) {
   return r;
 }
 
-// Pointer-table row of one page (wave-uniform): lanes 0..2 fetch the row,
-// lane 3 the V slot; the values are read out (readlane) only when needed.
-struct RowLd { int x, y; };
-struct Row {
-  int page_off, th_off, rad_off, vs;
-  bool ok;         // the row is present and addresses the pools
-  bool present;    // the row is one of the item's (p < end)
-};
-
-__device__ __forceinline__ RowLd row_issue(const Res& rs, int p, int re, int lane) {
-  const bool ok = p < re;
-  RowLd l;
-  l.x = __builtin_amdgcn_raw_buffer_load_b32(rs.ptab, (ok && lane < 3) ? 12 * p + 4 * lane : kOOB, 0, 0);
-  l.y = __builtin_amdgcn_raw_buffer_load_b32(rs.vslot, (ok && lane == 3) ? 4 * p : kOOB, 0, 0);
-  return l;
-}
-
-__device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int p, int re) {
-  Row r;
-  r.page_off = __builtin_amdgcn_readlane(l.x, 0);
-  r.th_off = __builtin_amdgcn_readlane(l.x, 1);
-  r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
-  r.vs = __builtin_amdgcn_readlane(l.y, 3);
-  r.present = p < re;
-  r.ok = p < re && r.page_off >= 0 && (int64_t)r.page_off + 8 <= a.pages_bytes && (r.page_off & 3) == 0 &&
-         r.vs >= 0 && r.vs < a.num_vpages;
-  if (!r.ok) { r.page_off = 0; r.th_off = 0; r.rad_off = 0; r.vs = 0; }
-  return r;
-}
-
-// A dense page's theta section holds n*DH*2 bytes; a compressed page's at most
-// ceil(16*G*b/8) < 2*DH.  Used only to decide what to prefetch; the page header
-// decides how the page is processed.
-template <int DH>
-__device__ __forceinline__ bool row_looks_dense(const Row& r) {
-  return r.ok && (r.rad_off - r.th_off) >= 2 * DH && (r.th_off & 15) == 0 && r.th_off >= 0;
-}
-
-// 512-byte staging window [page_off & ~15, +512) of a page: lanes < 32 hold
-// 16 bytes each (bytes past the end of the pool read as zero).
-__device__ __forceinline__ uint4 load_stage(const Res& rs, const Row& r, int lane) {
-  const int off = (r.ok && lane < 32) ? (r.page_off & ~15) + 16 * lane : kOOB;
-  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, off, 0, 0);
-  return uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
-}
-
-__device__ __forceinline__ int load_pos(const Res& rs, const Row& r, int p, int t) {
-  return __builtin_amdgcn_raw_buffer_load_b32(rs.pos, r.ok ? (p * kTile + t) * 4 : kOOB, 0, 0);
-}
-
-// V page layout, dim-major: element (token k, dim d) at half d * 16 + k.  Lane
-// l loads dims l + 64 hf (hf < DH/64), 16 tokens = 32 bytes each: vreg[2hf]
-// holds tokens 0..7, vreg[2hf + 1] tokens 8..15 -- the B operands of the
-// 4x4x4 PV MFMA.
-template <int DH>
-__device__ __forceinline__ void load_v(const DecodeArgs& a, const Row& r, int lane, half8 (&vreg)[DH / 32]) {
-  // 64-bit element offset: vslot * DH * 16 exceeds 2^31 from vslot 2^20 (DH 128)
-  const rsrc_t rs = make_rsrc(a.v_pool + (int64_t)r.vs * (DH * kTile), r.ok ? DH * kTile * 2 : 0);
-#pragma unroll
-  for (int hf = 0; hf < DH / 64; ++hf)
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, ((lane + 64 * hf) * kTile + 8 * k) * 2, 0, 0);
-      vreg[2 * hf + k] = __builtin_bit_cast(half8, uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]});
-    }
-}
-
 // Dimension of element s of chunk c for lane quarter u.  A lane's chunks
 // cover two runs of DH/8 dimensions: [(DH/8)u, (DH/8)(u+1)) of the first RoPE
 // half (chunks c < NP) and the same run of the second half (chunks c >= NP),
@@ -169,28 +106,120 @@ __host__ __device__ constexpr int chunk_dim(int c, int u) {
   return (c >= DH / 64 ? DH / 2 : 0) + (DH / 8) * u + 8 * (c % (DH / 64));
 }
 
-// Dense K rows of a page (fp16 [n][DH] at th_off, 16-byte aligned): lane
-// (t, u) loads chunks c = 0..NC-1 (dims chunk_dim(c, u) .. +8) of token t.  The
-// resource covers the page's theta section only when the pointer-table row
-// describes a dense page, so compressed pages cost no traffic here.
+// Per-lane byte offsets of the page loads, fixed for a whole work item (lane
+// l = token t = l % 16, quarter u = l / 16).  Lanes that load nothing carry
+// kOOB; the page-dependent part is a wave-uniform base added to them.
+struct LaneOff {
+  uint32_t row, vs, stg, pos, kd, v;
+};
+
 template <int DH>
-__device__ __forceinline__ void load_dense(const Res& rs, const Row& r, int t, int u, uint4 (&kd)[DH / 32]) {
-  const bool dense = row_looks_dense<DH>(r) && (int64_t)r.th_off + (int64_t)(t + 1) * DH * 2 <= r.rad_off;
+__device__ __forceinline__ LaneOff lane_offsets(int lane) {
+  const int t = lane & 15, u = lane >> 4;
+  LaneOff o;
+  o.row = lane < 3 ? 4u * lane : (uint32_t)kOOB;            // pointer-table row: 3 dwords
+  o.vs = lane == 3 ? 0u : (uint32_t)kOOB;                   // V slot
+  o.stg = lane < 32 ? 16u * lane : (uint32_t)kOOB;          // 512-byte staging window
+  o.pos = 4u * t;                                           // position of token t
+  o.kd = (uint32_t)(t * DH + chunk_dim<DH>(0, u)) * 2u;     // dense K: chunk 0 of (t, u)
+  o.v = (uint32_t)lane * kTile * 2u;                        // V: dim `lane`, 16 tokens
+  return o;
+}
+
+__device__ __forceinline__ uint32_t oob_or(int ok, uint32_t base) { return ok ? base : (uint32_t)kOOB; }
+
+// Pointer-table row of one page (wave-uniform): lanes 0..2 fetch the row,
+// lane 3 the V slot; the values are read out (readlane) when the page is
+// taken.  The page loop's scalar conditions are kept as 0/1 integers, which
+// stay single scalar registers (boolean values become 64-bit lane masks).
+struct RowLd { int x, y; };
+struct Row {
+  int page_off, th_off, rad_off, vs;
+  int ok;          // 1: the row is one of the item's and addresses the pools
+  int present;     // 1: the row is one of the item's (p < end)
+};
+
+__device__ __forceinline__ RowLd row_issue(const Res& rs, const LaneOff& lo, int p, int re) {
+  const int ok = p < re;
+  RowLd l;
+  l.x = __builtin_amdgcn_raw_buffer_load_b32(rs.ptab, (int)(oob_or(ok, 12u * (uint32_t)p) + lo.row), 0, 0);
+  l.y = __builtin_amdgcn_raw_buffer_load_b32(rs.vslot, (int)(oob_or(ok, 4u * (uint32_t)p) + lo.vs), 0, 0);
+  return l;
+}
+
+__device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int p, int re) {
+  Row r;
+  r.page_off = __builtin_amdgcn_readlane(l.x, 0);
+  r.th_off = __builtin_amdgcn_readlane(l.x, 1);
+  r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
+  r.vs = __builtin_amdgcn_readlane(l.y, 3);
+  r.present = p < re;
+  // page_off >= 0, 4-byte aligned, header inside the pool; V slot in the pool
+  r.ok = r.present & (int)((r.page_off & 0x80000003) == 0) & (int)(r.page_off <= a.pages_m8) &
+         (int)((uint32_t)r.vs < (uint32_t)a.nvp32);
+  return r;
+}
+
+// A dense page's theta section holds n*DH*2 bytes; a compressed page's at most
+// ceil(16*G*b/8) < 2*DH.  Used only to decide what to prefetch; the page header
+// decides how the page is processed.
+template <int DH>
+__device__ __forceinline__ int row_looks_dense(const Row& r) {
+  return r.ok & (int)((r.th_off & 0x8000000F) == 0) & (int)(r.rad_off >= 0) &
+         (int)((uint32_t)r.th_off + 2 * DH <= (uint32_t)r.rad_off);
+}
+
+// 512-byte staging window [page_off, +512) of a page (page_off is 4-byte
+// aligned): lanes < 32 hold 16 bytes each (bytes past the pool read as zero),
+// the other lanes zeros; the page header is lane 0's first dword.
+__device__ __forceinline__ uint4 load_stage(const Res& rs, const LaneOff& lo, const Row& r) {
+  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, (int)(oob_or(r.ok, (uint32_t)r.page_off) + lo.stg), 0, 0);
+  return uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
+}
+
+__device__ __forceinline__ int load_pos(const Res& rs, const LaneOff& lo, const Row& r, int p) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rs.pos, (int)(oob_or(r.ok, (uint32_t)p * (4u * kTile)) + lo.pos), 0, 0);
+}
+
+// V page layout, dim-major: element (token k, dim d) at half d * 16 + k.  Lane
+// l loads dims l + 64 hf (hf < DH/64), 16 tokens = 32 bytes each: vreg[2hf]
+// holds tokens 0..7, vreg[2hf + 1] tokens 8..15 -- the B operands of the
+// 4x4x4 PV MFMA.
+template <int DH>
+__device__ __forceinline__ void load_v(const DecodeArgs& a, const LaneOff& lo, const Row& r, half8 (&vreg)[DH / 32]) {
+  // 64-bit element offset: vslot * DH * 16 exceeds 2^31 from vslot 2^20 (DH 128)
+  const rsrc_t rs = make_rsrc(a.v_pool + (int64_t)r.vs * (DH * kTile), r.ok ? DH * kTile * 2 : 0);
 #pragma unroll
-  for (int c = 0; c < DH / 32; ++c) {
-    const int off = dense ? r.th_off + (t * DH + chunk_dim<DH>(c, u)) * 2 : kOOB;
-    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, off, 0, 0);
+  for (int hf = 0; hf < DH / 64; ++hf)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(lo.v + (64 * hf * kTile + 8 * k) * 2), 0, 0);
+      vreg[2 * hf + k] = __builtin_bit_cast(half8, uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]});
+    }
+}
+
+// Dense K rows of a page (fp16 [n][DH] at th_off, 16-byte aligned): lane
+// (t, u) loads chunks c = 0..NC-1 (dims chunk_dim(c, u) .. +8) of token t.
+// Compressed pages load nothing.  Rows of tokens past the page's count read
+// neighbouring bytes of the pool (or zeros past its end) and are not used.
+template <int DH>
+__device__ __forceinline__ void load_dense(const Res& rs, const LaneOff& lo, const Row& r, uint4 (&kd)[DH / 32]) {
+  constexpr int NC = DH / 32;
+  const uint32_t base = oob_or(row_looks_dense<DH>(r), (uint32_t)r.th_off) + lo.kd;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t d = (uint32_t)(chunk_dim<DH>(c, 0) - chunk_dim<DH>(0, 0)) * 2u;
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, (int)(base + d), 0, 0);
     kd[c] = uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
   }
 }
 
-// Waves per decode workgroup: 12 (3 per SIMD, up to 168 VGPRs each), which
-// leaves room to keep the lane-derived addresses of the page loop in
-// registers for GQA <= 4 (decode_hoist); GQA 8 recomputes them per page.
+// Waves per decode workgroup: 12 (3 per SIMD, up to 168 VGPRs each), enough
+// to keep the per-lane offsets and addresses of the page loop in registers;
+// 8 (2 per SIMD, 256 VGPRs) for GQA 8, whose two head sets double the QK
+// operands and accumulators.
 template <int GQA>
-__host__ __device__ constexpr int decode_waves() { return 12; }
-template <int GQA>
-__host__ __device__ constexpr bool decode_hoist() { return GQA <= 4; }
+__host__ __device__ constexpr int decode_waves() { return GQA <= 4 ? 12 : 8; }
 constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| < kDelta
 
 __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
@@ -202,11 +231,11 @@ __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 //    RoPE frequencies j, 4 x cos(2 pi f_j d) then 4 x sin(2 pi f_j d), fp32,
 //    rows padded by 16 bytes;
 //  * f_j in turns per token (fp64);
-//  * per wave: the 512-byte staging window of its page, the query rows
-//    rotated to the page centre (fp32, in the QK MFMA's operand order; slots
-//    of heads >= GQA stay zero), and the page's softmax weights P as fp16
-//    [max(GQA, 4)][16 tokens] (rows >= GQA stay zero), read back as the PV
-//    MFMA's A operand.
+//  * per wave: the staging area of its page (1 KB: the 512-byte window and the
+//    zeros of the lanes that load nothing), the query rows rotated to the page
+//    centre (fp32, in the QK MFMA's operand order; slots of heads >= GQA stay
+//    zero), and the page's softmax weights P as fp16 [max(GQA, 4)][16 tokens]
+//    (rows >= GQA stay zero), read back as the PV MFMA's A operand.
 template <int DH, int GQA>
 struct DecodeLds {
   static constexpr int kWaves = decode_waves<GQA>();
@@ -225,6 +254,7 @@ struct DecodeLds {
   static constexpr int o_dtab = align16(4 * (cb_n1 + cb_n2 + cb_n3));
   static constexpr int o_ftab = o_dtab + kDelta * drow;
   static constexpr int o_stage = o_ftab + NJ * 8;
+  static constexpr int stage_bytes = 1024;
   static constexpr int PR = GQA < 4 ? 4 : GQA;                   // heads padded to 4 (slots)
   static constexpr int NHS = PR / 4;                             // sets of 4 head slots
   // rotated query, fp32, per set of 4 head slots: block (half hf, group m)
@@ -235,7 +265,7 @@ struct DecodeLds {
   // per lane, banks (4 m + e + 16 u) mod 64 distinct) are conflict-free.
   static constexpr int kQBlk = 68;
   static constexpr int qset = 2 * MQ * kQBlk;                    // floats per head-slot set
-  static constexpr int o_qr = o_stage + kWaves * 512;
+  static constexpr int o_qr = o_stage + kWaves * stage_bytes;
   static constexpr int qr_wave = NHS * qset * 4;                 // bytes per wave
   static constexpr int o_pt = o_qr + kWaves * qr_wave;
   static constexpr int total = o_pt + kWaves * PR * 32;
@@ -247,52 +277,33 @@ struct DecodeLds {
 };
 
 // This lane's two codebook groups (one per RoPE half) of token t on a staged
-// compressed page: LDS offset (floats) of the centroid run the lane needs and
-// the radius r_hat = int8 / 127 * scale (pagebuilder.py:17-21).
+// compressed page (page byte 0 at st[0]; sections at thr / rdr): LDS byte
+// offsets of the two centroid runs the lane needs, and the radii rc * scale
+// (pagebuilder.py:17-21 without the 1/127 of the int8 code, which the page's
+// logit scale carries).  Only tokens t < n use the results; the reads of the
+// others stay inside the wave's 1 KB staging area.
 template <int DH, int GQA, int TID>
-__device__ __forceinline__ void locate_k(const uint8_t* st, int rel, int thr, int rdr, int t, int u, int n,
-                                         int (&cofs)[2], float (&rh)[2]) {
+__device__ __forceinline__ void locate_k(const uint8_t* st, int thr, int rdr, int t, int u, int (&cofs)[2],
+                                         float (&rh)[2]) {
   constexpr int g = tier_g(TID), b = tier_b(TID), C = tier_C(TID);
   constexpr int G = DH / g;
   using L = DecodeLds<DH, GQA>;
-  const bool live = t < n;
-  uint64_t bits = 0;
-  uint32_t rad[2] = {0u, 0u};
-  if (live) {
-    if constexpr (TID == 1 && G == 8) {            // 48 bits per token at byte 6t (2-aligned)
-      const uint16_t* p16 = reinterpret_cast<const uint16_t*>(st + thr + 6 * t);
-      bits = (uint64_t)p16[0] | ((uint64_t)p16[1] << 16) | ((uint64_t)p16[2] << 32);
-    } else if constexpr (TID == 2 && G == 8) {     // 32 bits per token at byte 4t
-      bits = *reinterpret_cast<const uint32_t*>(st + thr + 4 * t);
-    } else if constexpr (TID == 1 && G == 4) {     // 24 bits per token at byte 3t
-      const uint8_t* p8 = st + thr + 3 * t;
-      bits = (uint64_t)p8[0] | ((uint64_t)p8[1] << 8) | ((uint64_t)p8[2] << 16);
-    } else if constexpr (TID == 2 && G == 4) {     // 16 bits per token at byte 2t
-      bits = *reinterpret_cast<const uint16_t*>(st + thr + 2 * t);
-    } else {                                       // tier 3: G*3 bits at bit G*3*t
-      const int bit0 = t * G * b;
-      const uint8_t* p8 = st + thr + (bit0 >> 3);
-      bits = ((uint64_t)p8[0] | ((uint64_t)p8[1] << 8) | ((uint64_t)p8[2] << 16)) >> (bit0 & 7);
-    }
-    if constexpr (G == 8) {
-      rad[0] = *reinterpret_cast<const uint32_t*>(st + rdr + 8 * t);
-      rad[1] = *reinterpret_cast<const uint32_t*>(st + rdr + 8 * t + 4);
-    } else if constexpr (G == 4) {
-      rad[0] = *reinterpret_cast<const uint32_t*>(st + rdr + 4 * t);
-    } else {
-      rad[0] = *reinterpret_cast<const uint16_t*>(st + rdr + 2 * t);
-    }
-  }
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    const int d0 = hf * (DH / 2) + (DH / 8) * u;
-    const int gi = d0 / g, off = d0 - gi * g;
-    const int code = (int)((bits >> (gi * b)) & ((1u << b) - 1));
-    const int rc = (int)(int8_t)((rad[gi >> 2] >> (8 * (gi & 3))) & 0xFFu);
-    const float sc = live ? *reinterpret_cast<const float*>(st + rel + kHeaderBytes + 4 * gi) : 0.f;
-    rh[hf] = (float)rc * sc * (1.0f / 127.0f);
-    cofs[hf] = L::cb_off(TID) + (gi * C + code) * L::cb_pad(g) + off;
-  }
+  const int d0 = (DH / 8) * u;
+  const int gi = d0 / g, off = d0 % g;                 // first-half group; its RoPE partner is gi + G/2
+  // both codes lie in the 64 bits from the dword holding the first one
+  // (token bits LSB first, bitpacking.py:5-29)
+  const uint32_t bit = (uint32_t)(thr * 8 + t * (G * b) + gi * b);
+  const uint32_t* wp = reinterpret_cast<const uint32_t*>(st) + ((bit >> 5) & 127);
+  const uint32_t w = __builtin_amdgcn_alignbit(wp[1], wp[0], bit);
+  const int c0 = (int)(w & (C - 1));
+  const int c1 = (int)((w >> ((G / 2) * b)) & (C - 1));
+  const int8_t* rp = reinterpret_cast<const int8_t*>(st + rdr + t * G + gi);
+  const float* sp = reinterpret_cast<const float*>(st + kHeaderBytes) + gi;
+  rh[0] = (float)rp[0] * sp[0];
+  rh[1] = (float)rp[G / 2] * sp[G / 2];
+  constexpr int row = L::cb_pad(g) * 4;                // bytes per padded centroid row
+  cofs[0] = L::cb_off(TID) * 4 + (gi * C + c0) * row + off * 4;
+  cofs[1] = L::cb_off(TID) * 4 + ((gi + G / 2) * C + c1) * row + off * 4;
 }
 
 // Partial of one work item: [16 floats: m[GQA], l[GQA], pad] [acc: GQA * DH]
@@ -350,6 +361,15 @@ __device__ __forceinline__ float quarter_sum(floatx4 s) {
 __host__ __device__ constexpr int row_slot(int row) { return (0xD8 >> (2 * row)) & 3; }   // {0, 2, 1, 3}
 __host__ __device__ constexpr int slot_row(int slot) { return (0xD8 >> (2 * slot)) & 3; }  // its inverse
 
+__device__ __forceinline__ void set_prio(int lvl) {
+  if (lvl >= 3) __builtin_amdgcn_s_setprio(3);
+  else if (lvl == 2) __builtin_amdgcn_s_setprio(2);
+  else if (lvl == 1) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
+template <bool B> struct Flag { static constexpr bool value = B; };
+
 template <int DH, int GQA>
 __global__ __launch_bounds__(decode_waves<GQA>() * 64)
 __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() / 4))) void decode_kernel(
@@ -387,15 +407,17 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   const int seq = sh / a.num_kv;
   const int t = lane & 15;
   const int u = lane >> 4;
-  uint8_t* st = smem + L::o_stage + wave * 512;
+  uint8_t* st = smem + L::o_stage + wave * L::stage_bytes;
   float* qr = reinterpret_cast<float*>(smem + L::o_qr + wave * L::qr_wave);
+  _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
+  const LaneOff lo = lane_offsets<DH>(lane);
 
   int p = rb + wave * rstride;
   const Res rs = make_res(a);
   // ---- first pages' pointer-table rows, then the shared tables' loads ----
-  RowLd rl_c = row_issue(rs, p, re, lane);
-  RowLd rl_n = row_issue(rs, p + wstride, re, lane);
-  RowLd rl_2 = row_issue(rs, p + 2 * wstride, re, lane);
+  RowLd rl_c = row_issue(rs, lo, p, re);
+  RowLd rl_n = row_issue(rs, lo, p + wstride, re);
+  RowLd rl_2 = row_issue(rs, lo, p + 2 * wstride, re);
   // codebooks: every load of a thread is issued before its first LDS store
   constexpr int kT = kWaves * 64;
   constexpr int n4_1 = L::cb_n1 / 20 * 4, n4_2 = L::cb_n2 / 20 * 4, n4_3 = L::cb_n3 / 36 * 8;  // float4s
@@ -432,20 +454,11 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     if (lane < (4 - GQA) * 2) {
       half8 z;
       for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.f;
-      *reinterpret_cast<half8*>(reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile + GQA * kTile + 8 * lane) = z;
+      *reinterpret_cast<half8*>(pt + GQA * kTile + 8 * lane) = z;
     }
     for (int i = lane; i < 2 * MQ * 16; i += 64)          // i = (block, u, slot)
       if ((i & 3) >= GQA) *reinterpret_cast<floatx4*>(qr + (i >> 4) * L::kQBlk + 4 * (i & 15)) = (floatx4){0.f, 0.f, 0.f, 0.f};
   }
-  // first page's data and the next page's row
-  Row row_c = row_take(a, rl_c, p, re);
-  uint4 stg_c = load_stage(rs, row_c, lane);
-  int pos_c = load_pos(rs, row_c, p, t);
-  half8 vreg[DH / 32];
-  load_v<DH>(a, row_c, lane, vreg);
-  uint4 kd[NC];
-  load_dense<DH>(rs, row_c, t, u, kd);
-  Row row_n = row_take(a, rl_n, p + wstride, re);
   {
     int slot = 0;
 #pragma unroll
@@ -462,6 +475,13 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       }
     }
   }
+  // first page's staging window and positions (the rows were issued first,
+  // so they are in by now); its V and dense K are issued after the barrier,
+  // behind every wave's staging loads
+  Row row_c = row_take(a, rl_c, p, re);
+  uint4 stg_c = load_stage(rs, lo, row_c);
+  int pos_c = load_pos(rs, lo, row_c, p);
+  Row row_n = row_take(a, rl_n, p + wstride, re);
   if (threadIdx.x < NJ)
     ftab[threadIdx.x] = exp2(-(2.0 * threadIdx.x / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
   __syncthreads();
@@ -472,10 +492,21 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     row[j & 3] = z.x;
     row[4 + (j & 3)] = z.y;
   }
+  half8 vreg[DH / 32];
+  uint4 kd[NC];
   __syncthreads();
-  // everything loaded so far is complete before the page pipeline starts, so
-  // no wait inside the loop has to account for it
-  __builtin_amdgcn_s_waitcnt(0);
+  load_v<DH>(a, lo, row_c, vreg);
+  if (row_looks_dense<DH>(row_c)) load_dense<DH>(rs, lo, row_c, kd);
+
+  // Loop-invariant lane data: this lane's RoPE frequency (query rotation),
+  // LDS addresses of its query writes / reads and P write / read.
+  const double f_lane = ftab[lane % NJ];
+  float* qw;
+  {
+    const int j = lane % NJ, s = j % NPAIR;
+    qw = qr + (s >> 2) * L::kQBlk + (j / NPAIR) * 16 + (s & 3);
+  }
+  const float* qb = qr + u * 16 + (lane & 3) * 4;
 
   // Online-softmax state.  After a page's quarter sums, lane (row r, token t)
   // holds the logit of head 4 hs + row_slot(r) for token t; the running
@@ -494,9 +525,16 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   for (int hs = 0; hs < NHS; ++hs)
 #pragma unroll
     for (int hf = 0; hf < NHF; ++hf) acc[hs][hf] = (floatx4){0.f, 0.f, 0.f, 0.f};
-  _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
 
   int pages_done = 0;                                   // pages of this wave processed so far
+  int prio_next = 0;                                    // pages_done at which the priority changes
+  // issue priority of the wave's page d from its share of pages still to do:
+  // a SIMD serves its waves oldest first, so without it the youngest wave
+  // would finish last, alone on its SIMD
+  auto prio_of = [&](int d) {
+    const int left = nwp - d;                           // pages left, page d included
+    return 4 * left > 3 * nwp ? 3 : (2 * left > nwp ? 2 : (4 * left > nwp ? 1 : 0));
+  };
   int nbad = 0;                                         // malformed rows / pages of this wave
   // One page of the pipeline.  The staging window and positions of the next
   // page are loaded into the other register set of a pair, and the pointer-
@@ -505,105 +543,87 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // wait for that load.
   auto step = [&](const int p, uint4& stg_c, int& pos_c, uint4& stg_n, int& pos_n, RowLd& rl_issue,
                   RowLd& rl_take) __attribute__((always_inline)) {
-    // Without hoisting, lane-derived addresses are recomputed each iteration
-    // (a few VALU ops): the opaque copy of the lane id keeps the compiler from
-    // hoisting them into registers the budget does not have.
-    int lane_v = lane;
-    if constexpr (!decode_hoist<GQA>()) asm volatile("" : "+v"(lane_v));
-    const int t = lane_v & 15;
-    const int u = lane_v >> 4;
-    // ---- issue priority from this wave's share of pages still to do: a
-    //      SIMD serves its waves oldest first, so without it the youngest
-    //      wave would finish last, alone on its SIMD ---------------------------
-    {
-      const int left = nwp - pages_done;                                // pages left, this one included
-      const int lvl = 4 * left > 3 * nwp ? 3 : (2 * left > nwp ? 2 : (4 * left > nwp ? 1 : 0));
-      if (lvl >= 3) __builtin_amdgcn_s_setprio(3);
-      else if (lvl == 2) __builtin_amdgcn_s_setprio(2);
-      else if (lvl == 1) __builtin_amdgcn_s_setprio(1);
-      else __builtin_amdgcn_s_setprio(0);
+    // ---- issue priority (changes at most three times per item) ----------
+    if (pages_done == prio_next) {
+      const int lvl = prio_of(pages_done);
+      set_prio(lvl);
+      int d = pages_done + 1;
+      while (d < nwp && prio_of(d) == lvl) ++d;
+      prio_next = d;
     }
     // ---- issue: row three pages ahead, stage/positions one page ahead -----
-    rl_issue = row_issue(rs, p + 3 * wstride, re, lane);
-    stg_n = load_stage(rs, row_n, lane);
-    pos_n = load_pos(rs, row_n, p + wstride, t);
+    rl_issue = row_issue(rs, lo, p + 3 * wstride, re);
+    stg_n = load_stage(rs, lo, row_n);
+    pos_n = load_pos(rs, lo, row_n, p + wstride);
 
-    // ---- this page's header (lane 0's 16 bytes of the stage) --------------
-    const int rel = (int)(row_c.page_off & 15);
-    uint32_t hw = rel == 0 ? stg_c.x : (rel == 4 ? stg_c.y : (rel == 8 ? stg_c.z : stg_c.w));
-    hw = (uint32_t)__builtin_amdgcn_readfirstlane((int)hw);
-    int tid = row_c.ok ? (int)(hw & 0xFF) : 0;
-    const int cnt = (int)((hw >> 8) & 0xFF);
+    // ---- this page's header: lane 0's first dword of the stage ------------
+    const int hw = __builtin_amdgcn_readfirstlane((int)stg_c.x);
+    const int tid = row_c.ok ? (hw & 0xFF) : 0;
+    const int cnt = (hw >> 8) & 0xFF;
     // A malformed row or page contributes no token and is counted: a row that
     // does not address the pools, an unknown tier id, a count above 16, a
     // dense page whose K rows are not 16-byte aligned inside its section and
     // the pool, a compressed page whose sections leave its 512-byte staging
     // window or the pool.
-    bool bad = row_c.present && !row_c.ok;
-    if (!(tid == kDenseTier || (tid >= 1 && tid <= 3))) {
-      bad = bad || row_c.ok;
-      tid = 0;
+    const int dense = (int)(tid == kDenseTier);
+    const int comp = (int)((uint32_t)(tid - 1) < 3u);        // tiers 1..3
+    int bad = (row_c.present & (row_c.ok ^ 1)) | (row_c.ok & ((dense | comp) ^ 1)) |
+              ((dense | comp) & (int)(cnt > kTile));
+    int n = (dense | comp) ? min(cnt, kTile) : 0;
+    int thr = 0, rdr = 0;                       // section offsets from the page start
+    if (comp) {
+      // bits per token (G*b) and radius bytes per token (G) of tiers 1, 2, 3
+      constexpr uint32_t kGb = DH == 128 ? (48u | 32u << 8 | 12u << 16) : (24u | 16u << 8 | 6u << 16);
+      constexpr uint32_t kGg = DH == 128 ? (8u | 8u << 8 | 4u << 16) : (4u | 4u << 8 | 2u << 16);
+      const int sh8 = 8 * (tid - 1);
+      const int tb = (n * (int)((kGb >> sh8) & 0xFF) + 7) >> 3, rbytes = n * (int)((kGg >> sh8) & 0xFF);
+      const int t0 = (int)((uint32_t)row_c.th_off - (uint32_t)row_c.page_off);
+      const int r0 = (int)((uint32_t)row_c.rad_off - (uint32_t)row_c.page_off);
+      const int sec_ok = (int)(row_c.th_off >= row_c.page_off) & (int)(row_c.rad_off >= row_c.page_off) &
+                         (int)(t0 <= 508 - tb) & (int)(r0 <= 512 - rbytes) &
+                         (int)(row_c.th_off <= a.pages32 - tb) & (int)(row_c.rad_off <= a.pages32 - rbytes);
+      bad |= sec_ok ^ 1;
+      n = sec_ok ? n : 0;
+      thr = sec_ok ? t0 : 0;
+      rdr = sec_ok ? r0 : 0;
+    } else if (dense) {
+      const uint32_t kend = (uint32_t)row_c.th_off + (uint32_t)(n * DH * 2);
+      const int dense_ok = row_looks_dense<DH>(row_c) & (int)(kend <= (uint32_t)row_c.rad_off) &
+                           (int)(kend <= (uint32_t)a.pages32);
+      bad |= dense_ok ^ 1;
+      n = dense_ok ? n : 0;
     }
-    if (tid != 0 && cnt > kTile) bad = true;
-    int n = (tid == 0) ? 0 : min(cnt, kTile);
-    if (tid == kDenseTier &&
-        !(row_looks_dense<DH>(row_c) && (int64_t)row_c.th_off + (int64_t)n * DH * 2 <= row_c.rad_off &&
-          (int64_t)row_c.th_off + (int64_t)n * DH * 2 <= a.pages_bytes)) {
-      bad = true;
-      tid = 0;
-      n = 0;
-    }
-    int thr = 0, rdr = 0;                       // section offsets in the staging window
-    if (tid >= 1 && tid <= 3) {
-      const int base = row_c.page_off & ~15;
-      const int thr0 = row_c.th_off - base, rdr0 = row_c.rad_off - base;   // offsets are < 2^31
-      const int G = DH / tier_g(tid);
-      const int tb = (n * G * tier_b(tid) + 7) / 8;
-      const bool sec_ok = row_c.th_off >= base && row_c.rad_off >= base && thr0 + tb + 2 < 512 &&
-                          rdr0 + n * G <= 512 && (int64_t)row_c.th_off + tb <= a.pages_bytes &&
-                          (int64_t)row_c.rad_off + n * G <= a.pages_bytes;
-      if (sec_ok) {
-        thr = thr0;
-        rdr = rdr0;
-      } else {
-        bad = true;
-        n = 0;
-      }
-    }
-    nbad += bad ? 1 : 0;
-    if (!row_c.ok) pos_c = -1;
+    nbad += bad;
     const bool valid = (t < n) && (pos_c >= 0);
 
     // ---- page centre t_mid; query rows rotated by -t_mid into LDS ---------
     //      <q, R(pos) k> = <R(-t_mid) q, R(pos - t_mid) k>
-    int t_lo = __builtin_amdgcn_readlane(pos_c, 0);
-    int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
-    const int t_mid = (t_lo >= 0 && t_hi >= 0) ? (t_lo + t_hi) >> 1 : max(t_lo, 0);
-    if (lane_v < NJ) {
-      // lane = frequency j: pair e = j mod 4 of group m of quarter j / NPAIR
-      const int j = lane_v;
-      const float2 z = turn_phasor((double)t_mid * ftab[j]);
-      const int s = j % NPAIR;
-      float* w0 = qr + (s >> 2) * L::kQBlk + (j / NPAIR) * 16 + (s & 3);
-      float* w1 = w0 + MQ * L::kQBlk;
+    {
+      const int t_lo = __builtin_amdgcn_readlane(pos_c, 0);
+      const int t_hi = __builtin_amdgcn_readlane(pos_c, n > 0 ? n - 1 : 0);
+      const int t_mid = (t_lo >= 0 && t_hi >= 0) ? t_lo + ((t_hi - t_lo) >> 1) : max(t_lo, 0);
+      // lane = frequency j (lanes j and j + NJ write the same values when NJ = 32)
+      const float2 z = turn_phasor((double)t_mid * f_lane);
 #pragma unroll
       for (int hh = 0; hh < GQA; ++hh) {
         const int o = (hh >> 2) * L::qset + (hh & 3) * 4;
-        w0[o] = qf[hh][0] * z.x + qf[hh][1] * z.y;
-        w1[o] = qf[hh][1] * z.x - qf[hh][0] * z.y;
+        qw[o] = qf[hh][0] * z.x + qf[hh][1] * z.y;
+        qw[o + MQ * L::kQBlk] = qf[hh][1] * z.x - qf[hh][0] * z.y;
       }
+      // offset of this lane's token from the centre
+      pos_c = valid ? pos_c - t_mid : 0;
     }
+    const int dl = pos_c;
 
     // ---- locate this page's keys: centroid offsets + radii (compressed) ---
-    const bool dense = tid == kDenseTier;
     int cofs[2] = {0, 0};
     float rh[2] = {1.f, 1.f};                   // dense K enters unscaled
-    if (tid >= 1 && tid <= 3) {
-      if (lane_v < 32) *reinterpret_cast<uint4*>(st + 16 * lane_v) = stg_c;
+    if (comp) {
+      *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
       wave_lds_sync();
-      if (tid == 1) locate_k<DH, GQA, 1>(st, rel, thr, rdr, t, u, n, cofs, rh);
-      else if (tid == 2) locate_k<DH, GQA, 2>(st, rel, thr, rdr, t, u, n, cofs, rh);
-      else locate_k<DH, GQA, 3>(st, rel, thr, rdr, t, u, n, cofs, rh);
+      if (tid == 1) locate_k<DH, GQA, 1>(st, thr, rdr, t, u, cofs, rh);
+      else if (tid == 2) locate_k<DH, GQA, 2>(st, thr, rdr, t, u, cofs, rh);
+      else locate_k<DH, GQA, 3>(st, thr, rdr, t, u, cofs, rh);
     }
     wave_lds_sync();
 
@@ -619,72 +639,79 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     //      x0 or x1' of the lane's own token (column), one pair per
     //      instruction), so every lane's accumulators hold its own token's
     //      sums for head slots 0..3 and sg applies per lane afterwards.
-    //      Phasors come from the LDS delta table, or are formed directly when
-    //      |d| >= kDelta.
-    const int dl = valid ? pos_c - t_mid : 0;
+    //      Phasors come from the LDS delta table; a page with a lane at
+    //      |d| >= kDelta forms every lane's phasors directly.
     const int ad = dl < 0 ? -dl : dl;
-    const bool near = ad < kDelta;
-    const bool any_far = __ballot(!near) != 0;
-    const float* drw = reinterpret_cast<const float*>(dtab + (near ? ad : 0) * L::drow) + 2 * NPAIR * u;
-    const float* qb = qr + u * 16 + (lane_v & 3) * 4;
+    const bool any_far = __ballot(ad >= kDelta) != 0;
     const float sg = dl < 0 ? -1.f : 1.f;
     const float r1 = rh[0], r2 = sg * rh[1];
     const uint32_t kneg = dl < 0 ? 0x80008000u : 0u;  // dense: sg applied to K2's fp16 sign bits
+    const float* drw = reinterpret_cast<const float*>(dtab + (any_far ? 0 : ad) * L::drow) + 2 * NPAIR * u;
     floatx4 qk[NHS][2];
 #pragma unroll
     for (int hs = 0; hs < NHS; ++hs) { qk[hs][0] = (floatx4){0.f, 0.f, 0.f, 0.f}; qk[hs][1] = qk[hs][0]; }
+    auto kpath = [&](auto far_f, auto dense_f) __attribute__((always_inline)) {
+      constexpr bool FAR = decltype(far_f)::value, DENSE = decltype(dense_f)::value;
 #pragma unroll
-    for (int m = 0; m < MQ; ++m) {
-      float k1[4], k2[4];                        // k1 = r1 c1, k2 = sg r2 c2 on pairs 4m .. 4m + 3
-      if (dense) {
-        const uint4 w0 = kd[m >> 1], w1 = kd[NC / 2 + (m >> 1)];
-        const uint32_t a0 = (m & 1) ? w0.z : w0.x, a1 = (m & 1) ? w0.w : w0.y;
-        const uint32_t b0 = ((m & 1) ? w1.z : w1.x) ^ kneg, b1 = ((m & 1) ? w1.w : w1.y) ^ kneg;
-        const half2v ha0 = __builtin_bit_cast(half2v, a0), ha1 = __builtin_bit_cast(half2v, a1);
-        const half2v hb0 = __builtin_bit_cast(half2v, b0), hb1 = __builtin_bit_cast(half2v, b1);
-        k1[0] = (float)ha0[0]; k1[1] = (float)ha0[1]; k1[2] = (float)ha1[0]; k1[3] = (float)ha1[1];
-        k2[0] = (float)hb0[0]; k2[1] = (float)hb0[1]; k2[2] = (float)hb1[0]; k2[3] = (float)hb1[1];
-      } else {
-        const float4 c0 = *reinterpret_cast<const float4*>(cb_s + cofs[0] + 4 * m);
-        const float4 c1 = *reinterpret_cast<const float4*>(cb_s + cofs[1] + 4 * m);
-        k1[0] = r1 * c0.x; k1[1] = r1 * c0.y; k1[2] = r1 * c0.z; k1[3] = r1 * c0.w;
-        k2[0] = r2 * c1.x; k2[1] = r2 * c1.y; k2[2] = r2 * c1.z; k2[3] = r2 * c1.w;
-      }
-      float pc[4], ps[4];
-      {
-        const float4 c03 = *reinterpret_cast<const float4*>(drw + 8 * m);
-        const float4 s03 = *reinterpret_cast<const float4*>(drw + 8 * m + 4);
-        pc[0] = c03.x; pc[1] = c03.y; pc[2] = c03.z; pc[3] = c03.w;
-        ps[0] = s03.x; ps[1] = s03.y; ps[2] = s03.z; ps[3] = s03.w;
-      }
-      if (any_far && !near) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float2 z = turn_phasor((double)ad * ftab[NPAIR * u + 4 * m + e]);
-          pc[e] = z.x;
-          ps[e] = z.y;
+      for (int m = 0; m < MQ; ++m) {
+        float k1[4], k2[4];                      // k1 = r1 c1, k2 = sg r2 c2 on pairs 4m .. 4m + 3
+        if constexpr (DENSE) {
+          const uint4 w0 = kd[m >> 1], w1 = kd[NC / 2 + (m >> 1)];
+          const uint32_t a0 = (m & 1) ? w0.z : w0.x, a1 = (m & 1) ? w0.w : w0.y;
+          const uint32_t b0 = ((m & 1) ? w1.z : w1.x) ^ kneg, b1 = ((m & 1) ? w1.w : w1.y) ^ kneg;
+          const half2v ha0 = __builtin_bit_cast(half2v, a0), ha1 = __builtin_bit_cast(half2v, a1);
+          const half2v hb0 = __builtin_bit_cast(half2v, b0), hb1 = __builtin_bit_cast(half2v, b1);
+          k1[0] = (float)ha0[0]; k1[1] = (float)ha0[1]; k1[2] = (float)ha1[0]; k1[3] = (float)ha1[1];
+          k2[0] = (float)hb0[0]; k2[1] = (float)hb0[1]; k2[2] = (float)hb1[0]; k2[3] = (float)hb1[1];
+        } else {
+          const float4 c0 = *reinterpret_cast<const float4*>(smem + cofs[0] + 16 * m);
+          const float4 c1 = *reinterpret_cast<const float4*>(smem + cofs[1] + 16 * m);
+          k1[0] = r1 * c0.x; k1[1] = r1 * c0.y; k1[2] = r1 * c0.z; k1[3] = r1 * c0.w;
+          k2[0] = r2 * c1.x; k2[1] = r2 * c1.y; k2[2] = r2 * c1.z; k2[3] = r2 * c1.w;
         }
-      }
-      floatx4 q0[NHS], q1[NHS];
+        float pc[4], ps[4];
+        if constexpr (FAR) {
 #pragma unroll
-      for (int hs = 0; hs < NHS; ++hs) {
-        q0[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + m * L::kQBlk);
-        q1[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + (MQ + m) * L::kQBlk);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = k1[e] * pc[e] - k2[e] * ps[e];
-        const float x1 = k2[e] * pc[e] + k1[e] * ps[e];
+          for (int e = 0; e < 4; ++e) {
+            const float2 z = turn_phasor((double)ad * ftab[NPAIR * u + 4 * m + e]);
+            pc[e] = z.x;
+            ps[e] = z.y;
+          }
+        } else {
+          const float4 c03 = *reinterpret_cast<const float4*>(drw + 8 * m);
+          const float4 s03 = *reinterpret_cast<const float4*>(drw + 8 * m + 4);
+          pc[0] = c03.x; pc[1] = c03.y; pc[2] = c03.z; pc[3] = c03.w;
+          ps[0] = s03.x; ps[1] = s03.y; ps[2] = s03.z; ps[3] = s03.w;
+        }
+        floatx4 q0[NHS], q1[NHS];
 #pragma unroll
         for (int hs = 0; hs < NHS; ++hs) {
-          qk[hs][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(q0[hs][e], x0, qk[hs][0], 0, 0, 0);
-          qk[hs][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(q1[hs][e], x1, qk[hs][1], 0, 0, 0);
+          q0[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + m * L::kQBlk);
+          q1[hs] = *reinterpret_cast<const floatx4*>(qb + hs * L::qset + (MQ + m) * L::kQBlk);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = k1[e] * pc[e] - k2[e] * ps[e];
+          const float x1 = k2[e] * pc[e] + k1[e] * ps[e];
+#pragma unroll
+          for (int hs = 0; hs < NHS; ++hs) {
+            qk[hs][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(q0[hs][e], x0, qk[hs][0], 0, 0, 0);
+            qk[hs][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(q1[hs][e], x1, qk[hs][1], 0, 0, 0);
+          }
         }
       }
+    };
+    if (!any_far) {
+      if (dense) kpath(Flag<false>(), Flag<true>());
+      else kpath(Flag<false>(), Flag<false>());
+    } else {
+      if (dense) kpath(Flag<true>(), Flag<true>());
+      else kpath(Flag<true>(), Flag<false>());
     }
 
     // ---- logits and online softmax in the log2 domain: lane (row r, token
     //      t) ends with head 4 hs + row_slot(r)'s logit of token t ----------
+    const float scale = dense ? a.scale_log2 : a.scale_log2_c;
     float x[NHS];
     bool exceed = false;
 #pragma unroll
@@ -693,7 +720,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[i] = sg * qk[hs][1][i] + qk[hs][0][i];
       const float lg = quarter_sum(s);            // the cross-lane sum runs on every lane
-      x[hs] = (valid && 4 * hs + hr < GQA) ? lg * a.scale_log2 : -INFINITY;
+      x[hs] = (valid && 4 * hs + hr < GQA) ? lg * scale : -INFINITY;
       exceed |= x[hs] > m_run[hs] + kRescaleLog2;
     }
     // The running reference max of a head moves only when one of its logits
@@ -746,7 +773,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     wave_lds_sync();
 #pragma unroll
     for (int hs = 0; hs < NHS; ++hs) {
-      const half8* prow = reinterpret_cast<const half8*>(pt + (4 * hs + (lane_v & 3)) * kTile);
+      const half8* prow = reinterpret_cast<const half8*>(pt + (4 * hs + (lane & 3)) * kTile);
       const half8 p0 = prow[0], p1 = prow[1];
 #pragma unroll
       for (int tg = 0; tg < 4; ++tg) {
@@ -762,8 +789,15 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     }
 
     // ---- issue V / dense K of the next page into the freed registers ------
-    load_v<DH>(a, row_n, lane_v, vreg);
-    load_dense<DH>(rs, row_n, t, u, kd);
+    //      (their lane offsets are recomputed: a few VALU ops instead of two
+    //      registers held across the page)
+    {
+      int lane_v = lane;
+      asm volatile("" : "+v"(lane_v));
+      const LaneOff lv = lane_offsets<DH>(lane_v);
+      load_v<DH>(a, lv, row_n, vreg);
+      if (row_looks_dense<DH>(row_n)) load_dense<DH>(rs, lv, row_n, kd);
+    }
     wave_lds_sync();
 
     row_c = row_n;
@@ -929,7 +963,11 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.out = reinterpret_cast<_Float16*>(L.out); a.partials = L.partials;
   a.status = reinterpret_cast<uint32_t*>(L.partials + (int64_t)L.num_items * partial_stride<DH, GQA>());
   a.num_kv = L.num_kv; a.num_rows = L.num_rows; a.num_sh = L.num_seqs * L.num_kv;
+  a.pages32 = (int32_t)L.pages_bytes;
+  a.pages_m8 = (int32_t)L.pages_bytes - 8;
+  a.nvp32 = L.num_vpages > 0x7FFFFFFF ? 0x7FFFFFFF : (int32_t)L.num_vpages;
   a.scale_log2 = L.sm_scale * 1.4426950408889634f;
+  a.scale_log2_c = a.scale_log2 * (1.0f / 127.0f);
   a.log2_theta = __builtin_log2(L.rope_theta);
   if (L.num_items > 0) {
     if (phases & kPhasePartials)
