@@ -119,7 +119,7 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
   LaneOff o;
   o.row = lane < 3 ? 4u * lane : (uint32_t)kOOB;            // pointer-table row: 3 dwords
   o.vs = lane == 3 ? 0u : (uint32_t)kOOB;                   // V slot
-  o.stg = lane < 32 ? 16u * lane : (uint32_t)kOOB;          // 512-byte staging window
+  o.stg = 8u * lane;                                        // 512-byte staging window
   o.pos = 4u * t;                                           // position of token t
   o.kd = (uint32_t)(t * DH + chunk_dim<DH>(0, u)) * 2u;     // dense K: chunk 0 of (t, u)
   o.v = (uint32_t)lane * kTile * 2u;                        // V: dim `lane`, 16 tokens
@@ -170,11 +170,11 @@ __device__ __forceinline__ int row_looks_dense(const Row& r) {
 }
 
 // 512-byte staging window [page_off, +512) of a page (page_off is 4-byte
-// aligned): lanes < 32 hold 16 bytes each (bytes past the pool read as zero),
-// the other lanes zeros; the page header is lane 0's first dword.
-__device__ __forceinline__ uint4 load_stage(const Res& rs, const LaneOff& lo, const Row& r) {
-  const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.pages, (int)(oob_or(r.ok, (uint32_t)r.page_off) + lo.stg), 0, 0);
-  return uint4{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
+// aligned): 8 bytes per lane (bytes past the pool read as zero); the page
+// header is lane 0's first dword.
+__device__ __forceinline__ uint2 load_stage(const Res& rs, const LaneOff& lo, const Row& r) {
+  const auto w = __builtin_amdgcn_raw_buffer_load_b64(rs.pages, (int)(oob_or(r.ok, (uint32_t)r.page_off) + lo.stg), 0, 0);
+  return uint2{(uint32_t)w[0], (uint32_t)w[1]};
 }
 
 __device__ __forceinline__ int load_pos(const Res& rs, const LaneOff& lo, const Row& r, int p) {
@@ -231,11 +231,12 @@ __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 //    RoPE frequencies j, 4 x cos(2 pi f_j d) then 4 x sin(2 pi f_j d), fp32,
 //    rows padded by 16 bytes;
 //  * f_j in turns per token (fp64);
-//  * per wave: the staging area of its page (1 KB: the 512-byte window and the
-//    zeros of the lanes that load nothing), the query rows rotated to the page
-//    centre (fp32, in the QK MFMA's operand order; slots of heads >= GQA stay
-//    zero), and the page's softmax weights P as fp16 [max(GQA, 4)][16 tokens]
-//    (rows >= GQA stay zero), read back as the PV MFMA's A operand.
+//  * per wave: the staging area of its page (1 KB: the 512-byte window, and
+//    room for the reads of tokens past the page's count), the query rows
+//    rotated to the page centre (fp32, in the QK MFMA's operand order; slots
+//    of heads >= GQA stay zero), and the page's softmax weights P as fp16
+//    [max(GQA, 4)][16 tokens] (rows >= GQA stay zero), read back as the PV
+//    MFMA's A operand.
 template <int DH, int GQA>
 struct DecodeLds {
   static constexpr int kWaves = decode_waves<GQA>();
@@ -479,7 +480,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // so they are in by now); its V and dense K are issued after the barrier,
   // behind every wave's staging loads
   Row row_c = row_take(a, rl_c, p, re);
-  uint4 stg_c = load_stage(rs, lo, row_c);
+  uint2 stg_c = load_stage(rs, lo, row_c);
   int pos_c = load_pos(rs, lo, row_c, p);
   Row row_n = row_take(a, rl_n, p + wstride, re);
   if (threadIdx.x < NJ)
@@ -541,7 +542,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // table rows into the other slot of a pair, so the loop (unrolled by two)
   // never copies a register that a load is still filling: such a copy would
   // wait for that load.
-  auto step = [&](const int p, uint4& stg_c, int& pos_c, uint4& stg_n, int& pos_n, RowLd& rl_issue,
+  auto step = [&](const int p, uint2& stg_c, int& pos_c, uint2& stg_n, int& pos_n, RowLd& rl_issue,
                   RowLd& rl_take) __attribute__((always_inline)) {
     // ---- issue priority (changes at most three times per item) ----------
     if (pages_done == prio_next) {
@@ -619,7 +620,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     int cofs[2] = {0, 0};
     float rh[2] = {1.f, 1.f};                   // dense K enters unscaled
     if (comp) {
-      *reinterpret_cast<uint4*>(st + 16 * lane) = stg_c;
+      *reinterpret_cast<uint2*>(st + 8 * lane) = stg_c;
       wave_lds_sync();
       if (tid == 1) locate_k<DH, GQA, 1>(st, thr, rdr, t, u, cofs, rh);
       else if (tid == 2) locate_k<DH, GQA, 2>(st, thr, rdr, t, u, cofs, rh);
@@ -804,7 +805,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     row_n = row_take(a, rl_take, p + 2 * wstride, re);
     ++pages_done;
   };
-  uint4 stg_b;
+  uint2 stg_b;
   int pos_b;
   RowLd rl_3;
   for (; p < re; p += 2 * wstride) {
