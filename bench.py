@@ -83,13 +83,43 @@ def measured_traffic(config, layout):
     return None if v is None else int(v)
 
 
+def host_cpu() -> dict:
+    """The host CPU this process runs on: model name, logical CPUs of the
+    machine, CPUs in this process's affinity mask, the cgroup CPU quota (if
+    any), and `threads` = the CPUs the process can actually use (affinity,
+    capped by the quota)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+            if q != "max":
+                quota = int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(math.ceil(quota))))
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "affinity_cpus": affinity,
+            "cgroup_cpus": quota, "threads": threads}
+
+
 def cpu_baseline(wl, pool: ops.PagedPool, budget_s: float = 20.0):
-    """Reference Mode-B path restated in torch (oracle/torch_port.py), on the
-    host cores, over a bounded sample of the same workload: whole kv heads of
-    the config, as many as fit the time budget (at least one)."""
+    """Reference Mode-B path restated in torch (oracle/torch_port.py), on all
+    the host CPUs this process may use, over a bounded sample of the same
+    workload: whole kv heads of the config, as many as fit the time budget (at
+    least one)."""
     sys.path.insert(0, ROOT)
     from oracle import torch_port
-    threads = min(os.cpu_count() or 1, 16)
+    cpu = host_cpu()
+    threads = cpu["threads"]
     torch.set_num_threads(threads)
     pages = pool.pages.cpu().numpy()
     v_pool = pool.v_pool.cpu().numpy()
@@ -112,10 +142,53 @@ def cpu_baseline(wl, pool: ops.PagedPool, budget_s: float = 20.0):
     per_head = float(np.median(times))
     step_us = per_head * wl.plan.num_seqs * wl.plan.num_kv * 1e6
     return {"value": round(step_us, 1), "unit": "µs/decode step (extrapolated from per-head time)",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", **{k: v for k, v in cpu.items() if k != "threads"},
             "sample": f"{heads_done} of {wl.plan.num_seqs * wl.plan.num_kv} kv heads of {wl.name}, "
                       f"median per-head time x {wl.plan.num_seqs * wl.plan.num_kv} heads; torch CPU "
                       f"restatement of spherical_kv_pipeline.py:2143-2177,2348,2367"}
+
+
+def cpu_baseline_prefill(wl, budget_s: float = 20.0):
+    """Reference prefill paging restated in torch (oracle/torch_port.py) on all
+    the host CPUs this process may use: the reference grouping of the retained
+    tokens (oracle/paging.py, spherical_kv_pipeline.py:1156-1190), then per
+    16-token chunk the encode (:1136-1144) and page build (pagebuilder.py:8-33)
+    of _build_per_head_pages (:1187-1213); dense chunks are header + K bytes.
+    (seq, head)s are processed in order until the time budget is spent; the
+    layer time is extrapolated by retained tokens."""
+    sys.path.insert(0, ROOT)
+    from oracle import paging, torch_port
+    cpu = host_cpu()
+    torch.set_num_threads(cpu["threads"])
+    groups = paging.group_pages(paging.retained_tokens(wl.tier_of, wl.num_seqs, wl.num_kv))
+    cbs = {t: torch.from_numpy(np.ascontiguousarray(c, np.float32)) for t, c in wl.codebooks.items()}
+    total = sum(len(c) for tiers in groups.values() for _, chunks in tiers for c in chunks)
+    done, elapsed, heads = 0, 0.0, 0
+    for (s, h), tiers in groups.items():
+        K, V = wl.head_kv(s, h)
+        Kt = torch.from_numpy(K.astype(np.float32))
+        t0 = time.perf_counter()
+        for tier, chunks in tiers:
+            for chunk in chunks:
+                ix = torch.as_tensor(chunk, dtype=torch.long)
+                if tier == fmt.DENSE_TIER_ID:
+                    torch.cat([torch.zeros(8, dtype=torch.uint8), Kt[ix].half().reshape(-1).view(torch.uint8)])
+                else:
+                    g, b = paging.TIER_GEOMETRY[tier]
+                    r, codes = torch_port.encode_chunk(Kt[ix], cbs[tier][h], g, wl.dh // g)
+                    torch_port.build_page(r, codes, tier, b)
+                _ = V[chunk]                                             # the chunk's V rows
+                done += len(chunk)
+        elapsed += time.perf_counter() - t0
+        heads += 1
+        if elapsed > budget_s:
+            break
+    layer_us = elapsed / max(done, 1) * total * 1e6
+    return {"value": round(layer_us, 1), "unit": "µs/layer (extrapolated by retained tokens)",
+            "cores": cpu["threads"], "kind": "port", **{k: v for k, v in cpu.items() if k != "threads"},
+            "sample": f"{heads} of {len(groups)} (seq, kv head)s, {done} of {total} retained tokens of {wl.name}; "
+                      f"torch CPU restatement of spherical_kv_pipeline.py:1136-1144,1156-1213 + "
+                      f"pagebuilder.py:8-33 + bitpacking.py:5-29"}
 
 
 def modea_bytes(w) -> int:
@@ -152,8 +225,9 @@ def cpu_baseline_modea(w, budget_s: float = 20.0):
         if time.perf_counter() - t_start > budget_s:
             break
     step_us = float(np.median(times)) * w["num_kv"] * 1e6
+    cpu = host_cpu()
     return {"value": round(step_us, 1), "unit": "µs/decode step (extrapolated from per-head time)", "cores": 1,
-            "kind": "port", "sample": f"{done} of {w['num_kv']} kv heads, median per-head time x {w['num_kv']}; "
+            "kind": "port", **{k: v for k, v in cpu.items() if k != "threads"}, "sample": f"{done} of {w['num_kv']} kv heads, median per-head time x {w['num_kv']}; "
                                       f"numpy fp64 restatement of decode_kernel.cu:108-246"}
 
 
@@ -267,15 +341,9 @@ def bench_prefill(args, dev):
         f"encode_pages_kernel alone {enc_us:.1f} us")
     cpu = None
     if not args.no_cpu_baseline:
-        sys.path.insert(0, ROOT)
-        import oracle
-        c0 = time.perf_counter()
-        plan = fmt.plan_pages(wl.tier_of, None, wl.num_seqs, wl.num_kv, wl.dh, 16)
-        oracle.build_pool(synth.Workload(**{**wl.__dict__, "plan": plan}))
-        cpu_us = (time.perf_counter() - c0) * 1e6
-        cpu = {"value": round(cpu_us, 1), "unit": "µs/layer", "cores": 1, "kind": "port",
-               "sample": f"the whole layer ({kept} kept of {n_tok} token-heads): sphkv_format.plan_pages + "
-                         f"oracle C encode / page build (spherical_kv_pipeline.py:1130-1228, pagebuilder.py:8-33)"}
+        log("[bench] CPU baseline (torch restatement of the reference prefill paging)")
+        cpu = cpu_baseline_prefill(wl)
+        log(f"[bench] CPU {cpu['value']} us/layer on {cpu['cores']} threads")
     line = {
         "metric": "µs per prefill paging of one layer (plan + encode + bitpack + V placement), 1 GPU",
         "value": round(ms * 1e3, 3), "unit": "µs/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -389,7 +457,8 @@ def main():
     line = {
         "metric": METRIC, "value": round(us, 3), "unit": "µs/decode step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16 I/O, fp32 math",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 I/O; fp32 rotation, QK and softmax; P rounded to fp16 for the fp32-accumulated PV",
         "data": "synthetic (seeded generator, config spec of BASELINE.json)",
         "achieved_hbm_gbps": round(gbps, 1),
         "config": {"workload": f"config{args.config}: {wl.num_q} q / {wl.num_kv} kv heads, dh {wl.dh}, "

@@ -1,5 +1,14 @@
-"""Op-for-op torch restatement of the reference's Mode-B decode, for the CPU
-baseline of bench.py.  TEST / MEASUREMENT INFRASTRUCTURE (never shipped).
+"""Op-for-op torch restatements of the reference's Mode-B decode and of its
+prefill encode / page build, for the CPU baselines of bench.py.  TEST /
+MEASUREMENT INFRASTRUCTURE (never shipped).
+
+Encode (encode_chunk, build_page, pack_bits): spherical_kv_pipeline.py:1136-1144
+(view, norm, divide by r + EPS, einsum with the codebook, argmax),
+pagebuilder.py:17-33 (r_scale, int8 radii, header, concatenation) and
+bitpacking.py:5-29 (LSB-first scatter_add packing), called per page chunk as
+_build_per_head_pages does (spherical_kv_pipeline.py:1187-1213).
+
+Decode:
 
 Follows spherical_kv_pipeline.py:2100-2179 per (kv head, tier block):
 back-rotate q per token with cos/sin tables (:2143-2151, _rotate_half
@@ -18,6 +27,48 @@ import numpy as np
 import torch
 
 import oracle
+
+
+EPS = 1e-8                       # spherical_kv_pipeline.py EPS
+HEADER_BYTES = 8                 # config.py:3
+
+
+def encode_chunk(K_chunk: torch.Tensor, codebooks: torch.Tensor, g: int, G: int):
+    """K_chunk fp32 [N, dh], codebooks [G, C, g] -> (r [N, G], codes int32 [N, G])."""
+    N = K_chunk.shape[0]
+    K_grouped = K_chunk.view(N, G, g)
+    r_groups = K_grouped.norm(dim=-1)
+    K_dir = K_grouped / (r_groups.unsqueeze(-1) + EPS)
+    sims = torch.einsum('ngi,gci->ngc', K_dir, codebooks)
+    return r_groups, sims.argmax(dim=-1).to(torch.int32)
+
+
+def pack_bits(values: torch.Tensor, bits: int) -> torch.Tensor:
+    """values int32 [n] -> uint8 [ceil(n*bits/8)], value i's bit k at global bit i*bits + k."""
+    n = values.numel()
+    out = torch.zeros((n * bits + 7) // 8, dtype=torch.uint8)
+    bit_idx = torch.arange(bits)
+    bit_matrix = ((values.unsqueeze(1) >> bit_idx) & 1).bool()
+    global_bits = torch.arange(n).unsqueeze(1) * bits + bit_idx
+    byte_idx = (global_bits >> 3).long().reshape(-1)
+    bit_shift = (global_bits & 7).long().reshape(-1)
+    contrib = bit_matrix.reshape(-1).to(torch.uint8) << bit_shift.to(torch.uint8)
+    out.scatter_add_(0, byte_idx, contrib)
+    return out
+
+
+def build_page(r: torch.Tensor, codes: torch.Tensor, tier_id: int, b_theta: int) -> torch.Tensor:
+    """One page's bytes: header (tier id, N, pad, fp32 r_scale[G]), packed codes, int8 radii."""
+    N, G = r.shape
+    r_scale = r.abs().max(dim=0).values
+    safe = r_scale.clamp(min=1e-8).unsqueeze(0)
+    rc = (r / safe * 127).round().clamp(-127, 127).to(torch.int8)
+    packed = pack_bits(codes.flatten().to(torch.int32), b_theta)
+    hdr = torch.zeros(HEADER_BYTES + 4 * G, dtype=torch.uint8)
+    hdr[0] = tier_id & 0xFF
+    hdr[1] = N & 0xFF
+    hdr[HEADER_BYTES:] = r_scale.to(torch.float32).view(torch.uint8)
+    return torch.cat([hdr, packed, rc.flatten().view(torch.uint8)])
 
 
 def _rotate_half(x):

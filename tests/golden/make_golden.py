@@ -30,43 +30,23 @@ import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-EPS = 1e-8
-HEADER_BYTES = 8
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+from oracle import torch_port  # noqa: E402  (the torch restatements of the reference's ops)
+
+EPS = torch_port.EPS
+HEADER_BYTES = torch_port.HEADER_BYTES
 
 
 def t_encode(K: torch.Tensor, cb: torch.Tensor, g: int, G: int):
-    N = K.shape[0]
-    Kg = K.view(N, G, g)
-    r = Kg.norm(dim=-1)
-    Kd = Kg / (r.unsqueeze(-1) + EPS)
-    sims = torch.einsum('ngi,gci->ngc', Kd, cb)
-    return r, sims.argmax(dim=-1).to(torch.int32)
+    return torch_port.encode_chunk(K, cb, g, G)
 
 
 def t_pack_bits(values: torch.Tensor, bits: int) -> torch.Tensor:
-    n = values.numel()
-    out = torch.zeros((n * bits + 7) // 8, dtype=torch.uint8)
-    bit_idx = torch.arange(bits)
-    bit_matrix = ((values.unsqueeze(1) >> bit_idx) & 1).bool()
-    global_bits = torch.arange(n).unsqueeze(1) * bits + bit_idx
-    byte_idx = (global_bits >> 3).long().reshape(-1)
-    bit_shift = (global_bits & 7).long().reshape(-1)
-    contrib = bit_matrix.reshape(-1).to(torch.uint8) << bit_shift.to(torch.uint8)
-    out.scatter_add_(0, byte_idx, contrib)
-    return out
+    return torch_port.pack_bits(values, bits)
 
 
 def t_build_page(r: torch.Tensor, codes: torch.Tensor, tier_id: int, b_theta: int) -> torch.Tensor:
-    N, G = r.shape
-    r_scale = r.abs().max(dim=0).values
-    safe = r_scale.clamp(min=1e-8).unsqueeze(0)
-    rc = (r / safe * 127).round().clamp(-127, 127).to(torch.int8)
-    packed = t_pack_bits(codes.flatten().to(torch.int32), b_theta)
-    hdr = torch.zeros(HEADER_BYTES + 4 * G, dtype=torch.uint8)
-    hdr[0] = tier_id & 0xFF
-    hdr[1] = N & 0xFF
-    hdr[HEADER_BYTES:] = r_scale.to(torch.float32).view(torch.uint8)
-    return torch.cat([hdr, packed, rc.flatten().view(torch.uint8)])
+    return torch_port.build_page(r, codes, tier_id, b_theta)
 
 
 def margins(K: np.ndarray, cb: np.ndarray, g: int, G: int) -> np.ndarray:

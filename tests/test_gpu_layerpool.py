@@ -103,5 +103,5 @@ def test_layer_pool_build_and_steps(gpu, page_size):
     assert (pool.theta_codes.cpu().numpy() == th).all() and (pool.radius_codes.cpu().numpy() == rd).all()
     assert (pool.r_scales.cpu().numpy().view(np.uint32) == rs.view(np.uint32)).all()
     assert (pool.v_pool.cpu().numpy().view(np.uint16) == vp.view(np.uint16)).all()
-    assert (pool.block_table_gpu.cpu().numpy() == bt).all() and pool.block_table_cpu == bt.tolist()
+    assert (pool.block_table_gpu.cpu().numpy() == bt).all() and np.array_equal(pool.block_table_cpu, bt)
     assert (pool.ctx_lens_gpu.cpu().numpy() == want["ctx_lens"] + page_size + 24).all()
