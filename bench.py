@@ -77,6 +77,15 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
 TRAFFIC_BYTES = {(2, "default"): 85592537}
 
+# encode_pages_kernel at config 3, from rocprofv3 --pmc on MI355X
+# (profiles/encode_config3_counters.txt): VALU instructions per launch (MFMA
+# included) and HBM bytes (FETCH_SIZE * 2 + WRITE_SIZE).  The VALU-issue bound
+# is that count at one wave64 VALU instruction per 4 cycles on each of the
+# 1024 SIMDs at 2.4 GHz.
+ENCODE_VALU_INSTS = {3: 8653627}
+ENCODE_TRAFFIC_BYTES = {3: 55618560}
+SIMDS, CLOCK_HZ = 1024, 2.4e9
+
 
 def measured_traffic(config, layout):
     v = TRAFFIC_BYTES.get((config, layout))
@@ -352,9 +361,14 @@ def bench_prefill(args, dev):
         "config": {"workload": f"config{args.config}: {wl.num_kv} kv heads, dh {wl.dh}, {wl.num_seqs} seq x "
                                f"{L_max} tokens, tier mix of BASELINE", "rows": dp.rows,
                    "algorithmic_bytes_per_step": int(nbytes)},
-        "roofline": {"bound": "valu (argmax) / hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "encode_pages_kernel", "kernel_us": round(enc_us, 3)},
+        "roofline": {"bound": "valu", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": ENCODE_TRAFFIC_BYTES.get(args.config),
+                     "kernel": "encode_pages_kernel", "kernel_us": round(enc_us, 3),
+                     "hbm_bound_us": round(nbytes / (PEAK_HBM_GBPS * 1e9) * 1e6, 2),
+                     **({} if args.config not in ENCODE_VALU_INSTS else {
+                         "valu_bound_us": round(ENCODE_VALU_INSTS[args.config] * 4 / SIMDS / CLOCK_HZ * 1e6, 2),
+                         "valu_frac": round(ENCODE_VALU_INSTS[args.config] * 4 / SIMDS / CLOCK_HZ * 1e6 / enc_us, 4)})},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
