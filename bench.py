@@ -345,9 +345,20 @@ def bench_prefill(args, dev):
         step(time_encode=True)
     torch.cuda.synchronize()
     enc_us = float(np.median([a.elapsed_time(b) for a, b in enc_ms])) * 1e3
+    # the all-tier re-encode of every token (_codes_all, spherical_kv_pipeline.py:1536-1553),
+    # which the reference's prefill runs after the page build; timed on its own
+    ca_ms = []
+    for _ in range(max(args.steps // 4, 5)):
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        ops.encode_codes_all(k, wl.row_base(), wl.lengths, wl.num_kv, cbs)
+        c1.record()
+        ca_ms.append((c0, c1))
+    torch.cuda.synchronize()
+    codes_all_us = float(np.median([a.elapsed_time(b) for a, b in ca_ms])) * 1e3
     gbps = nbytes / (enc_us * 1e-6) / 1e9
     log(f"[bench] prefill paging {ms * 1e3:.1f} us/layer ({wall_ms * 1e3:.1f} us host wall), rows {dp.rows}; "
-        f"encode_pages_kernel alone {enc_us:.1f} us")
+        f"encode_pages_kernel alone {enc_us:.1f} us; all-tier re-encode (_codes_all) {codes_all_us:.1f} us")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (torch restatement of the reference prefill paging)")
@@ -360,7 +371,8 @@ def bench_prefill(args, dev):
         "dtype": "fp16 in, u8 pages", "data": "synthetic (seeded generator, config spec of BASELINE.json)",
         "config": {"workload": f"config{args.config}: {wl.num_kv} kv heads, dh {wl.dh}, {wl.num_seqs} seq x "
                                f"{L_max} tokens, tier mix of BASELINE", "rows": dp.rows,
-                   "algorithmic_bytes_per_step": int(nbytes)},
+                   "algorithmic_bytes_per_step": int(nbytes),
+                   "codes_all_us": round(codes_all_us, 1)},
         "roofline": {"bound": "valu", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
                      "traffic": ENCODE_TRAFFIC_BYTES.get(args.config),

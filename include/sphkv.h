@@ -81,6 +81,24 @@ int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int6
                        float* r_out, int32_t* code_out, int32_t dh, int32_t page_size, void* stream);
 
 /*
+ * Radii and codes only, for every token of every tier: the all-tier
+ * re-encode kept for the online refresh (_codes_all,
+ * spherical_kv_pipeline.py:1536-1553), which encodes each (layer, head)'s T
+ * tokens at each tier in one _encode_keys_with_codebooks call (:1130-1144).
+ * The tokens are given as pages of sphkv_encode_pages (src_rows, tier,
+ * count, seq_head; no pointer table, byte pool or V), and order_n[p] is the
+ * N of the torch call whose summation order the page's codes follow (its
+ * head's T; NULL: the page's count).  r_out fp32 / code_out int32
+ * [num_pages, page_size, dh/16] get each (token, group) of the compressed
+ * pages (groups past the tier's G untouched); codes are bit-exact with torch
+ * CPU's call over order_n tokens.
+ */
+int sphkv_encode_codes(const void* k, int32_t k_is_fp32, int64_t num_src_rows, const int64_t* src_rows,
+                       const int32_t* tier, const int32_t* count, const int32_t* order_n, const int32_t* seq_head,
+                       int32_t num_pages, int32_t num_kv, const float* cb1, const float* cb2, const float* cb3,
+                       float* r_out, int32_t* code_out, int32_t dh, int32_t page_size, void* stream);
+
+/*
  * Workspace bytes sphkv_decode_paged needs for num_items work items: one
  * (m, l, acc) partial per item, then 16 status bytes (uint32 [0]: malformed
  * rows / pages counted since the last merge, [1]: the count of the last

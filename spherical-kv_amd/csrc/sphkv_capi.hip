@@ -65,8 +65,24 @@ int sphkv_encode_pages(const void* k, int32_t k_is_fp32, const uint16_t* v, int6
     return fail(SPHKV_EINVAL, "sphkv_encode_pages: null pointer argument");
   sphkv::EncodeLaunch L{k, k_is_fp32, v, num_src_rows, src_rows, tier, count, ptable, vslot, seq_head,
                         num_pages, num_kv, cb1, cb2, cb3, pages, pages_bytes, v_pool, num_vpages,
-                        r_out, code_out, dh};
+                        r_out, code_out, dh, nullptr, 0};
   return launch_status(sphkv::launch_encode(L, (hipStream_t)stream), "sphkv_encode_pages");
+}
+
+int sphkv_encode_codes(const void* k, int32_t k_is_fp32, int64_t num_src_rows, const int64_t* src_rows,
+                       const int32_t* tier, const int32_t* count, const int32_t* order_n, const int32_t* seq_head,
+                       int32_t num_pages, int32_t num_kv, const float* cb1, const float* cb2, const float* cb3,
+                       float* r_out, int32_t* code_out, int32_t dh, int32_t page_size, void* stream) {
+  const char* fn = "sphkv_encode_codes";
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
+  if (num_pages < 0 || num_kv <= 0 || num_src_rows < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (num_pages == 0) return ok();
+  if (!k || !src_rows || !tier || !count || !seq_head || !r_out || !code_out)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::EncodeLaunch L{k, k_is_fp32, nullptr, num_src_rows, src_rows, tier, count, nullptr, nullptr, seq_head,
+                        num_pages, num_kv, cb1, cb2, cb3, nullptr, 0, nullptr, 0, r_out, code_out, dh, order_n, 1};
+  return launch_status(sphkv::launch_encode(L, (hipStream_t)stream), fn);
 }
 
 int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32_t dh) {

@@ -44,6 +44,8 @@ struct EncodeArgs {
   int64_t num_vpages;
   float* r_out;
   int32_t* code_out;
+  const int32_t* order_n;   // per page: N of the torch call whose summation order applies (NULL: count)
+  int32_t codes_only;       // 1: write r_out / code_out only (no pages, no V)
 };
 
 template <int DH>
@@ -229,6 +231,9 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     const int64_t row_raw = p_ok ? a.src_rows[(int64_t)p * kTile + t] : -1;
     const int tid_l = p_ok ? a.tier[p] : 0;
     const int n_l = p_ok ? min(max(a.count[p], 0), kTile) : 0;
+    // the summation order follows torch's call over ord_l tokens: the page's
+    // own count, or the caller's N (a whole head's tokens in one call)
+    const int ord_l = p_ok ? (a.order_n ? max(a.order_n[p], 1) : n_l) : 0;
     const int sh_l = p_ok ? a.seq_head[p] : -1;
     const int head_l = sh_l >= 0 ? sh_l % a.num_kv : 0;
     int64_t row = t < n_l ? row_raw : -1;
@@ -351,8 +356,8 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
         uint64_t mk = (uint64_t)lo | ((uint64_t)hi << 32);
         if (C < 64) mk &= (1ull << C) - 1;
         if (mk == 0) mk = C == 64 ? ~0ull : ((1ull << C) - 1);      // NaN similarities: score every code
-        const bool naive = n_l * 16 * C < 400;                       // torch's own small-bmm loop
-        const bool m1 = !naive && n_l == 1;                          // MKL's M = 1 kernel
+        const bool naive = ord_l * 16 * C < 400;                     // torch's own small-bmm loop
+        const bool m1 = !naive && ord_l == 1;                        // MKL's M = 1 kernel
         float best_sim = 0.f;
         int best = -1;
         while (mk) {
@@ -433,7 +438,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
       const cb_ptr cbg = (cb_ptr)(((uint64_t)(uint32_t)uniform((int)(cba >> 32)) << 32) |
                                   (uint32_t)uniform((int)(uint32_t)cba));
       if (mine) {
-        const bool naive = n_l * g * C < 400;                     // torch's own small-bmm loop
+        const bool naive = ord_l * g * C < 400;                   // torch's own small-bmm loop
         float r = 0.f;
         int code = 0;
         if (row >= 0) {
@@ -446,6 +451,22 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     }
   }
   __syncthreads();
+
+  if (a.codes_only) {
+    // radii and codes of every (token, group) of the workgroup's compressed
+    // pages, [page][slot][DH / 16]
+    const int j = threadIdx.x >> 4 & 3, t = threadIdx.x & 15, gbase = threadIdx.x >> 6;
+    const int p = p0 + j;
+    if (p >= a.num_pages) return;
+    const int tid = a.tier[p];
+    if (tid < 1 || tid > 3 || t >= min(max(a.count[p], 0), kTile)) return;
+    for (int gi = gbase; gi < DH / tier_g(tid); gi += kEncWaves) {
+      const int64_t o = ((int64_t)p * kTile + t) * (DH / 16) + gi;
+      if (a.r_out) a.r_out[o] = sm.r[16 * j + t][gi];
+      if (a.code_out) a.code_out[o] = sm.code[16 * j + t][gi];
+    }
+    return;
+  }
 
   const int j = wave & 3;
   const int p = p0 + j;
@@ -580,6 +601,7 @@ int launch_encode(const EncodeLaunch& L, hipStream_t stream) {
   a.num_kv = L.num_kv; a.cb[0] = nullptr; a.cb[1] = L.cb1; a.cb[2] = L.cb2; a.cb[3] = L.cb3;
   a.pages = L.pages; a.pages_bytes = L.pages_bytes; a.v_pool = reinterpret_cast<__half*>(L.v_pool);
   a.num_vpages = L.num_vpages; a.r_out = L.r_out; a.code_out = L.code_out;
+  a.order_n = L.order_n; a.codes_only = L.codes_only;
   const dim3 grid((L.num_pages + kEncPages - 1) / kEncPages), block(kEncWaves * 64);
   if (L.dh == 128) hipLaunchKernelGGL(encode_pages_kernel<128>, grid, block, 0, stream, a);
   else hipLaunchKernelGGL(encode_pages_kernel<64>, grid, block, 0, stream, a);

@@ -15,6 +15,8 @@ struct EncodeLaunch {
   const float* cb1; const float* cb2; const float* cb3;
   uint8_t* pages; int64_t pages_bytes; uint16_t* v_pool; int64_t num_vpages;
   float* r_out; int32_t* code_out; int32_t dh;
+  const int32_t* order_n;   // per page: N of the torch call whose summation order applies (NULL: count)
+  int32_t codes_only;       // 1: write r_out / code_out only (no pages, no V)
 };
 
 struct DecodeLaunch {

@@ -26,6 +26,7 @@ SIGNATURES = {
     "sphkv_version": (ctypes.c_char_p, []),
     "sphkv_encode_pages": (ctypes.c_int, [P, I32, P, I64, P, P, P, P, P, P, I32, I32, P, P, P,
                                           P, I64, P, I64, P, P, I32, I32, P]),
+    "sphkv_encode_codes": (ctypes.c_int, [P, I32, I64, P, P, P, P, P, I32, I32, P, P, P, P, P, I32, I32, P]),
     "sphkv_decode_paged_workspace_bytes": (I64, [I32, I32, I32]),
     "sphkv_decode_paged": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P,
                                           I32, I32, I32, P, P, P, I64, I32, I32, F32, F64, P]),

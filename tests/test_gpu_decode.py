@@ -222,6 +222,58 @@ def test_ragged_logits_matches_oracle(gpu):
         assert max_err(got[fin], want[fin]) < 2e-4
 
 
+@pytest.mark.parametrize("tid,page_size,dh", [(1, 128, 128), (3, 128, 128), (3, 16, 128), (2, 128, 64)])
+def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh):
+    # the reference's call shape: PAGE_SIZE = 128 pages (config.py:4,
+    # spherical_kv_pipeline.py:1109-1125) and tier-3 decode pages (:1900-1910);
+    # pages laid out back to back as _build_per_head_pages does (:1198-1213)
+    import fused_decode
+    from oracle import paging
+    rng = np.random.default_rng(700 + tid + page_size + dh)
+    num_kv, grp, L = 2, 4, 300
+    g, b = fmt.TIER_GEOMETRY[tid]
+    G = dh // g
+    cbs = synth.make_codebooks(rng, num_kv, dh, [tid])[tid]
+    buf, ptab, heads, pos = [], [], [], []
+    base = 0
+    for h in range(num_kv):
+        K = (rng.standard_normal((L, dh)) * np.exp(rng.normal(0, 0.5, dh))).astype(np.float16)
+        idx = np.sort(rng.choice(4000, size=L, replace=False))
+        counts = [min(page_size, L - s) for s in range(0, L, page_size)]
+        rows = paging.page_offsets(tid, counts, dh).astype(np.int64) + base
+        for ci, s0 in enumerate(range(0, L, page_size)):
+            n = counts[ci]
+            r, codes = oracle.encode_groups(K[s0:s0 + n].astype(np.float32), cbs[h])
+            buf.append(oracle.build_page(r, codes, tid, b))
+            pp = np.full(page_size, -1, np.int32)
+            pp[:n] = idx[s0:s0 + n]
+            if ci == 0:
+                pp[3] = -1                                   # a masked token inside the page
+            pos.append(pp)
+            heads.append(h)
+        ptab.append(rows)
+        base += sum(x.size for x in buf[len(buf) - len(counts):])
+    pages = np.concatenate(buf)
+    ptable = np.concatenate(ptab).astype(np.int32)
+    heads = np.asarray(heads, np.int32)
+    pos = np.concatenate(pos).astype(np.int32)
+    cos_t, sin_t = fmt.rope_tables(4100, dh, 500000.0)
+    q = rng.standard_normal((num_kv * grp, dh)).astype(np.float32)
+    cb = cbs.reshape(num_kv * G, 2 ** b, g)
+    log(f"ragged tier {tid}, page_size {page_size}, dh {dh}: {ptable.shape[0]} pages")
+    got = fused_decode.fused_decode_ragged(
+        torch.as_tensor(pages, device=gpu), torch.as_tensor(ptable, device=gpu), torch.as_tensor(heads, device=gpu),
+        torch.as_tensor(pos, device=gpu), torch.as_tensor(cos_t, device=gpu), torch.as_tensor(sin_t, device=gpu),
+        torch.as_tensor(q, device=gpu), grp, num_kv, torch.as_tensor(cb, device=gpu), dh, G, g, b, page_size)
+    torch.cuda.synchronize()
+    want = oracle.ragged_logits(pages, ptable, heads, pos, cos_t, sin_t, q, grp, cb, dh, G, g, b, page_size)
+    got = got.cpu().numpy()
+    fin = np.isfinite(want)
+    assert fin.sum() == num_kv * (L - 1) * grp                  # every token but the masked ones
+    assert (np.isneginf(got) == ~fin).all()
+    assert max_err(got[fin], want[fin]) < 2e-4
+
+
 def test_decode_split_phases_equal_fused_call(gpu):
     # partials + merge as two calls give exactly the one-call result, and the
     # partials merge (fp64, on the host) to the same output
