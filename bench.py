@@ -44,6 +44,15 @@ import sphkv_synth as synth  # noqa: E402
 
 PEAK_HBM_GBPS = 8000.0
 METRIC = "µs/decode step + achieved HBM GB/s (compressed KV), 8B shape, 32K ctx, 1 GPU"
+# the same measurement on the other decode configs of BASELINE.json (parity
+# cases there; bench lines here with their own workload named)
+METRICS = {
+    1: "µs/decode step + achieved HBM GB/s (compressed KV), 1B shape (32 q / 8 kv, dh 64), 4K ctx, all tier 1, 1 GPU",
+    2: METRIC,
+    4: "µs/decode step + achieved HBM GB/s (compressed KV), 8B shape, 64 seqs x U[2K, 32K] ctx on a ~1.2M-page "
+       "shared pool, 1 GPU",
+    5: "µs/decode step + achieved HBM GB/s (compressed KV), 70B shape (64 q / 8 kv), 4 seqs x 131K ctx, 1 GPU",
+}
 ROTATE = 6
 COPY_BYTES = 256 << 20
 SETTLE_S = 0.3
@@ -75,7 +84,7 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
 # with `bench.py --calibrate` under rocprofv3 --pmc (summary and commands in
 # profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
-TRAFFIC_BYTES = {(2, "default"): 85592537}
+TRAFFIC_BYTES = {(2, "default"): 85718733}
 
 # encode_pages_kernel at config 3, from rocprofv3 --pmc on MI355X
 # (profiles/encode_config3_counters.txt): VALU instructions per launch (MFMA
@@ -481,7 +490,7 @@ def main():
         log(f"[bench] CPU {cpu['value']} us/step on {cpu['cores']} threads")
 
     line = {
-        "metric": METRIC, "value": round(us, 3), "unit": "µs/decode step", "n_gpus": 1,
+        "metric": METRICS[args.config], "value": round(us, 3), "unit": "µs/decode step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16 I/O; fp32 rotation, QK and softmax; P rounded to fp16 for the fp32-accumulated PV",
