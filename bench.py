@@ -435,7 +435,9 @@ def main():
         sys.exit(2)
 
     log(f"[bench] building config{args.config} workload")
-    wl = synth.make_decode_workload(args.config, layout=args.layout)
+    # configs 4 and 5 draw their K / V on the device (gigabytes of rows)
+    wl = synth.make_decode_workload(args.config, layout=args.layout,
+                                    kv_device=dev if args.config in (4, 5) else None)
     pool0, _, _ = ops.build_pool_gpu(wl, dev)
     pools = [pool0] + [clone_pool(pool0) for _ in range(args.rotate - 1)]
     torch.cuda.synchronize()
