@@ -8,14 +8,16 @@
 // each wave walks every kWaves-th page of the range with its own online-softmax
 // state; the states are merged in LDS and written as one (m, l, acc) partial.
 // A second, widely parallel kernel merges the partials of each (sequence, kv
-// head) (log-sum-exp) and writes the fp16 output.  (Merging in the
-// last-arriving workgroup needs an agent-scope release fence per workgroup,
-// which writes back the XCD's L2 and measured tens of microseconds on MI355X.)
+// head) (log-sum-exp) and writes the fp16 output.  (Merging in the workgroup
+// that completes a head needs device-scope stores, loads and counters, whose
+// cost on MI355X exceeds the kernel boundary.)
 //
 // Page loop, software pipelined per wave: while page p is computed, the
 // 512-byte staging window and positions of the wave's next page, its V and
 // (dense pages) its K rows, and the pointer-table row of the one after are in
-// flight.
+// flight.  The scalar work per page (validation of the row and the header,
+// page centre, issue priority) is kept to integer arithmetic on scalar
+// registers, and every lane's load offsets are fixed for the whole item.
 //
 // Per page (16 tokens, positions pos_t), lane l = (token t = l % 16, quarter
 // u = l / 16), page centre t_mid = (min pos + max pos) / 2:
@@ -24,20 +26,19 @@
 //   2. k_hat of token t on this lane's 32 dimensions (chunk_dim):
 //      compressed  k_hat_d = r_hat_g * centroid_g[code][d mod g],
 //                  r_hat_g = int8 / 127 * scale_g         (pagebuilder.py:17-21)
+//                  (the 1/127 goes into the page's logit scale)
 //      dense       k_hat_d = K[t][d] (fp16);
 //   3. k_rot = R(pos_t - t_mid) k_hat in fp32 with phasors from an LDS table
-//      of e^{i 2 pi f_j d}, |d| < kDelta (formed directly beyond).  Since
-//      <R(-pos) q, k_hat> = <R(-t_mid) q, R(pos - t_mid) k_hat>, this is the
-//      reference's back-rotated query (spherical_kv_pipeline.py:2143-2176;
-//      its clip of the cosine to [-1, 1] only acts on rounding error).  Phases
-//      are formed in fp64 turns and reduced to [0, 1) before the fp32 hardware
-//      sine / cosine;
+//      of e^{i 2 pi f_j d}, |d| < kDelta (a page with a token beyond forms all
+//      its phasors directly).  Since <R(-pos) q, k_hat> = <R(-t_mid) q,
+//      R(pos - t_mid) k_hat>, this is the reference's back-rotated query
+//      (spherical_kv_pipeline.py:2143-2176; its clip of the cosine to [-1, 1]
+//      only acts on rounding error).  Phases are formed in fp64 turns and
+//      reduced to [0, 1) before the fp32 hardware sine / cosine;
 //   4. S[t][h] = k_rot . q_rot_h on the fp32 MFMA (4x4x1, 16 blocks = 4 lane
-//      quarters x 4 token groups, one dimension per instruction), then the
-//      quarters' partial sums are added with row swaps: fp32 products and
-//      sums, no operand splitting.  GQA > 4 uses the fp16 16x16x32 MFMA
-//      instead (its 16 output columns hold all heads), both operands split
-//      hi + lo fp16 (hi*hi + lo*hi + hi*lo, about fp32 accuracy);
+//      quarters x 4 token groups, one dimension per instruction; GQA 8 runs
+//      two head sets), then the quarters' partial sums are added with row
+//      swaps: fp32 products and sums, no operand splitting;
 //   5. online softmax in the log2 domain.  The running reference max of a head
 //      only moves when a page's max exceeds it by more than 2^8, so the
 //      accumulator rescale is rare; p = 2^(s - m) <= 256 is rounded to fp16 and
