@@ -260,65 +260,89 @@ def encode_pages(pool: PagedPool, k: torch.Tensor, v: torch.Tensor, src_rows: to
     check(rc, "sphkv_encode_pages")
 
 
+class CodesAll:
+    """The all-tier re-encode of every token (_codes_all,
+    spherical_kv_pipeline.py:1536-1553) for one token layout, with the batch's
+    sequences in place of the reference's layers: built once per layout (the
+    page list of 16 consecutive tokens per (seq, head, tier) and the output
+    buffers on the device), then called per K (sphkv_encode_codes).  The
+    tokens of (seq s, head h) are K rows row_base[s*num_kv + h] + 0 .. L_s - 1;
+    `tiers` are the tier ids encoded (those with a codebook)."""
+
+    def __init__(self, row_base, lengths, num_kv: int, dh: int, tiers, device):
+        self.lengths = [int(x) for x in lengths]
+        self.num_kv, self.dh, self.tiers, self.device = num_kv, dh, list(tiers), device
+        base = np.asarray(row_base, np.int64)
+        num_sh = len(self.lengths) * num_kv
+        if base.shape != (num_sh,):
+            raise ValueError("row_base needs one entry per (seq, kv head)")
+        sh_len = np.repeat(np.asarray(self.lengths, np.int64), num_kv)
+        pages_per_sh = (sh_len + 15) // 16
+        self.P_t = P_t = int(pages_per_sh.sum())                 # pages per tier
+        sh_of_page = np.repeat(np.arange(num_sh), pages_per_sh)
+        self.first = np.cumsum(pages_per_sh) - pages_per_sh      # first page of each (seq, head)
+        tok0 = (np.arange(P_t) - self.first[sh_of_page]) * 16
+        count = np.minimum(sh_len[sh_of_page] - tok0, 16)
+        slot = np.arange(16)
+        src = np.where(slot[None, :] < count[:, None], base[sh_of_page][:, None] + tok0[:, None] + slot[None, :], -1)
+        nt = len(self.tiers)
+        self.P = P_t * nt
+
+        def dev(x, dt):
+            return torch.from_numpy(np.ascontiguousarray(np.concatenate([x] * nt), dtype=dt)).to(device)
+
+        self.src, self.count = dev(src, np.int64), dev(count, np.int32)
+        self.order_n, self.seq_head = dev(sh_len[sh_of_page], np.int32), dev(sh_of_page, np.int32)
+        self.tier = torch.from_numpy(np.repeat(np.asarray(self.tiers, np.int32), P_t)).to(device)
+        self.r = torch.empty((self.P, 16, dh // 16), dtype=torch.float32, device=device)
+        self.codes = torch.empty((self.P, 16, dh // 16), dtype=torch.int32, device=device)
+
+    def launch(self, k: torch.Tensor, codebooks: Dict[int, torch.Tensor]) -> None:
+        """Encode into the output buffers (asynchronous, current stream)."""
+        if k.dtype not in (torch.float16, torch.float32) or k.dim() != 2 or k.shape[1] != self.dh:
+            raise TypeError(f"k must be fp16 or fp32 [rows, {self.dh}]")
+        _need(k, k.dtype, "k", self.device)
+        cb = [codebooks.get(t) for t in (1, 2, 3)]
+        for t in self.tiers:
+            if cb[t - 1] is None:
+                raise ValueError(f"no codebook for tier {t}")
+        for t in cb:
+            if t is not None:
+                _need(t, torch.float32, "codebook", self.device)
+        if self.P:
+            rc = load().sphkv_encode_codes(
+                k.data_ptr(), 1 if k.dtype == torch.float32 else 0, k.shape[0], self.src.data_ptr(),
+                self.tier.data_ptr(), self.count.data_ptr(), self.order_n.data_ptr(), self.seq_head.data_ptr(),
+                self.P, self.num_kv, *[_ptr(t) for t in cb], self.r.data_ptr(), self.codes.data_ptr(), self.dh, 16,
+                _stream())
+            check(rc, "sphkv_encode_codes")
+
+    def result(self) -> Dict[Tuple[int, int], Dict[int, Tuple[torch.Tensor, torch.Tensor]]]:
+        """{(s, h): {tier: (r fp32 [L_s, G], codes int32 [L_s, G])}}: views of the
+        output buffers (valid until the next launch)."""
+        out: Dict[Tuple[int, int], Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = {}
+        for i, t in enumerate(self.tiers):
+            G = self.dh // (32 if t == 3 else 16)
+            r_t = self.r[i * self.P_t:(i + 1) * self.P_t, :, :G].reshape(-1, G)
+            c_t = self.codes[i * self.P_t:(i + 1) * self.P_t, :, :G].reshape(-1, G)
+            for sh in range(len(self.lengths) * self.num_kv):
+                s, h = divmod(sh, self.num_kv)
+                a0 = int(self.first[sh]) * 16
+                out.setdefault((s, h), {})[t] = (r_t[a0:a0 + self.lengths[s]], c_t[a0:a0 + self.lengths[s]])
+        return out
+
+
 def encode_codes_all(k: torch.Tensor, row_base, lengths, num_kv: int, codebooks: Dict[int, torch.Tensor]
                      ) -> Dict[Tuple[int, int], Dict[int, Tuple[torch.Tensor, torch.Tensor]]]:
     """Every token of every (sequence, kv head) encoded at every tier that has
-    a codebook: the reference's _codes_all (spherical_kv_pipeline.py:1536-1553),
-    with the batch's sequences in place of its layers, computed on the GPU
-    (sphkv_encode_codes).  k: [rows, dh] fp16 / fp32 on the device, the
-    tokens of (seq s, head h) at rows row_base[s*num_kv + h] + 0 .. L_s - 1;
-    codebooks[tier]: [num_kv, G, C, g] fp32 on the device.  Returns
-    {(s, h): {tier: (r fp32 [L_s, G], codes int32 [L_s, G])}} on the device,
-    bit-exact with one _encode_keys_with_codebooks call over the L_s tokens."""
-    dev = k.device
-    if k.dtype not in (torch.float16, torch.float32) or k.dim() != 2:
-        raise TypeError("k must be fp16 or fp32 [rows, dh]")
-    dh = k.shape[1]
-    lengths = [int(x) for x in lengths]
-    base = np.asarray(row_base, np.int64)
-    num_sh = len(lengths) * num_kv
-    if base.shape != (num_sh,):
-        raise ValueError("row_base needs one entry per (seq, kv head)")
-    tiers = [t for t in (1, 2, 3) if codebooks.get(t) is not None]
-    # pages of 16 consecutive tokens, tier by tier, (seq, head) by (seq, head)
-    sh_len = np.repeat(np.asarray(lengths, np.int64), num_kv)
-    pages_per_sh = (sh_len + 15) // 16
-    P_t = int(pages_per_sh.sum())
-    sh_of_page = np.repeat(np.arange(num_sh), pages_per_sh)
-    first = np.cumsum(pages_per_sh) - pages_per_sh
-    tok0 = (np.arange(P_t) - first[sh_of_page]) * 16
-    count = np.minimum(sh_len[sh_of_page] - tok0, 16)
-    slot = np.arange(16)
-    src = np.where(slot[None, :] < count[:, None], base[sh_of_page][:, None] + tok0[:, None] + slot[None, :], -1)
-    P = P_t * len(tiers)
-    tier_arr = np.repeat(np.asarray(tiers, np.int32), P_t)
-    out_r = torch.empty((P, 16, dh // 16), dtype=torch.float32, device=dev)
-    out_c = torch.empty((P, 16, dh // 16), dtype=torch.int32, device=dev)
-    if P:
-        d = lambda x, dt: torch.from_numpy(np.ascontiguousarray(np.tile(x, (len(tiers),) + (1,) * (x.ndim - 1)),
-                                                                 dtype=dt)).to(dev)
-        src_d, cnt_d = d(src, np.int64), d(count, np.int32)
-        ord_d, sh_d = d(sh_len[sh_of_page], np.int32), d(sh_of_page, np.int32)
-        tier_d = torch.from_numpy(tier_arr).to(dev)
-        cb = [codebooks.get(t) for t in (1, 2, 3)]
-        for t in cb:
-            if t is not None:
-                _need(t, torch.float32, "codebook", dev)
-        rc = load().sphkv_encode_codes(
-            k.data_ptr(), 1 if k.dtype == torch.float32 else 0, k.shape[0], src_d.data_ptr(), tier_d.data_ptr(),
-            cnt_d.data_ptr(), ord_d.data_ptr(), sh_d.data_ptr(), P, num_kv, *[_ptr(t) for t in cb],
-            out_r.data_ptr(), out_c.data_ptr(), dh, 16, _stream())
-        check(rc, "sphkv_encode_codes")
-    out: Dict[Tuple[int, int], Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = {}
-    for i, t in enumerate(tiers):
-        G = dh // (32 if t == 3 else 16)
-        r_t = out_r[i * P_t:(i + 1) * P_t, :, :G].reshape(-1, G)
-        c_t = out_c[i * P_t:(i + 1) * P_t, :, :G].reshape(-1, G)
-        for sh in range(num_sh):
-            s, h = divmod(sh, num_kv)
-            a0 = int(first[sh]) * 16
-            out.setdefault((s, h), {})[t] = (r_t[a0:a0 + lengths[s]], c_t[a0:a0 + lengths[s]])
-    return out
+    a codebook (see CodesAll): {(s, h): {tier: (r fp32 [L_s, G], codes int32
+    [L_s, G])}} on the device, bit-exact with one _encode_keys_with_codebooks
+    call (spherical_kv_pipeline.py:1130-1144) over the L_s tokens.
+    codebooks[tier]: [num_kv, G, C, g] fp32 on the device."""
+    ca = CodesAll(row_base, lengths, num_kv, k.shape[1], [t for t in (1, 2, 3) if codebooks.get(t) is not None],
+                  k.device)
+    ca.launch(k, codebooks)
+    return ca.result()
 
 
 def _decode_workspace(pool: PagedPool, gqa: int, workspace: Optional[torch.Tensor]) -> torch.Tensor:
