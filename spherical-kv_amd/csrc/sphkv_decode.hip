@@ -451,6 +451,31 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       qf[hh][1] = (float)qh[hh * DH + j + NJ];
     }
   }
+  // This lane's RoPE frequency f_j (j = lane mod NJ) in turns per token.  A
+  // workgroup has a multiple of NJ threads, so the delta-table entries
+  // (d, j) = i, i = threadIdx.x + k * kT, of a thread all have its own j: the
+  // table is built from registers while the first loads are in flight.
+  const double f_lane = exp2(-(2.0 * (lane % NJ) / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
+  static_assert((kWaves * 64) % NJ == 0, "delta-table rows need whole frequency runs per thread");
+  if (wave == 0 && lane < NJ) ftab[lane] = f_lane;       // the far pages' phasors read it
+  for (int i = threadIdx.x; i < kDelta * NJ; i += kT) {
+    const int d = i / NJ, j = i % NJ;
+    const float2 z = turn_phasor((double)d * f_lane);
+    float* row = reinterpret_cast<float*>(const_cast<uint8_t*>(dtab) + d * L::drow) + (j >> 2) * 8;
+    row[j & 3] = z.x;
+    row[4 + (j & 3)] = z.y;
+  }
+  // first page: its staging window, positions, V and dense K are issued as
+  // soon as its pointer-table row is in, so the page data streams in while
+  // the codebooks are stored
+  Row row_c = row_take(a, rl_c, p, re);
+  uint2 stg_c = load_stage(rs, lo, row_c);
+  int pos_c = load_pos(rs, lo, row_c, p);
+  half8 vreg[DH / 32];
+  uint4 kd[NC];
+  load_v<DH>(a, lo, row_c, vreg);
+  if (row_looks_dense<DH>(row_c)) load_dense<DH>(rs, lo, row_c, kd);
+  Row row_n = row_take(a, rl_n, p + wstride, re);
   if (GQA < 4) {
     // zero P rows GQA..3 and the query slots GQA..3 of this wave (never written)
     if (lane < (4 - GQA) * 2) {
@@ -477,32 +502,10 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       }
     }
   }
-  // first page's staging window and positions (the rows were issued first,
-  // so they are in by now); its V and dense K are issued after the barrier,
-  // behind every wave's staging loads
-  Row row_c = row_take(a, rl_c, p, re);
-  uint2 stg_c = load_stage(rs, lo, row_c);
-  int pos_c = load_pos(rs, lo, row_c, p);
-  Row row_n = row_take(a, rl_n, p + wstride, re);
-  if (threadIdx.x < NJ)
-    ftab[threadIdx.x] = exp2(-(2.0 * threadIdx.x / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
   __syncthreads();
-  for (int i = threadIdx.x; i < kDelta * NJ; i += kT) {
-    const int d = i / NJ, j = i % NJ;
-    const float2 z = turn_phasor((double)d * ftab[j]);
-    float* row = reinterpret_cast<float*>(const_cast<uint8_t*>(dtab) + d * L::drow) + (j >> 2) * 8;
-    row[j & 3] = z.x;
-    row[4 + (j & 3)] = z.y;
-  }
-  half8 vreg[DH / 32];
-  uint4 kd[NC];
-  __syncthreads();
-  load_v<DH>(a, lo, row_c, vreg);
-  if (row_looks_dense<DH>(row_c)) load_dense<DH>(rs, lo, row_c, kd);
 
-  // Loop-invariant lane data: this lane's RoPE frequency (query rotation),
-  // LDS addresses of its query writes / reads and P write / read.
-  const double f_lane = ftab[lane % NJ];
+  // Loop-invariant lane data: LDS addresses of this lane's query writes /
+  // reads and P write / read.
   float* qw;
   {
     const int j = lane % NJ, s = j % NPAIR;
