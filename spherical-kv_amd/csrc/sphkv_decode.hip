@@ -221,7 +221,7 @@ __device__ __forceinline__ void load_dense(const Res& rs, const LaneOff& lo, con
 // operands and accumulators.
 template <int GQA>
 __host__ __device__ constexpr int decode_waves() { return GQA <= 4 ? 12 : 8; }
-constexpr int kDelta = 64;             // delta-phasor table rows: |pos - page centre| < kDelta
+constexpr int kDelta = 96;             // delta-phasor table rows: |pos - page centre| < kDelta
 
 __host__ __device__ constexpr int align16(int x) { return (x + 15) & ~15; }
 

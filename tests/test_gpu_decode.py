@@ -132,15 +132,18 @@ def test_decode_edge_cases(gpu):
 
 @pytest.mark.parametrize("dh,gqa", [(128, 4), (64, 1), (128, 2), (128, 8)])
 def test_decode_partial_and_far_pages(gpu, dh, gqa):
-    # Every tier with a partial last page (250 tokens: 15 full pages + 10), and
-    # pages whose tokens lie 10 positions apart (page span > the phasor table,
-    # so the direct phasors run), full and partial.  Logits span several
-    # units, so a token's weight depends on its own logit.
+    # Every tier with a partial last page (250 tokens: 15 full pages + 10);
+    # pages whose tokens lie 10 positions apart (|pos - centre| up to 75: the
+    # far rows of the phasor table); and pages whose tokens lie 14 positions
+    # apart (page span > the phasor table, so the direct phasors run), full
+    # and partial.  Logits span several units, so a token's weight depends on
+    # its own logit.
     rng = np.random.default_rng(19)
     H = 2
     cases = [("dense", 250, lambda i: fmt.DENSE_TIER_ID), ("t1", 250, lambda i: 1), ("t2", 250, lambda i: 2),
-             ("t3", 250, lambda i: 3), ("far", 1600, lambda i: 1 if i % 10 == 0 else fmt.DENSE_TIER_ID),
-             ("far-partial", 1500, lambda i: 1 if i % 10 == 0 else 2)]
+             ("t3", 250, lambda i: 3), ("wide", 1600, lambda i: 1 if i % 10 == 0 else fmt.DENSE_TIER_ID),
+             ("far", 2240, lambda i: 1 if i % 14 == 0 else fmt.DENSE_TIER_ID),
+             ("far-partial", 2100, lambda i: 1 if i % 14 == 0 else 2)]
     for name, L, tier in cases:
         tier_of = [np.array([tier(i) for i in range(L)], np.int32) for _ in range(H)]
         cbs = synth.make_codebooks(rng, H, dh, [1, 2, 3])
