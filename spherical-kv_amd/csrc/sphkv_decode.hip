@@ -111,15 +111,13 @@ __host__ __device__ constexpr int chunk_dim(int c, int u) {
 // l = token t = l % 16, quarter u = l / 16).  Lanes that load nothing carry
 // kOOB; the page-dependent part is a wave-uniform base added to them.
 struct LaneOff {
-  uint32_t row, vs, stg, pos, kd, v;
+  uint32_t stg, pos, kd, v;
 };
 
 template <int DH>
 __device__ __forceinline__ LaneOff lane_offsets(int lane) {
   const int t = lane & 15, u = lane >> 4;
   LaneOff o;
-  o.row = lane < 3 ? 4u * lane : (uint32_t)kOOB;            // pointer-table row: 3 dwords
-  o.vs = lane == 3 ? 0u : (uint32_t)kOOB;                   // V slot
   o.stg = 8u * lane;                                        // 512-byte staging window
   o.pos = 4u * t;                                           // position of token t
   o.kd = (uint32_t)(t * DH + chunk_dim<DH>(0, u)) * 2u;     // dense K: chunk 0 of (t, u)
@@ -129,67 +127,119 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
 
 __device__ __forceinline__ uint32_t oob_or(int ok, uint32_t base) { return ok ? base : (uint32_t)kOOB; }
 
-// Pointer-table row of one page (wave-uniform): lanes 0..2 fetch the row,
-// lane 3 the V slot; the values are read out (readlane) when the page is
-// taken.  The page loop's scalar conditions are kept as 0/1 integers, which
-// stay single scalar registers (boolean values become 64-bit lane masks).
-struct RowLd { int x, y; };
-struct Row {
-  int page_off, th_off, rad_off, vs;
-  int ok;          // 1: the row is one of the item's and addresses the pools
-  int present;     // 1: the row is one of the item's (p < end)
-};
+// Page table of up to 64 pages of a wave, one page per lane (lane i: the
+// wave's page kb + i).  Lanes load the pages' pointer-table rows, V slots
+// and header dwords and check them once, lane-parallel, so a page step only
+// reads its page's entries with readlane.  A malformed row or page
+// contributes no token and is counted: a row that does not address the pools
+// (page_off < 0, not 4-byte aligned, header past the pool, V slot past the
+// pool), an unknown tier id, a count above 16, a dense page whose K rows are
+// not 16-byte aligned inside its section and the pool, a compressed page
+// whose sections leave its 512-byte staging window or the pool.
+//   sbase  staging-window offset (page_off), kOOB for a bad row
+//   vsl    V slot, -1 for a bad row
+//   dbase  dense K rows (th_off) of a row that can be a dense page's (th_off
+//          16-byte aligned, th_off + 2*DH <= rad_off: a compressed page's
+//          theta section is < 2*DH bytes), kOOB otherwise -- a prefetch hint;
+//          the header decides how the page is processed
+//   desc   tier (1..3, 0: none) | dense << 2 | n << 3 | thr << 8 | rdr << 18 |
+//          bad << 28: the page's tokens to use and its compressed sections'
+//          offsets from the page start
+struct PageRows { int page_off, th_off, rad_off, vs; };
+struct PageTab { int sbase, vsl, dbase, desc; };
 
-__device__ __forceinline__ RowLd row_issue(const Res& rs, const LaneOff& lo, int p, int re) {
-  const int ok = p < re;
-  RowLd l;
-  l.x = __builtin_amdgcn_raw_buffer_load_b32(rs.ptab, (int)(oob_or(ok, 12u * (uint32_t)p) + lo.row), 0, 0);
-  l.y = __builtin_amdgcn_raw_buffer_load_b32(rs.vslot, (int)(oob_or(ok, 4u * (uint32_t)p) + lo.vs), 0, 0);
-  return l;
-}
-
-__device__ __forceinline__ Row row_take(const DecodeArgs& a, const RowLd& l, int p, int re) {
-  Row r;
-  r.page_off = __builtin_amdgcn_readlane(l.x, 0);
-  r.th_off = __builtin_amdgcn_readlane(l.x, 1);
-  r.rad_off = __builtin_amdgcn_readlane(l.x, 2);
-  r.vs = __builtin_amdgcn_readlane(l.y, 3);
-  r.present = p < re;
-  // page_off >= 0, 4-byte aligned, header inside the pool; V slot in the pool
-  r.ok = r.present & (int)((r.page_off & 0x80000003) == 0) & (int)(r.page_off <= a.pages_m8) &
-         (int)((uint32_t)r.vs < (uint32_t)a.nvp32);
+__device__ __forceinline__ PageRows rows_issue(const Res& rs, int p0, int wstride, int kb, int nwp, int lane) {
+  const int k = kb + lane;
+  const uint32_t p = (uint32_t)(k < nwp ? p0 + k * wstride : 0);
+  const auto w = __builtin_amdgcn_raw_buffer_load_b96(rs.ptab, (int)(k < nwp ? 12u * p : (uint32_t)kOOB), 0, 0);
+  PageRows r;
+  r.page_off = (int)w[0];
+  r.th_off = (int)w[1];
+  r.rad_off = (int)w[2];
+  r.vs = __builtin_amdgcn_raw_buffer_load_b32(rs.vslot, (int)(k < nwp ? 4u * p : (uint32_t)kOOB), 0, 0);
   return r;
 }
 
-// A dense page's theta section holds n*DH*2 bytes; a compressed page's at most
-// ceil(16*G*b/8) < 2*DH.  Used only to decide what to prefetch; the page header
-// decides how the page is processed.
+// Row checks (lane-parallel): the staging / V / dense-K load bases.
 template <int DH>
-__device__ __forceinline__ int row_looks_dense(const Row& r) {
-  return r.ok & (int)((r.th_off & 0x8000000F) == 0) & (int)(r.rad_off >= 0) &
-         (int)((uint32_t)r.th_off + 2 * DH <= (uint32_t)r.rad_off);
+__device__ __forceinline__ PageTab page_bases(const DecodeArgs& a, const PageRows& r, int kb, int nwp, int lane) {
+  const bool present = kb + lane < nwp;
+  const bool ok = present && (r.page_off & 0x80000003) == 0 && r.page_off <= a.pages_m8 &&
+                  (uint32_t)r.vs < (uint32_t)a.nvp32;
+  const bool dense_like = ok && (r.th_off & 0x8000000F) == 0 && r.rad_off >= 0 &&
+                          (uint32_t)r.th_off + 2 * DH <= (uint32_t)r.rad_off;
+  PageTab t;
+  t.sbase = ok ? r.page_off : kOOB;
+  t.vsl = ok ? r.vs : -1;
+  t.dbase = dense_like ? r.th_off : kOOB;
+  t.desc = 0;
+  return t;
 }
 
-// 512-byte staging window [page_off, +512) of a page (page_off is 4-byte
-// aligned): 8 bytes per lane (bytes past the pool read as zero); the page
-// header is lane 0's first dword.
-__device__ __forceinline__ uint2 load_stage(const Res& rs, const LaneOff& lo, const Row& r) {
-  const auto w = __builtin_amdgcn_raw_buffer_load_b64(rs.pages, (int)(oob_or(r.ok, (uint32_t)r.page_off) + lo.stg), 0, 0);
+// Header dword of each lane's page (zero for a bad row: its load is out of
+// range).
+__device__ __forceinline__ int header_issue(const Res& rs, const PageTab& t) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rs.pages, t.sbase, 0, 0);
+}
+
+// Header checks (lane-parallel) -> desc; returns the bad pages' count.
+template <int DH>
+__device__ __forceinline__ int page_check(const DecodeArgs& a, const PageRows& r, PageTab& t, int hw, int kb,
+                                          int nwp, int lane) {
+  const bool present = kb + lane < nwp;
+  const bool ok = t.sbase != kOOB;
+  const int tid = ok ? (hw & 0xFF) : 0;
+  const int cnt = (hw >> 8) & 0xFF;
+  const bool dense = tid == kDenseTier;
+  const bool comp = (uint32_t)(tid - 1) < 3u;                  // tiers 1..3
+  bool bad = (present && !ok) || (ok && !(dense || comp)) || ((dense || comp) && cnt > kTile);
+  int n = (dense || comp) ? min(cnt, kTile) : 0;
+  int thr = 0, rdr = 0;
+  if (comp) {
+    // theta bytes ceil(n*G*b/8) and radius bytes n*G of tiers 1, 2, 3; the
+    // theta section ends 4 bytes before the window's end (the code reads
+    // take 64 bits)
+    const int G = DH / tier_g(tid), tb = (n * G * tier_b(tid) + 7) >> 3, rbytes = n * G;
+    const int t0 = (int)((uint32_t)r.th_off - (uint32_t)r.page_off);
+    const int r0 = (int)((uint32_t)r.rad_off - (uint32_t)r.page_off);
+    const bool sec_ok = r.th_off >= r.page_off && r.rad_off >= r.page_off && t0 <= 508 - tb && r0 <= 512 - rbytes &&
+                        r.th_off <= a.pages32 - tb && r.rad_off <= a.pages32 - rbytes;
+    bad = bad || !sec_ok;
+    n = sec_ok ? n : 0;
+    thr = sec_ok ? t0 : 0;
+    rdr = sec_ok ? r0 : 0;
+  } else if (dense) {
+    const uint32_t kend = (uint32_t)r.th_off + (uint32_t)(n * DH * 2);
+    const bool dense_ok = t.dbase != kOOB && kend <= (uint32_t)r.rad_off && kend <= (uint32_t)a.pages32;
+    bad = bad || !dense_ok;
+    n = dense_ok ? n : 0;
+  }
+  t.desc = (comp ? tid : 0) | (int)dense << 2 | n << 3 | thr << 8 | rdr << 18 | (int)bad << 28;
+  return __builtin_popcountll(__ballot(bad));
+}
+
+// 512-byte staging window [sbase, +512) of a page (sbase is 4-byte aligned):
+// 8 bytes per lane (bytes past the pool read as zero); the page header is
+// lane 0's first dword.
+__device__ __forceinline__ uint2 load_stage(const Res& rs, const LaneOff& lo, int sbase) {
+  const auto w = __builtin_amdgcn_raw_buffer_load_b64(rs.pages, (int)((uint32_t)sbase + lo.stg), 0, 0);
   return uint2{(uint32_t)w[0], (uint32_t)w[1]};
 }
 
-__device__ __forceinline__ int load_pos(const Res& rs, const LaneOff& lo, const Row& r, int p) {
-  return __builtin_amdgcn_raw_buffer_load_b32(rs.pos, (int)(oob_or(r.ok, (uint32_t)p * (4u * kTile)) + lo.pos), 0, 0);
+// Positions of row p's 16 tokens (lane t: token t's); none for a bad row.
+__device__ __forceinline__ int load_pos(const Res& rs, const LaneOff& lo, int sbase, int p) {
+  return __builtin_amdgcn_raw_buffer_load_b32(
+      rs.pos, (int)(oob_or(sbase != kOOB, (uint32_t)p * (4u * kTile)) + lo.pos), 0, 0);
 }
 
 // V page layout, dim-major: element (token k, dim d) at half d * 16 + k.  Lane
 // l loads dims l + 64 hf (hf < DH/64), 16 tokens = 32 bytes each: vreg[2hf]
 // holds tokens 0..7, vreg[2hf + 1] tokens 8..15 -- the B operands of the
-// 4x4x4 PV MFMA.
+// 4x4x4 PV MFMA.  vsl < 0: nothing (zeros).
 template <int DH>
-__device__ __forceinline__ void load_v(const DecodeArgs& a, const LaneOff& lo, const Row& r, half8 (&vreg)[DH / 32]) {
+__device__ __forceinline__ void load_v(const DecodeArgs& a, const LaneOff& lo, int vsl, half8 (&vreg)[DH / 32]) {
   // 64-bit element offset: vslot * DH * 16 exceeds 2^31 from vslot 2^20 (DH 128)
-  const rsrc_t rs = make_rsrc(a.v_pool + (int64_t)r.vs * (DH * kTile), r.ok ? DH * kTile * 2 : 0);
+  const rsrc_t rs = make_rsrc(a.v_pool + (int64_t)max(vsl, 0) * (DH * kTile), vsl >= 0 ? DH * kTile * 2 : 0);
 #pragma unroll
   for (int hf = 0; hf < DH / 64; ++hf)
 #pragma unroll
@@ -199,14 +249,14 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, const LaneOff& lo, c
     }
 }
 
-// Dense K rows of a page (fp16 [n][DH] at th_off, 16-byte aligned): lane
+// Dense K rows of a page (fp16 [n][DH] at dbase, 16-byte aligned): lane
 // (t, u) loads chunks c = 0..NC-1 (dims chunk_dim(c, u) .. +8) of token t.
-// Compressed pages load nothing.  Rows of tokens past the page's count read
-// neighbouring bytes of the pool (or zeros past its end) and are not used.
+// Rows of tokens past the page's count read neighbouring bytes of the pool
+// (or zeros past its end) and are not used.
 template <int DH>
-__device__ __forceinline__ void load_dense(const Res& rs, const LaneOff& lo, const Row& r, uint4 (&kd)[DH / 32]) {
+__device__ __forceinline__ void load_dense(const Res& rs, const LaneOff& lo, int dbase, uint4 (&kd)[DH / 32]) {
   constexpr int NC = DH / 32;
-  const uint32_t base = oob_or(row_looks_dense<DH>(r), (uint32_t)r.th_off) + lo.kd;
+  const uint32_t base = (uint32_t)dbase + lo.kd;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const uint32_t d = (uint32_t)(chunk_dim<DH>(c, 0) - chunk_dim<DH>(0, 0)) * 2u;
@@ -414,12 +464,11 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   _Float16* pt = reinterpret_cast<_Float16*>(smem + L::o_pt) + wave * L::PR * kTile;
   const LaneOff lo = lane_offsets<DH>(lane);
 
-  int p = rb + wave * rstride;
+  const int p0 = rb + wave * rstride;                   // row of the wave's first page
   const Res rs = make_res(a);
-  // ---- first pages' pointer-table rows, then the shared tables' loads ----
-  RowLd rl_c = row_issue(rs, lo, p, re);
-  RowLd rl_n = row_issue(rs, lo, p + wstride, re);
-  RowLd rl_2 = row_issue(rs, lo, p + 2 * wstride, re);
+  // ---- pointer-table rows of the wave's first 64 pages (one page per
+  //      lane), then the shared tables' loads -----------------------------
+  const PageRows rows0 = rows_issue(rs, p0, wstride, 0, nwp, lane);
   // codebooks: every load of a thread is issued before its first LDS store
   constexpr int kT = kWaves * 64;
   constexpr int n4_1 = L::cb_n1 / 20 * 4, n4_2 = L::cb_n2 / 20 * 4, n4_3 = L::cb_n3 / 36 * 8;  // float4s
@@ -465,17 +514,23 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     row[j & 3] = z.x;
     row[4 + (j & 3)] = z.y;
   }
-  // first page: its staging window, positions, V and dense K are issued as
-  // soon as its pointer-table row is in, so the page data streams in while
-  // the codebooks are stored
-  Row row_c = row_take(a, rl_c, p, re);
-  uint2 stg_c = load_stage(rs, lo, row_c);
-  int pos_c = load_pos(rs, lo, row_c, p);
+  // row checks; the pages' header loads and the first page's staging window,
+  // positions, V and dense K are issued as soon as the rows are in, so the
+  // page data streams in while the codebooks are stored
+  PageTab T = page_bases<DH>(a, rows0, 0, nwp, lane);
+  const int hdr0 = header_issue(rs, T);
+  uint2 stg_c, stg_b;
+  int pos_c, pos_b;
   half8 vreg[DH / 32];
   uint4 kd[NC];
-  load_v<DH>(a, lo, row_c, vreg);
-  if (row_looks_dense<DH>(row_c)) load_dense<DH>(rs, lo, row_c, kd);
-  Row row_n = row_take(a, rl_n, p + wstride, re);
+  {
+    const int sb = __builtin_amdgcn_readfirstlane(T.sbase);
+    stg_c = load_stage(rs, lo, sb);
+    pos_c = load_pos(rs, lo, sb, p0);
+    load_v<DH>(a, lo, __builtin_amdgcn_readfirstlane(T.vsl), vreg);
+    const int db = __builtin_amdgcn_readfirstlane(T.dbase);
+    if (db != kOOB) load_dense<DH>(rs, lo, db, kd);
+  }
   if (GQA < 4) {
     // zero P rows GQA..3 and the query slots GQA..3 of this wave (never written)
     if (lane < (4 - GQA) * 2) {
@@ -503,6 +558,9 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     }
   }
   __syncthreads();
+  // the header checks wait for this wave's header loads only (after the
+  // barrier, so no wave waits for another's)
+  int nbad = page_check<DH>(a, rows0, T, hdr0, 0, nwp, lane);   // malformed rows / pages of this wave
 
   // Loop-invariant lane data: LDS addresses of this lane's query writes /
   // reads and P write / read.
@@ -531,8 +589,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
 #pragma unroll
     for (int hf = 0; hf < NHF; ++hf) acc[hs][hf] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
-  int pages_done = 0;                                   // pages of this wave processed so far
-  int prio_next = 0;                                    // pages_done at which the priority changes
+  int prio_next = 0;                                    // page index at which the priority changes
   // issue priority of the wave's page d from its share of pages still to do:
   // a SIMD serves its waves oldest first, so without it the youngest wave
   // would finish last, alone on its SIMD
@@ -540,65 +597,40 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
     const int left = nwp - d;                           // pages left, page d included
     return 4 * left > 3 * nwp ? 3 : (2 * left > nwp ? 2 : (4 * left > nwp ? 1 : 0));
   };
-  int nbad = 0;                                         // malformed rows / pages of this wave
-  // One page of the pipeline.  The staging window and positions of the next
-  // page are loaded into the other register set of a pair, and the pointer-
-  // table rows into the other slot of a pair, so the loop (unrolled by two)
-  // never copies a register that a load is still filling: such a copy would
-  // wait for that load.
-  auto step = [&](const int p, uint2& stg_c, int& pos_c, uint2& stg_n, int& pos_n, RowLd& rl_issue,
-                  RowLd& rl_take) __attribute__((always_inline)) {
+  // Page k of the pipeline.  The staging window and positions of the next
+  // page are loaded into the other register set of a pair, so the loop
+  // (unrolled by two) never copies a register that a load is still filling:
+  // such a copy would wait for that load.
+  auto step = [&](const int k, uint2& stg_c, int& pos_c, uint2& stg_n, int& pos_n) __attribute__((always_inline)) {
     // ---- issue priority (changes at most three times per item) ----------
-    if (pages_done == prio_next) {
-      const int lvl = prio_of(pages_done);
+    if (k == prio_next) {
+      const int lvl = prio_of(k);
       set_prio(lvl);
-      int d = pages_done + 1;
+      int d = k + 1;
       while (d < nwp && prio_of(d) == lvl) ++d;
       prio_next = d;
     }
-    // ---- issue: row three pages ahead, stage/positions one page ahead -----
-    rl_issue = row_issue(rs, lo, p + 3 * wstride, re);
-    stg_n = load_stage(rs, lo, row_n);
-    pos_n = load_pos(rs, lo, row_n, p + wstride);
-
-    // ---- this page's header: lane 0's first dword of the stage ------------
-    const int hw = __builtin_amdgcn_readfirstlane((int)stg_c.x);
-    const int tid = row_c.ok ? (hw & 0xFF) : 0;
-    const int cnt = (hw >> 8) & 0xFF;
-    // A malformed row or page contributes no token and is counted: a row that
-    // does not address the pools, an unknown tier id, a count above 16, a
-    // dense page whose K rows are not 16-byte aligned inside its section and
-    // the pool, a compressed page whose sections leave its 512-byte staging
-    // window or the pool.
-    const int dense = (int)(tid == kDenseTier);
-    const int comp = (int)((uint32_t)(tid - 1) < 3u);        // tiers 1..3
-    int bad = (row_c.present & (row_c.ok ^ 1)) | (row_c.ok & ((dense | comp) ^ 1)) |
-              ((dense | comp) & (int)(cnt > kTile));
-    int n = (dense | comp) ? min(cnt, kTile) : 0;
-    int thr = 0, rdr = 0;                       // section offsets from the page start
-    if (comp) {
-      // bits per token (G*b) and radius bytes per token (G) of tiers 1, 2, 3
-      constexpr uint32_t kGb = DH == 128 ? (48u | 32u << 8 | 12u << 16) : (24u | 16u << 8 | 6u << 16);
-      constexpr uint32_t kGg = DH == 128 ? (8u | 8u << 8 | 4u << 16) : (4u | 4u << 8 | 2u << 16);
-      const int sh8 = 8 * (tid - 1);
-      const int tb = (n * (int)((kGb >> sh8) & 0xFF) + 7) >> 3, rbytes = n * (int)((kGg >> sh8) & 0xFF);
-      const int t0 = (int)((uint32_t)row_c.th_off - (uint32_t)row_c.page_off);
-      const int r0 = (int)((uint32_t)row_c.rad_off - (uint32_t)row_c.page_off);
-      const int sec_ok = (int)(row_c.th_off >= row_c.page_off) & (int)(row_c.rad_off >= row_c.page_off) &
-                         (int)(t0 <= 508 - tb) & (int)(r0 <= 512 - rbytes) &
-                         (int)(row_c.th_off <= a.pages32 - tb) & (int)(row_c.rad_off <= a.pages32 - rbytes);
-      bad |= sec_ok ^ 1;
-      n = sec_ok ? n : 0;
-      thr = sec_ok ? t0 : 0;
-      rdr = sec_ok ? r0 : 0;
-    } else if (dense) {
-      const uint32_t kend = (uint32_t)row_c.th_off + (uint32_t)(n * DH * 2);
-      const int dense_ok = row_looks_dense<DH>(row_c) & (int)(kend <= (uint32_t)row_c.rad_off) &
-                           (int)(kend <= (uint32_t)a.pages32);
-      bad |= dense_ok ^ 1;
-      n = dense_ok ? n : 0;
+    // ---- this page's descriptor; the last page of 64 loads and checks the
+    //      next 64 pages' table (a wait for two loads, once per 64 pages) ---
+    const int kl = k & 63;
+    const int desc = __builtin_amdgcn_readlane(T.desc, kl);
+    if (kl == 63 && k + 1 < nwp) {
+      const PageRows rw = rows_issue(rs, p0, wstride, k + 1, nwp, lane);
+      T = page_bases<DH>(a, rw, k + 1, nwp, lane);
+      nbad += page_check<DH>(a, rw, T, header_issue(rs, T), k + 1, nwp, lane);
     }
-    nbad += bad;
+    const int kn = (k + 1) & 63;
+    // ---- issue: stage / positions one page ahead ------------------------
+    {
+      const int sb = __builtin_amdgcn_readlane(T.sbase, kn);
+      stg_n = load_stage(rs, lo, sb);
+      pos_n = load_pos(rs, lo, sb, p0 + (k + 1) * wstride);
+    }
+    const int tid = desc & 3;                   // compressed tier (0: not compressed)
+    const int comp = (int)(tid != 0);
+    const int dense = (desc >> 2) & 1;
+    const int n = (desc >> 3) & 31;             // tokens to use
+    const int thr = (desc >> 8) & 1023, rdr = (desc >> 18) & 1023;   // section offsets from the page start
     const bool valid = (t < n) && (pos_c >= 0);
 
     // ---- page centre t_mid; query rows rotated by -t_mid into LDS ---------
@@ -800,22 +832,16 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
       int lane_v = lane;
       asm volatile("" : "+v"(lane_v));
       const LaneOff lv = lane_offsets<DH>(lane_v);
-      load_v<DH>(a, lv, row_n, vreg);
-      if (row_looks_dense<DH>(row_n)) load_dense<DH>(rs, lv, row_n, kd);
+      load_v<DH>(a, lv, __builtin_amdgcn_readlane(T.vsl, kn), vreg);
+      const int db = __builtin_amdgcn_readlane(T.dbase, kn);
+      if (db != kOOB) load_dense<DH>(rs, lv, db, kd);
     }
     wave_lds_sync();
-
-    row_c = row_n;
-    row_n = row_take(a, rl_take, p + 2 * wstride, re);
-    ++pages_done;
   };
-  uint2 stg_b;
-  int pos_b;
-  RowLd rl_3;
-  for (; p < re; p += 2 * wstride) {
-    step(p, stg_c, pos_c, stg_b, pos_b, rl_3, rl_2);
-    if (p + wstride >= re) break;
-    step(p + wstride, stg_b, pos_b, stg_c, pos_c, rl_2, rl_3);
+  for (int k = 0; k < nwp; k += 2) {
+    step(k, stg_c, pos_c, stg_b, pos_b);
+    if (k + 1 >= nwp) break;
+    step(k + 1, stg_b, pos_b, stg_c, pos_c);
   }
 
   __builtin_amdgcn_s_setprio(0);

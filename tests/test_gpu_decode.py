@@ -58,6 +58,20 @@ def test_decode_work_split_invariance(gpu):
     assert max_err(outs[0], outs[1]) < 2e-3 * 0.25 and max_err(outs[1], outs[2]) < 2e-3 * 0.25
 
 
+def test_decode_long_items_matches_oracle(gpu):
+    # one work item per (seq, head): ~1,300 pages per item, over 100 per wave,
+    # so each wave's page table is reloaded (and rechecked) past its 64th page
+    wl = synth.make_decode_workload(2, ctx_override=20000)
+    pool, cpu = pool_from_oracle(wl, gpu, rows_per_item=1 << 20)
+    per_item = np.diff(pool.work_start.cpu().numpy())
+    assert per_item.max() == 1 and pool.num_items == wl.num_kv
+    got = _decode(pool, wl, gpu)
+    want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+    err = max_err(got, want)
+    log(f"long items: {pool.num_items} items, rows {wl.plan.tokens.shape[0]}, max abs err {err:.3e}")
+    assert err <= TOL
+
+
 def test_decode_interleaved_and_contiguous_items_agree(gpu):
     # the same pool decoded with interleaved (strided) and contiguous work
     # items: only the order of the log-sum-exp merge differs
