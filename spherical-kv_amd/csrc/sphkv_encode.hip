@@ -77,6 +77,33 @@ __device__ __forceinline__ float torch_norm(const float* x, int g) {
   return __builtin_sqrtf(b);  // correctly rounded expansion (v_sqrt_f32 alone is not)
 }
 
+// dir[i] = x[i] / den, correctly rounded, for the GG values of one group
+// (den = the group's norm + 1e-8 > 0).  The division's own sequence is a
+// reciprocal of den refined once, then the quotient refined twice, framed by
+// operand scaling and a special-value fixup; with fp16 inputs (x = 0 or
+// 2^-24 <= |x| <= den) and a finite den, neither the scaling nor the fixup
+// changes anything (no operand or quotient is denormal or near overflow), so
+// the same steps run with the reciprocal shared by the group and give the
+// same bits.  (The fixup gives a zero quotient the sign of x; copysign does
+// here.)  Other inputs divide each value on its own.
+template <int GG>
+__device__ __forceinline__ void group_directions(const float* x, float den, bool fp16_in, float* dir) {
+  if (fp16_in && den < 1e30f) {
+    const float r0 = __builtin_amdgcn_rcpf(den);
+    const float r = __builtin_fmaf(__builtin_fmaf(-den, r0, 1.0f), r0, r0);
+#pragma unroll
+    for (int i = 0; i < GG; ++i) {
+      const float q = __fmul_rn(x[i], r);
+      const float q1 = __builtin_fmaf(__builtin_fmaf(-den, q, x[i]), r, q);
+      const float q2 = __builtin_fmaf(__builtin_fmaf(-den, q1, x[i]), r, q1);
+      dir[i] = __builtin_copysignf(q2, x[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < GG; ++i) dir[i] = __fdiv_rn(x[i], den);
+  }
+}
+
 typedef const float __attribute__((address_space(4)))* cb_ptr;   // read through the scalar cache
 
 constexpr int kEncWaves = 8;       // waves per workgroup: one per group in the argmax phase
@@ -200,8 +227,7 @@ __device__ __forceinline__ void encode_group(const EncodeArgs& a, int64_t kofs, 
   const float r = torch_norm(x, GG);
   const float den = __fadd_rn(r, 1e-8f);
   float dir[GG];
-#pragma unroll
-  for (int i = 0; i < GG; ++i) dir[i] = __fdiv_rn(x[i], den);
+  group_directions<GG>(x, den, !a.k_is_fp32, dir);
   r_out = r;
   code_out = naive ? argmax_codes<GG, true>(dir, cbg, C) : argmax_codes<GG, false>(dir, cbg, C);
 }
@@ -296,8 +322,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
         }
         r = live ? torch_norm(x, 16) : 0.f;
         const float den = __fadd_rn(r, 1e-8f);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dir[i] = live ? __fdiv_rn(x[i], den) : 0.f;
+        group_directions<16>(x, den, !a.k_is_fp32, dir);         // x = 0 (dir = +0) where not live
       }
       {
         _Float16* d = sm.u.arg.dh[wave][lane];
