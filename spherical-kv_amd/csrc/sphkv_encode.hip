@@ -123,7 +123,6 @@ struct EncodeLds {
     } arg;
     struct {                                   // build phase
       uint8_t stage[kEncPages][512];           // page images
-      int32_t cs[kEncPages][kTile * kEncMaxG]; // a page's codes, token-major
       _Float16 vt[kEncPages][DH * kTile];      // V pages, dim-major
     } build;
   } u;
@@ -579,7 +578,6 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     scale_[k] = m;
   }
   uint8_t* st = sm.u.build.stage[j];
-  int32_t* cs = sm.u.build.cs[j];
   const int nG = n * G;
   const int tb = (nG * b + 7) / 8;
   const int hdr = kHeaderBytes + 4 * G;
@@ -589,11 +587,28 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     const int gi = gs + 4 * k;
     if (t == 0 && gi < G) *reinterpret_cast<float*>(st + kHeaderBytes + 4 * gi) = scale_[k];
   }
+  // LSB-first bit stream (bitpacking.py:14-27): bit j of item i = (token t,
+  // group gi), i = t*G + gi, at bit i*b + j.  The theta section's dwords (hdr
+  // = 8 + 4G is a multiple of 4) are cleared, then every item ORs its b bits
+  // into the one or two dwords they fall in.
+  uint32_t* thw = reinterpret_cast<uint32_t*>(st + hdr);
+  for (int w = lane; w < (tb + 3) / 4; w += kWave) thw[w] = 0u;
+  wave_lds_sync();
+  for (int k = 0; k < nk; ++k) {
+    const int gi = gs + 4 * k;
+    if (!tok_ok || gi >= G) continue;
+    const uint32_t c = (uint32_t)best_[k];
+    const int o = (t * G + gi) * b, w = o >> 5, sh = o & 31;
+    __hip_atomic_fetch_or(thw + w, c << sh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (sh + b > 32) __hip_atomic_fetch_or(thw + w + 1, c >> (32 - sh), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  // the radius codes, after the ORs (the first radius bytes can share the
+  // last theta dword)
+  wave_lds_sync();
   for (int k = 0; k < nk; ++k) {
     const int gi = gs + 4 * k;
     if (!tok_ok || gi >= G) continue;
     const int item = t * G + gi;
-    cs[item] = best_[k];
     const float safe = scale_[k] < 1e-8f ? 1e-8f : scale_[k];
     float qv = __fmul_rn(__fdiv_rn(rr_[k], safe), 127.0f);
     qv = __builtin_rintf(qv);
@@ -603,19 +618,14 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
     if (a.code_out) a.code_out[((int64_t)p * kTile + t) * (DH / 16) + gi] = best_[k];
   }
   wave_lds_sync();
-  // LSB-first bit stream (bitpacking.py:14-27): bit j of item i at bit i*b + j
-  for (int byte = lane; byte < tb; byte += kWave) {
-    uint32_t v = 0;
-    for (int bit = 0; bit < 8; ++bit) {
-      const int gb = byte * 8 + bit;
-      const int item = gb / b;
-      if (item < nG) v |= (uint32_t)((cs[item] >> (gb - item * b)) & 1) << bit;
-    }
-    st[hdr + byte] = (uint8_t)v;
+  if (page_off >= 0 && page_off + size <= a.pages_bytes) {
+    // whole dwords where the page is 4-byte aligned, then its last bytes
+    // (the next page may start right after it)
+    const int nw = (page_off & 3) == 0 ? size >> 2 : 0;
+    uint32_t* dw = reinterpret_cast<uint32_t*>(a.pages + page_off);
+    for (int i = lane; i < nw; i += kWave) dw[i] = reinterpret_cast<const uint32_t*>(st)[i];
+    for (int i = 4 * nw + lane; i < size; i += kWave) a.pages[page_off + i] = st[i];
   }
-  wave_lds_sync();
-  if (page_off >= 0 && page_off + size <= a.pages_bytes)
-    for (int i = lane; i < size; i += kWave) a.pages[page_off + i] = st[i];
 }
 
 int launch_encode(const EncodeLaunch& L, hipStream_t stream) {
