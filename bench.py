@@ -91,8 +91,8 @@ TRAFFIC_BYTES = {(2, "default"): 86461801}
 # included) and HBM bytes (FETCH_SIZE * 2 + WRITE_SIZE).  The VALU-issue bound
 # is that count at one wave64 VALU instruction per 4 cycles on each of the
 # 1024 SIMDs at 2.4 GHz.
-ENCODE_VALU_INSTS = {3: 8653627}
-ENCODE_TRAFFIC_BYTES = {3: 55618560}
+ENCODE_VALU_INSTS = {3: 6770579}
+ENCODE_TRAFFIC_BYTES = {3: 55598602}
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
