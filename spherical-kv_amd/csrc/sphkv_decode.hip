@@ -12,12 +12,14 @@
 // that completes a head needs device-scope stores, loads and counters, whose
 // cost on MI355X exceeds the kernel boundary.)
 //
-// Page loop, software pipelined per wave: while page p is computed, the
-// 512-byte staging window and positions of the wave's next page, its V and
-// (dense pages) its K rows, and the pointer-table row of the one after are in
-// flight.  The scalar work per page (validation of the row and the header,
-// page centre, issue priority) is kept to integer arithmetic on scalar
-// registers, and every lane's load offsets are fixed for the whole item.
+// Page loop, software pipelined per wave: while page k is computed, the
+// 512-byte staging window and positions of the wave's next page and its V and
+// (dense pages) its K rows are in flight.  The pointer-table rows, V slots
+// and header dwords of 64 pages at a time are loaded one page per lane and
+// checked lane-parallel (the page table); a page step reads its page's
+// descriptor and load bases with readlane, and its remaining scalar work
+// (page centre, issue priority) is integer arithmetic on scalar registers.
+// Every lane's load offsets are fixed for the whole item.
 //
 // Per page (16 tokens, positions pos_t), lane l = (token t = l % 16, quarter
 // u = l / 16), page centre t_mid = (min pos + max pos) / 2:
