@@ -349,6 +349,40 @@ def test_decode_v_slots_beyond_2_pow_20(gpu):
     del pool_hi
 
 
+def test_decode_malformed_rows_past_the_first_page_table(gpu):
+    # one work item per (seq, head), so wave w's page k is the head's row
+    # w + 12 k: rows past 12 * 64 = 768 sit in a wave's second page table
+    # (loaded and checked after its 64th page); four malformed rows there are
+    # skipped and counted like the others (this layout puts every dense page,
+    # the sink tokens' tier, in the first table)
+    wl = synth.make_decode_workload(2, ctx_override=20000)
+    pool, cpu = pool_from_oracle(wl, gpu, rows_per_item=1 << 20)
+    plan = wl.plan
+    rs = plan.row_start
+    assert pool.num_items == wl.num_kv and min(np.diff(rs)) > 900
+    comp = [p for p in range(rs[2] + 800, rs[3]) if plan.tier[p] == 1]
+    r_off, r_vs, r_tier, r_sec = int(rs[1]) + 801, int(rs[4]) + 870, int(rs[5]) + 900, comp[4]
+    assert min(r - rs[h] for r, h in [(r_off, 1), (r_vs, 4), (r_tier, 5), (r_sec, 2)]) >= 12 * 64
+    pt = plan.ptable.copy()
+    vs = plan.vslot.copy()
+    pt[r_off, 0] = -16                                 # page offset outside the pool
+    vs[r_vs] = plan.num_vpages + 5                     # V slot outside the V pool
+    pt[r_sec, 2] += 600                                # radius section beyond the 512-byte window
+    pages = pool.pages.clone()
+    pages[int(plan.ptable[r_tier, 0])] = 7             # unknown tier id
+    bad = ops.PagedPool(**{**pool.__dict__, "ptable": torch.as_tensor(pt, device=gpu),
+                           "vslot": torch.as_tensor(vs, device=gpu), "pages": pages})
+    q = torch.as_tensor(wl.q, device=gpu)
+    ws = torch.zeros(pool.workspace_bytes(wl.gqa), dtype=torch.uint8, device=gpu)
+    out = ops.decode_paged(bad, q, wl.gqa, wl.rope_theta, workspace=ws)
+    assert ops.decode_status(bad, ws, wl.gqa) == 4
+    want = oracle.decode_mode_b(cpu, _drop_rows(plan, [r_off, r_vs, r_tier, r_sec]), wl.codebooks,
+                                wl.q, wl.gqa, wl.rope_theta)
+    err = max_err(out.float().cpu().numpy(), want)
+    log(f"  malformed rows past the first page table skipped: max abs err {err:.3e}")
+    assert err <= TOL and torch.isfinite(out).all()
+
+
 def test_decode_malformed_rows_are_skipped_and_counted(gpu):
     # five malformed rows of different kinds: each contributes no token, the
     # checked entry reports all five, the output equals the oracle over the
