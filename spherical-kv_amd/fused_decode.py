@@ -20,13 +20,13 @@ import math
 import torch
 
 import sphkv_lib
-from sphkv_lib import check
+from sphkv_lib import check, current_stream
 
 _lib = sphkv_lib.load()          # raises if libsphkv.so is missing
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return current_stream()
 
 
 def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:

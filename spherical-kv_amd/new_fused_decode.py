@@ -12,13 +12,13 @@ from __future__ import annotations
 import torch
 
 import sphkv_lib
-from sphkv_lib import check
+from sphkv_lib import check, current_stream
 
 _lib = sphkv_lib.load()          # raises if libsphkv.so is missing
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return current_stream()
 
 
 def _dev(t, name, dtype):

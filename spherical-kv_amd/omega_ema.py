@@ -45,7 +45,7 @@ def omega_ema(m_q: torch.Tensor, l_q: torch.Tensor, omega_prev: torch.Tensor, nu
         raise ValueError("out must be a contiguous fp32 tensor shaped like omega_prev")
     rc = _lib.sphkv_omega_ema(m_q.data_ptr(), l_q.data_ptr(), m_q.stride(0), m_q.stride(1), omega_prev.data_ptr(),
                               out.data_ptr(), int(num_kv), int(kv_groups), int(max_blocks), float(ema_beta),
-                              torch.cuda.current_stream().cuda_stream)
+                              sphkv_lib.current_stream())
     check(rc, "omega_ema")
     return out
 

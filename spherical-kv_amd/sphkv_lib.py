@@ -80,6 +80,22 @@ def load():
     return _lib
 
 
+_raw_stream = None
+
+
+def current_stream() -> int:
+    """Raw handle of torch's current stream on the current device: every
+    launch of this package goes to it.  Uses torch's raw accessor where this
+    torch build has it (no Stream object built per launch)."""
+    global _raw_stream
+    import torch
+    if _raw_stream is None:
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+    if _raw_stream:
+        return _raw_stream(torch.cuda.current_device())
+    return torch.cuda.current_stream().cuda_stream
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().sphkv_last_error().decode(errors="replace")

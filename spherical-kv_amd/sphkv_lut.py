@@ -125,7 +125,7 @@ class LayerPool:
                 r_all.data_ptr(), th_all.data_ptr(), r_all.numel(), v_all.data_ptr(), v_all.shape[0],
                 page_src.data_ptr(), P, 0, self.theta_codes.data_ptr(), self.radius_codes.data_ptr(),
                 self.r_scales.data_ptr(), self.v_pool.data_ptr(), n_total, page_size, G_max, dh,
-                torch.cuda.current_stream().cuda_stream), "LayerPool page build")
+                sphkv_lib.current_stream()), "LayerPool page build")
 
         # ---- tables: host mirror (numpy) and device copies ------------------
         self.block_table_cpu = np.full((num_kv, self.max_blocks), -1, np.int32)

@@ -14,7 +14,7 @@ import numpy as np
 import torch
 
 import sphkv_format as fmt
-from sphkv_lib import check, load
+from sphkv_lib import check, current_stream, load
 
 _check_rc = check      # decode_paged's `check` argument shadows the name there
 
@@ -22,7 +22,7 @@ ROWS_PER_ITEM = 64     # pointer-table rows per decode work item (8 pages per wa
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return current_stream()
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -55,27 +55,29 @@ def auto_rows_per_item(row_start: np.ndarray, num_cus: int, slots_per_cu: int = 
     if total == 0 or lens.size == 0:
         return 8
 
-    def items(r: int) -> int:
-        return int(np.sum(np.maximum(1, -(-lens // r))))
+    def items(r: np.ndarray) -> np.ndarray:        # item totals of candidate row counts r
+        return np.maximum(1, -(-lens[None, :] // r[:, None])).sum(1)
 
     lo = max(8, -(-total // target))
     hi = max(lo, int(lens.max()))
-    if items(hi) > target:
+    if items(np.array([hi]))[0] > target:
         return max(8, -(-total // (4 * target)))
-    while lo < hi:                      # items(r) does not grow with r
-        mid = (lo + hi) // 2
-        if items(mid) <= target:
-            hi = mid
-        else:
-            lo = mid + 1
-    return lo
+    # items(r) does not grow with r: narrow [lo, hi] to its first r with
+    # items(r) <= target, 32 evenly spaced candidates per round
+    while hi - lo > 32:
+        r = lo + (np.arange(1, 33, dtype=np.int64) * (hi - lo)) // 32
+        ok = items(r) <= target
+        j = int(np.argmax(ok))                      # the last candidate (hi) always fits
+        lo, hi = (lo if j == 0 else int(r[j - 1]) + 1), int(r[j])
+    r = np.arange(lo, hi + 1, dtype=np.int64)
+    return int(r[int(np.argmax(items(r) <= target))])
 
 
 def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM, interleave: bool = True):
     """Split each (seq, head) row range [b, e) into n = ceil((e - b) /
-    rows_per_item) items of <= rows_per_item rows.  Returns (work int32
-    [n_items, 4] = (sh, first_row, end_row, stride), work_start int32
-    [num_sh + 1]).
+    rows_per_item) items of <= rows_per_item rows (an empty range gets one
+    empty item: its output is still written).  Returns (work int32 [n_items,
+    4] = (sh, first_row, end_row, stride), work_start int32 [num_sh + 1]).
 
     interleave (default): item i takes rows b + i, b + i + n, ... -- a head's
     rows are grouped by tier, so contiguous items would each hold one tier and
@@ -83,20 +85,24 @@ def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM, interle
     items all hold the head's tier mix.  Otherwise items are contiguous
     ranges (stride 1)."""
     rs = np.asarray(row_start, np.int64)
-    work, ws = [], [0]
-    for sh in range(rs.shape[0] - 1):
-        b, e = int(rs[sh]), int(rs[sh + 1])
-        if e == b:
-            work.append((sh, b, b, 1))       # empty context still writes its output
-        n = -(-(e - b) // rows_per_item)
-        for i in range(n):
-            if interleave:
-                work.append((sh, b + i, e, n))
-            else:
-                work.append((sh, b + i * rows_per_item, min(e, b + (i + 1) * rows_per_item), 1))
-        ws.append(len(work))
-    w = np.asarray(work, np.int32).reshape(-1, 4)
-    return w, np.asarray(ws, np.int32)
+    b, e = rs[:-1], rs[1:]
+    n = np.maximum(1, -(-(e - b) // rows_per_item))
+    ws = np.concatenate([[0], np.cumsum(n)])
+    sh = np.repeat(np.arange(b.size, dtype=np.int64), n)
+    i = np.arange(int(ws[-1]), dtype=np.int64) - ws[:-1][sh]      # item index within its range
+    if interleave:
+        cols = (sh, b[sh] + i, e[sh], n[sh])
+    else:
+        cols = (sh, b[sh] + i * rows_per_item, np.minimum(e[sh], b[sh] + (i + 1) * rows_per_item),
+                np.ones_like(sh))
+    return np.stack(cols, axis=1).astype(np.int32).reshape(-1, 4), ws.astype(np.int32)
+
+
+def _work_tensors(work: np.ndarray, ws: np.ndarray, dev) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The work list and its per-range starts on the device, in one copy."""
+    buf = torch.from_numpy(np.concatenate([work.reshape(-1), ws])).to(dev)
+    n = work.size
+    return buf[:n].view(-1, 4), buf[n:]
 
 
 def validate_plan(plan: fmt.PagePlan) -> None:
@@ -185,8 +191,7 @@ class PagedPool:
             positions=torch.as_tensor(plan.positions, device=dev),
             v_pool=torch.zeros((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
             codebooks=cbs,
-            work=torch.as_tensor(work, device=dev),
-            work_start=torch.as_tensor(ws, device=dev),
+            **dict(zip(("work", "work_start"), _work_tensors(work, ws, dev))),
             tier=torch.as_tensor(plan.tier, device=dev),
             count=torch.as_tensor(plan.count, device=dev),
             seq_head=torch.as_tensor(plan.seq_head, device=dev),
@@ -217,7 +222,7 @@ class PagedPool:
             plan=plan, pages=torch.zeros(plan.pages_bytes, dtype=torch.uint8, device=dev), ptable=plan.ptable,
             vslot=plan.vslot, positions=plan.positions,
             v_pool=torch.empty((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
-            codebooks=cbs, work=torch.as_tensor(work, device=dev), work_start=torch.as_tensor(ws, device=dev),
+            codebooks=cbs, **dict(zip(("work", "work_start"), _work_tensors(work, ws, dev))),
             tier=plan.tier, count=plan.count, seq_head=plan.seq_head)
 
     def cb_ptrs(self):
@@ -526,11 +531,13 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
         raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")
     if nbytes < 0 or ovf:
         raise ValueError("a sequence length exceeds tier_of's width, or the byte pool exceeds int32 offsets")
-    i32 = dict(dtype=torch.int32, device=dev)
-    out = dict(tier=torch.empty(rows, **i32), count=torch.empty(rows, **i32), ptable=torch.empty((rows, 3), **i32),
-               seq_head=torch.empty(rows, **i32), vslot=torch.empty(rows, **i32),
-               tokens=torch.empty((rows, 16), dtype=torch.int64, device=dev), positions=torch.empty((rows, 16), **i32),
-               src_rows=None if row_base is None else torch.empty((rows, 16), dtype=torch.int64, device=dev))
+    # the plan's arrays as views of two allocations (int32, int64)
+    b32 = torch.empty(rows * 23, dtype=torch.int32, device=dev)
+    b64 = torch.empty(rows * (16 if row_base is None else 32), dtype=torch.int64, device=dev)
+    out = dict(tier=b32[:rows], count=b32[rows:2 * rows], ptable=b32[2 * rows:5 * rows].view(rows, 3),
+               seq_head=b32[5 * rows:6 * rows], vslot=b32[6 * rows:7 * rows],
+               positions=b32[7 * rows:].view(rows, 16), tokens=b64[:16 * rows].view(rows, 16),
+               src_rows=None if row_base is None else b64[16 * rows:].view(rows, 16))
     rc = lib.sphkv_plan_pages_fill(
         tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), _ptr(positions),
         0 if positions is None else positions.stride(0), _ptr(row_base), num_seqs, int(num_kv), max_len, int(dh),
