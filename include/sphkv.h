@@ -368,8 +368,10 @@ int sphkv_build_layer_pool(const float* r, const int32_t* theta, int64_t n_elems
  * the counts from phase 1 to phase 2 (same arguments in both).
  *
  * Phase 1, sphkv_plan_pages_count: row_start int32
- * [num_seqs * num_kv + 1]; totals int32 [4], zero on entry, receives (rows,
- * byte-pool size or -1 when >= 2 GiB, invalid tier ids, offset overflows).
+ * [num_seqs * num_kv + 1]; totals int32 [4] receives (rows, byte-pool size
+ * or -1 when >= 2 GiB, invalid tier ids, sequence-length and offset
+ * overflows); both are written whole (no initial value needed) when
+ * num_seqs > 0.
  *
  * Phase 2, sphkv_plan_pages_fill: per row (capacity max_rows >= totals[0])
  * tier, count, ptable [rows, 3], seq_head, vslot (= row), tokens int64
@@ -387,6 +389,31 @@ int sphkv_plan_pages_fill(const uint8_t* tier_of, int64_t tier_stride, const int
                           int32_t max_len, int32_t dh, const int32_t* work, int32_t max_rows, int32_t* tier,
                           int32_t* count, int32_t* ptable, int32_t* seq_head, int32_t* vslot, int64_t* tokens,
                           int32_t* positions_out, int64_t* src_rows, void* stream);
+
+/*
+ * Host-side work list of sphkv_decode_paged (host pointers, no stream, no GPU
+ * call).  No reference counterpart: the reference's decode
+ * (decode_kernel.cu:249-289) runs one program per (batch, head) and has no
+ * work list; these split each (seq, head) row range [row_start[i],
+ * row_start[i + 1]) over work items.  row_start int32 [num_sh + 1],
+ * non-decreasing.
+ *
+ * sphkv_work_rows_per_item: rows per item.  When one item per CU can cover
+ * every range, the smallest r >= max(8, ceil(total / (num_cus *
+ * slots_per_cu))) whose item total sum_i max(1, ceil(len_i / r)) fits num_cus
+ * * slots_per_cu; otherwise max(8, ceil(total / (4 * num_cus *
+ * slots_per_cu))).  Returns r >= 8, or a negative SPHKV_E* code.
+ *
+ * sphkv_work_fill: work int32 [n, 4] = (sh, first_row, end_row, stride) with
+ * n = sum_i max(1, ceil(len_i / rows_per_item)) (capacity max_items), and
+ * work_start int32 [num_sh + 1] = first item of each range.  interleave != 0:
+ * item j of a range of n_i items takes rows b + j, b + j + n_i, ...;
+ * otherwise contiguous runs of rows_per_item rows (stride 1).  Returns n, or
+ * a negative SPHKV_E* code.
+ */
+int32_t sphkv_work_rows_per_item(const int32_t* row_start, int32_t num_sh, int32_t num_cus, int32_t slots_per_cu);
+int64_t sphkv_work_fill(const int32_t* row_start, int32_t num_sh, int32_t rows_per_item, int32_t interleave,
+                        int32_t* work, int64_t max_items, int32_t* work_start);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "../../include/sphkv.h"
 #include "sphkv_internal.h"
 
@@ -36,6 +38,24 @@ int launch_status(int rc, const char* what) {
     return fail(SPHKV_ELAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
   }
   return ok();
+}
+
+// a work list's row_start: num_sh + 1 non-decreasing, non-negative row indices
+bool row_start_ok(const int32_t* rs, int32_t num_sh) {
+  if (num_sh < 0 || (num_sh > 0 && !rs) || (rs && rs[0] < 0)) return false;
+  for (int32_t i = 0; i < num_sh; ++i)
+    if (rs[i + 1] < rs[i]) return false;
+  return true;
+}
+
+// items the ranges take at r rows per item: sum of max(1, ceil(len / r))
+int64_t work_items(const int32_t* rs, int32_t num_sh, int64_t r) {
+  int64_t n = 0;
+  for (int32_t i = 0; i < num_sh; ++i) {
+    const int64_t len = (int64_t)rs[i + 1] - rs[i];
+    n += len > r ? (len + r - 1) / r : 1;
+  }
+  return n;
 }
 
 bool dh_ok(int32_t dh) { return dh == 64 || dh == 128; }
@@ -457,6 +477,60 @@ int sphkv_plan_pages_fill(const uint8_t* tier_of, int64_t tier_stride, const int
   L.work = const_cast<int32_t*>(work); L.max_rows = max_rows; L.tier = tier; L.count = count; L.ptable = ptable;
   L.seq_head = seq_head; L.vslot = vslot; L.tokens = tokens; L.positions = positions_out; L.src_rows = src_rows;
   return launch_status(sphkv::launch_plan(L, 1, (hipStream_t)stream), fn);
+}
+
+int32_t sphkv_work_rows_per_item(const int32_t* row_start, int32_t num_sh, int32_t num_cus, int32_t slots_per_cu) {
+  const char* fn = "sphkv_work_rows_per_item";
+  if (num_cus < 1 || slots_per_cu < 1) return fail(SPHKV_EINVAL, "%s: num_cus and slots_per_cu must be >= 1", fn);
+  if (!row_start_ok(row_start, num_sh))
+    return fail(SPHKV_EINVAL, "%s: row_start must hold num_sh + 1 non-decreasing rows >= 0", fn);
+  const int64_t total = num_sh > 0 ? (int64_t)row_start[num_sh] - row_start[0] : 0;
+  if (total == 0) { ok(); return 8; }
+  const int64_t target = (int64_t)num_cus * slots_per_cu;
+  int64_t max_len = 0;
+  for (int32_t i = 0; i < num_sh; ++i) max_len = std::max<int64_t>(max_len, (int64_t)row_start[i + 1] - row_start[i]);
+  int64_t lo = std::max<int64_t>(8, (total + target - 1) / target), hi = std::max(lo, max_len);
+  ok();
+  // more ranges than one item per CU covers: about four smaller items per CU
+  if (work_items(row_start, num_sh, hi) > target) return (int32_t)std::max<int64_t>(8, (total + 4 * target - 1) / (4 * target));
+  // the item total does not grow with r: the first r in [lo, hi] that fits
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (work_items(row_start, num_sh, mid) <= target) hi = mid; else lo = mid + 1;
+  }
+  return (int32_t)lo;
+}
+
+int64_t sphkv_work_fill(const int32_t* row_start, int32_t num_sh, int32_t rows_per_item, int32_t interleave,
+                        int32_t* work, int64_t max_items, int32_t* work_start) {
+  const char* fn = "sphkv_work_fill";
+  if (rows_per_item < 1) return fail(SPHKV_EINVAL, "%s: rows_per_item must be >= 1", fn);
+  if (!row_start_ok(row_start, num_sh))
+    return fail(SPHKV_EINVAL, "%s: row_start must hold num_sh + 1 non-decreasing rows >= 0", fn);
+  const int64_t n = work_items(row_start, num_sh, rows_per_item);
+  if (n > INT32_MAX) return fail(SPHKV_EINVAL, "%s: more than 2^31 - 1 work items", fn);
+  if (n > max_items) return fail(SPHKV_EINVAL, "%s: %lld items exceed the capacity %lld", fn, (long long)n, (long long)max_items);
+  if (!work_start || (n > 0 && !work)) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  int32_t k = 0;
+  for (int32_t i = 0; i < num_sh; ++i) {
+    const int32_t b = row_start[i], e = row_start[i + 1];
+    const int64_t len = (int64_t)e - b;
+    const int32_t ni = len > rows_per_item ? (int32_t)((len + rows_per_item - 1) / rows_per_item) : 1;
+    work_start[i] = k;
+    for (int32_t j = 0; j < ni; ++j, ++k) {
+      int32_t* w = work + 4 * (int64_t)k;
+      w[0] = i;
+      if (interleave) {
+        w[1] = b + j; w[2] = e; w[3] = ni;
+      } else {
+        const int64_t r0 = b + (int64_t)j * rows_per_item;
+        w[1] = (int32_t)r0; w[2] = (int32_t)std::min<int64_t>(e, r0 + rows_per_item); w[3] = 1;
+      }
+    }
+  }
+  work_start[num_sh] = k;
+  ok();
+  return n;
 }
 
 }  // extern "C"

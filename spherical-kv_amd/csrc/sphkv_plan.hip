@@ -13,11 +13,21 @@
 // Kernels (a (sequence, head)'s tokens are cut into chunks of kPlanChunk):
 //   plan_count_kernel  per (sequence, head, chunk): tokens and first index
 //                      per tier, by wave ballots
-//   plan_scan_kernel   one workgroup: per (sequence, head) the chunks' rank
-//                      bases, tier order and rows (a thread each), then one
-//                      thread places the tier runs back to back (page i of a
-//                      run starts at run_start + i * align16(size of a full
-//                      page), so a run is placed in O(1))
+//   plan_scan_kernel   one workgroup: per (sequence, head) a wave scans its
+//                      chunks' counts into rank bases (64 chunks per load) and
+//                      sets the tier order and rows; then the tier runs are
+//                      placed back to back by a block-wide scan of placement
+//                      maps (below), each thread taking a contiguous span of
+//                      (sequence, head) ranges
+//
+// Placement as a map of the running byte offset x: a run of a compressed
+// tier starts at align16(x), a dense run at align16(x + 8) - 8 (payload
+// 16-byte aligned after the header); page i of a run starts at run_start +
+// i * align16(size of a full page), so the run ends at start + B with B fixed
+// by the tier and count.  Each run is therefore x -> 16 ceil((x + a) / 16) +
+// b (a = 0 or 8), and so is any chain of runs: (a1, b1) then (a2, b2) is
+// (a1, 16 ceil((b1 + a2) / 16) + b2).  The maps form a monoid (with the
+// identity for ranges without tokens) and scan in parallel.
 //   plan_fill_kernel   per (sequence, head, chunk): its share of the page
 //                      rows, then each token's rank within its tier (chunk
 //                      base + wave ballots) puts it in its page slot
@@ -53,8 +63,48 @@ __device__ __forceinline__ int64_t place(int64_t off, int k) {
 
 // per (sequence, head) record in the workspace, followed by the chunks' records
 enum : int { kCnt = 0, kFirst = 4, kRows = 8, kOrder = 9, kRunStart = 10, kRowStart = 14, kRec = 16 };
-enum : int { kChCnt = 0, kChFirst = 4, kChRec = 8 };    // per chunk: counts (then rank bases), first index
+// per chunk: counts (then rank bases), first index, invalid ids, sequence-length flag
+enum : int { kChCnt = 0, kChFirst = 4, kChBad = 8, kChLen = 9, kChRec = 12 };
 constexpr int kPlanChunk = 2048;
+constexpr int kScanThreads = 1024;
+constexpr int64_t kMaxOff = 0x7FFFFF00LL;   // byte offsets stay int32
+
+// placement map x -> 16 ceil((x + a) / 16) + b, or the identity (id != 0)
+struct Place { int64_t b; int a, id; };
+__device__ __forceinline__ int64_t ceil16(int64_t v) { return ((v + 15) >> 4) << 4; }
+__device__ __forceinline__ Place then(const Place& f, const Place& g) {      // f, then g
+  if (f.id) return g;
+  if (g.id) return f;
+  return Place{ceil16(f.b + g.a) + g.b, f.a, 0};
+}
+__device__ __forceinline__ int64_t apply(const Place& f, int64_t x) { return f.id ? x : ceil16(x + f.a) + f.b; }
+// bytes from a run's start to its end: full pages at align16 strides, then the last page
+__device__ __forceinline__ int64_t run_bytes(int k, int n, int dh) {
+  const int pages = (n + 15) / 16, last = n - 16 * (pages - 1);
+  return (int64_t)(pages - 1) * align16(page_bytes(k, 16, dh)) + page_bytes(k, last, dh);
+}
+__device__ __forceinline__ Place run_map(int k, int n, int dh) {
+  return k == 3 ? Place{run_bytes(k, n, dh) - kHeader, kHeader, 0} : Place{run_bytes(k, n, dh), 0, 0};
+}
+
+__device__ __forceinline__ int wave_scan_incl(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
 
 __device__ __forceinline__ int32_t* sh_rec(const PlanLaunch& a, int sh) { return a.work + (int64_t)sh * kRec; }
 __device__ __forceinline__ int32_t* ch_rec(const PlanLaunch& a, int sh, int c) {
@@ -67,7 +117,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(PlanLaunch a) 
   __shared__ int wc[kPlanThreads / 64][4], wf[kPlanThreads / 64][4], wbad[kPlanThreads / 64];
   const int sh = blockIdx.x / a.nchunks, c = blockIdx.x % a.nchunks, s = sh / a.num_kv;
   const int L = min(a.lens[s], a.max_len), t0 = c * kPlanChunk, t1 = min(L, t0 + kPlanChunk);
-  if (c == 0 && threadIdx.x == 0 && (a.lens[s] > a.max_len || a.lens[s] < 0)) atomicAdd(a.totals + 3, 1);
   const uint8_t* t_of = a.tier_of + (int64_t)sh * a.tier_stride;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int cnt[4] = {0, 0, 0, 0}, first[4] = {0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF}, bad = 0;
@@ -97,64 +146,129 @@ __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(PlanLaunch a) 
   if (threadIdx.x == 0) {
     int nb = 0;
     for (int w = 0; w < kPlanThreads / 64; ++w) nb += wbad[w];
-    if (nb) atomicAdd(a.totals + 2, nb);
+    int32_t* r = ch_rec(a, sh, c);
+    r[kChBad] = nb;
+    r[kChLen] = c == 0 && (a.lens[s] > a.max_len || a.lens[s] < 0);
   }
 }
 
-__global__ __launch_bounds__(1024) void plan_scan_kernel(PlanLaunch a) {
-  // per (sequence, head): chunk rank bases, counts, first index, tier order, rows
-  for (int sh = threadIdx.x; sh < a.num_sh; sh += blockDim.x) {
-    int cnt[4] = {0, 0, 0, 0}, first[4] = {0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF};
-    for (int c = 0; c < a.nchunks; ++c) {
-      int32_t* r = ch_rec(a, sh, c);
+__global__ __launch_bounds__(kScanThreads) void plan_scan_kernel(PlanLaunch a) {
+  __shared__ int64_t sb[kScanThreads];
+  __shared__ int sa[kScanThreads], srow[kScanThreads];
+  __shared__ int nbad, nflag;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
+  if (t == 0) { nbad = 0; nflag = 0; }
+  __syncthreads();
+  // (1) a wave per (sequence, head): its chunks' exclusive rank bases per
+  // tier, 64 chunks per step, then totals, first indices, tier order, rows
+  for (int sh = wave; sh < a.num_sh; sh += kScanThreads / 64) {
+    int carry[4] = {0, 0, 0, 0}, first[4] = {0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF}, bad = 0, flag = 0;
+    for (int c0 = 0; c0 < a.nchunks; c0 += 64) {          // wave-uniform trip count
+      const int c = c0 + lane;
+      int32_t* r = c < a.nchunks ? ch_rec(a, sh, c) : nullptr;
+      int n[4], f[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) { n[k] = r ? r[kChCnt + k] : 0; f[k] = r ? r[kChFirst + k] : 0x7FFFFFFF; }
+      if (r) { bad += r[kChBad]; flag |= r[kChLen]; }
+#pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int n = r[kChCnt + k];
-        r[kChCnt + k] = cnt[k];                          // exclusive rank base of the chunk
-        cnt[k] += n;
-        first[k] = min(first[k], r[kChFirst + k]);
+        const int incl = wave_scan_incl(n[k], lane);
+        if (r) r[kChCnt + k] = carry[k] + incl - n[k];
+        carry[k] += __shfl(incl, 63, 64);
+        first[k] = min(first[k], f[k]);
       }
     }
-    int32_t* rec = sh_rec(a, sh);
-    int order = 0, n_runs = 0, rows = 0;
-    bool used[4] = {false, false, false, false};
-    for (int q = 0; q < 4; ++q) {                        // tiers by first appearance
-      int best = -1;
-      for (int k = 0; k < 4; ++k)
-        if (!used[k] && cnt[k] > 0 && (best < 0 || first[k] < first[best])) best = k;
-      if (best < 0) break;
-      used[best] = true;
-      order |= best << (4 * n_runs);
-      ++n_runs;
-      rows += (cnt[best] + 15) / 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) first[k] = wave_min(first[k]);
+    bad = wave_sum(bad);
+    flag = wave_sum(flag);
+    if (lane == 0) {
+      int order = 0, n_runs = 0, rows = 0;
+      bool used[4] = {false, false, false, false};
+      for (int q = 0; q < 4; ++q) {                      // tiers by first appearance
+        int best = -1;
+        for (int k = 0; k < 4; ++k)
+          if (!used[k] && carry[k] > 0 && (best < 0 || first[k] < first[best])) best = k;
+        if (best < 0) break;
+        used[best] = true;
+        order |= best << (4 * n_runs);
+        ++n_runs;
+        rows += (carry[best] + 15) / 16;
+      }
+      for (int q = n_runs; q < 4; ++q) order |= 0xF << (4 * q);
+      int32_t* rec = sh_rec(a, sh);
+      for (int k = 0; k < 4; ++k) { rec[kCnt + k] = carry[k]; rec[kFirst + k] = first[k]; }
+      rec[kRows] = rows;
+      rec[kOrder] = order;
+      if (bad) atomicAdd(&nbad, bad);
+      if (flag) atomicAdd(&nflag, flag);
     }
-    for (int q = n_runs; q < 4; ++q) order |= 0xF << (4 * q);
-    for (int k = 0; k < 4; ++k) { rec[kCnt + k] = cnt[k]; rec[kFirst + k] = first[k]; }
-    rec[kRows] = rows;
-    rec[kOrder] = order;
   }
+  __syncthreads();                                       // the records above are visible to the whole workgroup
+  // (2) placement: thread t takes ranges [s0, s1); its runs composed into one
+  // map, an exclusive block scan of (map, rows), then its runs placed from
+  // the scanned offset
+  const int per = (a.num_sh + kScanThreads - 1) / kScanThreads;
+  const int s0 = min(t * per, a.num_sh), s1 = min(s0 + per, a.num_sh);
+  Place m{0, 0, 1};
+  int rows = 0;
+  for (int sh = s0; sh < s1; ++sh) {
+    const int32_t* rec = sh_rec(a, sh);
+    const int order = rec[kOrder];
+    rows += rec[kRows];
+    for (int q = 0; q < 4; ++q) {
+      const int k = (order >> (4 * q)) & 0xF;
+      if (k != 0xF) m = then(m, run_map(k, rec[kCnt + k], a.dh));
+    }
+  }
+  // Hillis-Steele inclusive scan over the threads (identity: a = -1)
+  sb[t] = m.b; sa[t] = m.id ? -1 : m.a; srow[t] = rows;
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  for (int d = 1; d < kScanThreads; d <<= 1) {
+    Place p{0, 0, 1};
+    int pr = 0;
+    if (t >= d) { p = Place{sb[t - d], sa[t - d] < 0 ? 0 : sa[t - d], sa[t - d] < 0}; pr = srow[t - d]; }
+    __syncthreads();
+    if (t >= d) {
+      m = then(p, m);
+      rows += pr;
+      sb[t] = m.b; sa[t] = m.id ? -1 : m.a; srow[t] = rows;
+    }
+    __syncthreads();
+  }
+  // exclusive prefix: the inclusive value of thread t - 1
   int64_t off = 0;
   int row = 0;
-  for (int sh = 0; sh < a.num_sh; ++sh) {
+  if (t > 0) {
+    off = apply(Place{sb[t - 1], sa[t - 1] < 0 ? 0 : sa[t - 1], sa[t - 1] < 0}, 0);
+    row = srow[t - 1];
+  }
+  int ovf = 0;
+  for (int sh = s0; sh < s1; ++sh) {
     int32_t* rec = sh_rec(a, sh);
+    const int order = rec[kOrder];
     rec[kRowStart] = row;
     a.row_start[sh] = row;
     row += rec[kRows];
     for (int q = 0; q < 4; ++q) {
-      const int k = (rec[kOrder] >> (4 * q)) & 0xF;
+      const int k = (order >> (4 * q)) & 0xF;
       if (k == 0xF) { rec[kRunStart + q] = -1; continue; }
-      const int n = rec[kCnt + k], pages = (n + 15) / 16, last = n - 16 * (pages - 1);
       const int64_t start = place(off, k);
-      if (start > 0x7FFFFF00LL) { atomicAdd(a.totals + 3, 1); rec[kRunStart + q] = 0; continue; }
-      rec[kRunStart + q] = (int32_t)start;
-      off = start + (int64_t)(pages - 1) * align16(page_bytes(k, 16, a.dh)) + page_bytes(k, last, a.dh);
+      if (start > kMaxOff) ++ovf;
+      rec[kRunStart + q] = start > kMaxOff ? 0 : (int32_t)start;
+      off = start + run_bytes(k, rec[kCnt + k], a.dh);
     }
   }
-  a.row_start[a.num_sh] = row;
-  const int64_t total = align16(off) + 16;
-  a.totals[0] = row;
-  a.totals[1] = total > 0x7FFFFF00LL ? -1 : (int32_t)total;
+  if (ovf) atomicAdd(&nflag, ovf);
+  __syncthreads();
+  if (t == kScanThreads - 1) {                           // holds the last range (or the full scan)
+    a.row_start[a.num_sh] = row;
+    const int64_t total = align16(off) + 16;
+    a.totals[0] = row;
+    a.totals[1] = total > kMaxOff ? -1 : (int32_t)total;
+    a.totals[2] = nbad;
+    a.totals[3] = nflag;
+  }
 }
 
 __global__ __launch_bounds__(kPlanThreads) void plan_fill_kernel(PlanLaunch a) {
@@ -256,7 +370,7 @@ int launch_plan(const PlanLaunch& L0, int phase, hipStream_t stream) {
   if (grid > 0x7FFFFFFF) return -1;
   if (phase == 0) {
     hipLaunchKernelGGL(plan_count_kernel, dim3((unsigned)grid), dim3(kPlanThreads), 0, stream, L);
-    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, stream, L);
+    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, L);
   } else {
     hipLaunchKernelGGL(plan_fill_kernel, dim3((unsigned)grid), dim3(kPlanThreads), 0, stream, L);
   }

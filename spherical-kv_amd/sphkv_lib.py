@@ -54,6 +54,8 @@ SIGNATURES = {
                                              P, P]),
     "sphkv_build_layer_pool": (ctypes.c_int, [P, P, I64, P, I64, P, I32, I32, P, P, P, P, I64, I32, I32, I32,
                                               P]),
+    "sphkv_work_rows_per_item": (I32, [P, I32, I32, I32]),
+    "sphkv_work_fill": (I64, [P, I32, I32, I32, P, I64, P]),
 }
 
 

@@ -42,67 +42,77 @@ def _need(t: torch.Tensor, dtype, name: str, device=None):
         raise ValueError(f"{name} is on {t.device}, expected {device}")
 
 
+def _row_start32(row_start) -> np.ndarray:
+    """row_start as contiguous int32 (num_sh + 1 rows), checked to fit."""
+    rs = np.asarray(row_start)
+    if rs.ndim != 1 or rs.size < 1:
+        raise ValueError("row_start must be 1-D with num_sh + 1 entries")
+    if rs.dtype != np.int32:
+        if int(rs.min()) < 0 or int(rs.max()) > 2 ** 31 - 1:
+            raise ValueError("row_start entries must lie in [0, 2^31)")
+        rs = rs.astype(np.int32)
+    return np.ascontiguousarray(rs)
+
+
 def auto_rows_per_item(row_start: np.ndarray, num_cus: int, slots_per_cu: int = 1) -> int:
-    """Rows per work item.  When one item per CU can cover every (seq, head)
-    range, the smallest row count whose item total fits num_cus * slots_per_cu
-    (one workgroup per CU, all running at once; at least 8 rows).  When there
-    are more ranges than that (each needs an item of its own), about four
-    smaller items per CU, which the dispatcher balances as CUs free up."""
-    rs = np.asarray(row_start, np.int64)
-    lens = rs[1:] - rs[:-1]
-    total = int(lens.sum())
-    target = max(1, num_cus * slots_per_cu)
-    if total == 0 or lens.size == 0:
-        return 8
+    """Rows per work item (library routine sphkv_work_rows_per_item).  When
+    one item per CU can cover every (seq, head) range, the smallest row count
+    whose item total fits num_cus * slots_per_cu (one workgroup per CU, all
+    running at once; at least 8 rows).  When there are more ranges than that
+    (each needs an item of its own), about four smaller items per CU, which
+    the dispatcher balances as CUs free up."""
+    rs = _row_start32(row_start)
+    r = load().sphkv_work_rows_per_item(rs.ctypes.data, rs.size - 1, int(num_cus), int(slots_per_cu))
+    check(min(r, 0), "sphkv_work_rows_per_item")
+    return int(r)
 
-    def items(r: np.ndarray) -> np.ndarray:        # item totals of candidate row counts r
-        return np.maximum(1, -(-lens[None, :] // r[:, None])).sum(1)
 
-    lo = max(8, -(-total // target))
-    hi = max(lo, int(lens.max()))
-    if items(np.array([hi]))[0] > target:
-        return max(8, -(-total // (4 * target)))
-    # items(r) does not grow with r: narrow [lo, hi] to its first r with
-    # items(r) <= target, 32 evenly spaced candidates per round
-    while hi - lo > 32:
-        r = lo + (np.arange(1, 33, dtype=np.int64) * (hi - lo)) // 32
-        ok = items(r) <= target
-        j = int(np.argmax(ok))                      # the last candidate (hi) always fits
-        lo, hi = (lo if j == 0 else int(r[j - 1]) + 1), int(r[j])
-    r = np.arange(lo, hi + 1, dtype=np.int64)
-    return int(r[int(np.argmax(items(r) <= target))])
+def _work_fill(rs: np.ndarray, rows_per_item: int, interleave: bool, buf_ptr: int, head: int, cap: int) -> int:
+    """Fill work_start at buf_ptr and the work rows `head` int32 further on."""
+    n = load().sphkv_work_fill(rs.ctypes.data, rs.size - 1, int(rows_per_item), int(bool(interleave)),
+                               buf_ptr + 4 * head, cap, buf_ptr)
+    check(min(n, 0), "sphkv_work_fill")
+    return int(n)
+
+
+def _work_capacity(rs: np.ndarray, rows_per_item: int) -> int:
+    # sum_i max(1, ceil(len_i / r)) <= num_sh + floor(total / r)
+    if rows_per_item < 1:
+        raise ValueError("rows_per_item must be >= 1")
+    return rs.size - 1 + (int(rs[-1]) - int(rs[0])) // int(rows_per_item)
 
 
 def make_work(row_start: np.ndarray, rows_per_item: int = ROWS_PER_ITEM, interleave: bool = True):
     """Split each (seq, head) row range [b, e) into n = ceil((e - b) /
     rows_per_item) items of <= rows_per_item rows (an empty range gets one
-    empty item: its output is still written).  Returns (work int32 [n_items,
-    4] = (sh, first_row, end_row, stride), work_start int32 [num_sh + 1]).
+    empty item: its output is still written); library routine
+    sphkv_work_fill.  Returns (work int32 [n_items, 4] = (sh, first_row,
+    end_row, stride), work_start int32 [num_sh + 1]).
 
     interleave (default): item i takes rows b + i, b + i + n, ... -- a head's
     rows are grouped by tier, so contiguous items would each hold one tier and
     run at that tier's cost (dense pages load 4 KB of K more); interleaved
     items all hold the head's tier mix.  Otherwise items are contiguous
     ranges (stride 1)."""
-    rs = np.asarray(row_start, np.int64)
-    b, e = rs[:-1], rs[1:]
-    n = np.maximum(1, -(-(e - b) // rows_per_item))
-    ws = np.concatenate([[0], np.cumsum(n)])
-    sh = np.repeat(np.arange(b.size, dtype=np.int64), n)
-    i = np.arange(int(ws[-1]), dtype=np.int64) - ws[:-1][sh]      # item index within its range
-    if interleave:
-        cols = (sh, b[sh] + i, e[sh], n[sh])
-    else:
-        cols = (sh, b[sh] + i * rows_per_item, np.minimum(e[sh], b[sh] + (i + 1) * rows_per_item),
-                np.ones_like(sh))
-    return np.stack(cols, axis=1).astype(np.int32).reshape(-1, 4), ws.astype(np.int32)
+    rs = _row_start32(row_start)
+    cap = _work_capacity(rs, rows_per_item)
+    head = rs.size
+    buf = np.empty(head + 4 * max(cap, 1), np.int32)
+    n = _work_fill(rs, rows_per_item, interleave, buf.ctypes.data, head, cap)
+    return buf[head:head + 4 * n].reshape(-1, 4).copy(), buf[:head].copy()
 
 
-def _work_tensors(work: np.ndarray, ws: np.ndarray, dev) -> Tuple[torch.Tensor, torch.Tensor]:
-    """The work list and its per-range starts on the device, in one copy."""
-    buf = torch.from_numpy(np.concatenate([work.reshape(-1), ws])).to(dev)
-    n = work.size
-    return buf[:n].view(-1, 4), buf[n:]
+def _work_device(row_start, rows_per_item: int, dev) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The interleaved work list and its per-range starts on the device:
+    filled in pinned host memory and uploaded without a host wait (torch's
+    pinned-memory cache keeps the buffer until the copy has run)."""
+    rs = _row_start32(row_start)
+    cap = _work_capacity(rs, rows_per_item)
+    head = (rs.size + 3) & ~3              # work_start, padded: the work rows start 16-byte aligned
+    buf = torch.empty(head + 4 * max(cap, 1), dtype=torch.int32, pin_memory=True)
+    n = _work_fill(rs, rows_per_item, True, buf.data_ptr(), head, cap)
+    d = buf[:head + 4 * n].to(dev, non_blocking=True)
+    return d[head:].view(-1, 4), d[:rs.size]
 
 
 def validate_plan(plan: fmt.PagePlan) -> None:
@@ -171,7 +181,7 @@ class PagedPool:
         dev = torch.device(device)
         if rows_per_item is None:
             rows_per_item = auto_rows_per_item(plan.row_start, torch.cuda.get_device_properties(dev).multi_processor_count)
-        work, ws = make_work(plan.row_start, rows_per_item)
+        work, work_start = _work_device(plan.row_start, rows_per_item, dev)
         cbs = {int(t): torch.as_tensor(np.ascontiguousarray(c, np.float32), device=dev)
                for t, c in codebooks.items()}
         for tid in np.unique(plan.tier):
@@ -191,7 +201,7 @@ class PagedPool:
             positions=torch.as_tensor(plan.positions, device=dev),
             v_pool=torch.zeros((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
             codebooks=cbs,
-            **dict(zip(("work", "work_start"), _work_tensors(work, ws, dev))),
+            work=work, work_start=work_start,
             tier=torch.as_tensor(plan.tier, device=dev),
             count=torch.as_tensor(plan.count, device=dev),
             seq_head=torch.as_tensor(plan.seq_head, device=dev),
@@ -206,7 +216,7 @@ class PagedPool:
         dev = torch.device(device)
         if rows_per_item is None:
             rows_per_item = auto_rows_per_item(plan.row_start, torch.cuda.get_device_properties(dev).multi_processor_count)
-        work, ws = make_work(plan.row_start, rows_per_item)
+        work, work_start = _work_device(plan.row_start, rows_per_item, dev)
         cbs = {}
         for t, c in codebooks.items():
             if isinstance(c, torch.Tensor) and c.device == dev and c.dtype == torch.float32 and c.is_contiguous():
@@ -222,7 +232,7 @@ class PagedPool:
             plan=plan, pages=torch.zeros(plan.pages_bytes, dtype=torch.uint8, device=dev), ptable=plan.ptable,
             vslot=plan.vslot, positions=plan.positions,
             v_pool=torch.empty((plan.num_vpages, plan.page_size * plan.dh), dtype=torch.float16, device=dev),
-            codebooks=cbs, **dict(zip(("work", "work_start"), _work_tensors(work, ws, dev))),
+            codebooks=cbs, work=work, work_start=work_start,
             tier=plan.tier, count=plan.count, seq_head=plan.seq_head)
 
     def cb_ptrs(self):
@@ -517,15 +527,19 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
     if nw < 0:
         raise ValueError("bad planner sizes")
     work = torch.empty(max(nw, 1), dtype=torch.int32, device=dev)
-    # totals and row_start in one buffer: phase 1 completes both, so one copy
-    # to the host (the planner's only synchronisation) brings back both
-    meta = torch.zeros(4 + num_sh + 1, dtype=torch.int32, device=dev)
+    # totals and row_start in one buffer: phase 1 writes both whole (nothing
+    # when there are no sequences), so one copy to the host (the planner's
+    # only synchronisation) brings back both
+    meta = (torch.empty if num_sh else torch.zeros)(4 + num_sh + 1, dtype=torch.int32, device=dev)
     totals, row_start = meta[:4], meta[4:]
     rc = lib.sphkv_plan_pages_count(tier_of.data_ptr(), tier_of.stride(0), lens.data_ptr(), num_seqs, int(num_kv),
                                     max_len, int(dh), work.data_ptr(), work.numel(), row_start.data_ptr(),
                                     totals.data_ptr(), _stream())
     check(rc, "sphkv_plan_pages_count")
-    meta_h = meta.cpu().numpy()
+    meta_pin = torch.empty(meta.numel(), dtype=torch.int32, pin_memory=True)
+    meta_pin.copy_(meta, non_blocking=True)
+    torch.cuda.current_stream(dev).synchronize()
+    meta_h = meta_pin.numpy()
     rows, nbytes, bad, ovf = (int(x) for x in meta_h[:4])
     if bad:
         raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")

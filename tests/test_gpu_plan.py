@@ -61,6 +61,10 @@ def _check(dp, tier_of, lengths, num_kv, base=None, positions_of=None):
     assert (off[o][1:] >= off[o][:-1] + size[o][:-1]).all(), "pages overlap"
     assert plan.num_rows == 0 or int((off + size).max()) <= plan.pages_bytes
     assert np.unique(plan.vslot).size == plan.num_rows and plan.num_vpages >= plan.num_rows
+    # the placement is the host planner's logical placement, offset for offset
+    host = fmt.plan_pages(tier_of, positions_of, len(lengths), num_kv, plan.dh)
+    assert np.array_equal(plan.ptable, host.ptable) and plan.pages_bytes == host.pages_bytes
+    assert np.array_equal(plan.row_start, host.row_start)
     if base is not None and dp.src_rows is not None:
         tk = plan.tokens
         src = np.where(tk >= 0, tk + base[plan.seq_head][:, None], -1)
@@ -125,3 +129,24 @@ def test_device_planned_pool_matches_the_oracle(gpu):
     err = max_err(got, want)
     log(f"  device-planned pool: decode max abs err {err:.3e}")
     assert err <= 2e-3
+
+
+def test_device_plan_many_ranges_and_many_chunks(gpu):
+    # 1300 (seq, head) ranges: more than the scan's 1024 threads, so threads
+    # place several ranges each; then one head of 140000 tokens: 69 chunks of
+    # 2048, more than one 64-chunk step of the chunk scan
+    rng = np.random.default_rng(11)
+    ids = np.array([0, 1, 2, 3, fmt.DENSE_TIER_ID])
+    num_kv, lengths = 4, [int(x) for x in rng.integers(0, 90, size=325)]
+    tier_of = [rng.choice(ids, size=L).astype(np.int32) for L in lengths for _ in range(num_kv)]
+    t, lens, _ = _device_inputs(tier_of, lengths, num_kv, gpu)
+    base = _row_base(lengths, num_kv)
+    dp = ops.plan_pages_gpu(t, lens, num_kv, 128, row_base=torch.from_numpy(base).to(gpu))
+    log(f"1300 ranges: rows {dp.rows} pool bytes {dp.pages_bytes}")
+    _check(dp, tier_of, lengths, num_kv, base)
+    lengths = [140000]
+    tier_of = [rng.choice(ids, size=lengths[0], p=[0.1, 0.3, 0.3, 0.2, 0.1]).astype(np.int32)]
+    t, lens, _ = _device_inputs(tier_of, lengths, 1, gpu)
+    dp = ops.plan_pages_gpu(t, lens, 1, 64)
+    log(f"140000 tokens: rows {dp.rows} pool bytes {dp.pages_bytes}")
+    _check(dp, tier_of, lengths, 1)

@@ -55,3 +55,63 @@ def test_auto_rows_per_item_with_more_ranges_than_cus_terminates():
     assert r == max(8, -(-int(lens.sum()) // 1024))
     work, ws = ops.make_work(rs, r)
     assert len(work) >= 512
+
+
+def _items(lens, r):
+    return sum(max(1, -(-int(n) // r)) for n in lens)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_auto_rows_per_item_is_the_first_fitting_row_count(seed):
+    # brute force over r: the smallest r >= max(8, ceil(total / target)) whose
+    # item total fits the target, or the many-ranges rule when none does
+    rng = np.random.default_rng(seed)
+    num_sh = int(rng.integers(1, 40))
+    lens = rng.integers(0, 3000, size=num_sh) * (rng.random(num_sh) < 0.9)
+    rs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cus, slots = int(rng.choice([4, 16, 256])), int(rng.integers(1, 3))
+    target, total = cus * slots, int(lens.sum())
+    got = ops.auto_rows_per_item(rs, cus, slots)
+    if total == 0:
+        assert got == 8
+        return
+    lo = max(8, -(-total // target))
+    hi = max(lo, int(lens.max()))
+    if _items(lens, hi) > target:
+        assert got == max(8, -(-total // (4 * target)))
+    else:
+        want = next(r for r in range(lo, hi + 1) if _items(lens, r) <= target)
+        assert got == want
+
+
+@pytest.mark.parametrize("interleave", [True, False])
+def test_make_work_matches_a_loop_restatement(interleave):
+    rng = np.random.default_rng(7)
+    lens = rng.integers(0, 500, size=33)
+    rs = np.concatenate([[5], 5 + np.cumsum(lens)])
+    for rpi in (1, 3, 16, 100, 499, 500, 10 ** 6):
+        work, ws = ops.make_work(rs, rpi, interleave=interleave)
+        want, want_ws = [], []
+        for sh in range(len(lens)):
+            b, e = int(rs[sh]), int(rs[sh + 1])
+            n = max(1, -(-(e - b) // rpi))
+            want_ws.append(len(want))
+            for i in range(n):
+                want.append((sh, b + i, e, n) if interleave else (sh, b + i * rpi, min(e, b + (i + 1) * rpi), 1))
+        want_ws.append(len(want))
+        np.testing.assert_array_equal(work, np.array(want, np.int32).reshape(-1, 4))
+        np.testing.assert_array_equal(ws, np.array(want_ws, np.int32))
+
+
+def test_work_helpers_reject_bad_row_starts():
+    from sphkv_lib import SphkvError
+    with pytest.raises(SphkvError, match="non-decreasing"):
+        ops.make_work(np.array([0, 10, 4]), 8)
+    with pytest.raises(SphkvError, match="non-decreasing"):
+        ops.auto_rows_per_item(np.array([0, 10, 4]), 256)
+    with pytest.raises(ValueError):
+        ops.make_work(np.array([0, 10]), 0)
+    with pytest.raises(ValueError):
+        ops.make_work(np.array([0, 2 ** 31]), 8)
+    work, ws = ops.make_work(np.array([3]), 8)                 # no ranges
+    assert work.shape == (0, 4) and list(ws) == [0]
