@@ -5,7 +5,8 @@
  * Every entry point takes device pointers, plain integer sizes and a HIP
  * stream (hipStream_t passed as void*; NULL = the null stream), launches
  * asynchronously on that stream and returns 0 on success or a negative
- * SPHKV_E* code.  The caller owns every buffer, outputs included, as in the
+ * SPHKV_E* code (the two host-side work-list routines at the end take host
+ * pointers and no stream).  The caller owns every buffer, outputs included, as in the
  * reference (decode_kernel.cu:249-289 writes through the caller's tensors).
  * sphkv_last_error() returns a message for the last failure on the calling
  * thread.

@@ -152,11 +152,28 @@ __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(PlanLaunch a) 
   }
 }
 
+// wave-inclusive scan of (map, rows) over the lanes, by shuffles
+__device__ __forceinline__ void wave_scan_place(Place& m, int& rows, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int lo = __shfl_up((int)(uint32_t)m.b, d, 64), hi = __shfl_up((int)(m.b >> 32), d, 64);
+    const int pa = __shfl_up(m.id ? -1 : m.a, d, 64), pr = __shfl_up(rows, d, 64);
+    if (lane >= d) {
+      const Place p{(int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo), pa < 0 ? 0 : pa, pa < 0};
+      m = then(p, m);
+      rows += pr;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kScanThreads) void plan_scan_kernel(PlanLaunch a) {
-  __shared__ int64_t sb[kScanThreads];
-  __shared__ int sa[kScanThreads], srow[kScanThreads];
+  // per-range summaries kept for the placement when the ranges fit one per thread
+  __shared__ int s_order[kScanThreads], s_rows[kScanThreads], s_cnt[kScanThreads][4];
+  __shared__ int64_t w_b[kScanThreads / 64];
+  __shared__ int w_a[kScanThreads / 64], w_rows[kScanThreads / 64];
   __shared__ int nbad, nflag;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
+  const bool cached = a.num_sh <= kScanThreads;
   if (t == 0) { nbad = 0; nflag = 0; }
   __syncthreads();
   // (1) a wave per (sequence, head): its chunks' exclusive rank bases per
@@ -200,63 +217,74 @@ __global__ __launch_bounds__(kScanThreads) void plan_scan_kernel(PlanLaunch a) {
       for (int k = 0; k < 4; ++k) { rec[kCnt + k] = carry[k]; rec[kFirst + k] = first[k]; }
       rec[kRows] = rows;
       rec[kOrder] = order;
+      if (cached) {
+        s_order[sh] = order;
+        s_rows[sh] = rows;
+        for (int k = 0; k < 4; ++k) s_cnt[sh][k] = carry[k];
+      }
       if (bad) atomicAdd(&nbad, bad);
       if (flag) atomicAdd(&nflag, flag);
     }
   }
   __syncthreads();                                       // the records above are visible to the whole workgroup
-  // (2) placement: thread t takes ranges [s0, s1); its runs composed into one
-  // map, an exclusive block scan of (map, rows), then its runs placed from
-  // the scanned offset
+  // (2) placement: thread t takes ranges [s0, s1) (one each when they fit);
+  // its runs composed into one map, an exclusive scan of (map, rows) over the
+  // threads (shuffles in each wave, then the wave totals), then its runs
+  // placed from the scanned offset
   const int per = (a.num_sh + kScanThreads - 1) / kScanThreads;
   const int s0 = min(t * per, a.num_sh), s1 = min(s0 + per, a.num_sh);
+  auto summary = [&](int sh, int& order, int& rows, int (&cnt)[4]) {
+    if (cached) {
+      order = s_order[sh]; rows = s_rows[sh];
+      for (int k = 0; k < 4; ++k) cnt[k] = s_cnt[sh][k];
+    } else {
+      const int32_t* rec = sh_rec(a, sh);
+      order = rec[kOrder]; rows = rec[kRows];
+      for (int k = 0; k < 4; ++k) cnt[k] = rec[kCnt + k];
+    }
+  };
   Place m{0, 0, 1};
   int rows = 0;
   for (int sh = s0; sh < s1; ++sh) {
-    const int32_t* rec = sh_rec(a, sh);
-    const int order = rec[kOrder];
-    rows += rec[kRows];
+    int order, nr, cnt[4];
+    summary(sh, order, nr, cnt);
+    rows += nr;
     for (int q = 0; q < 4; ++q) {
       const int k = (order >> (4 * q)) & 0xF;
-      if (k != 0xF) m = then(m, run_map(k, rec[kCnt + k], a.dh));
+      if (k != 0xF) m = then(m, run_map(k, cnt[k], a.dh));
     }
   }
-  // Hillis-Steele inclusive scan over the threads (identity: a = -1)
-  sb[t] = m.b; sa[t] = m.id ? -1 : m.a; srow[t] = rows;
+  wave_scan_place(m, rows, lane);
+  if (lane == 63) { w_b[wave] = m.b; w_a[wave] = m.id ? -1 : m.a; w_rows[wave] = rows; }
+  // this thread's exclusive value within its wave: lane - 1's inclusive one
+  const int lo = __shfl_up((int)(uint32_t)m.b, 1, 64), hi = __shfl_up((int)(m.b >> 32), 1, 64);
+  const int pa = __shfl_up(m.id ? -1 : m.a, 1, 64), pr = __shfl_up(rows, 1, 64);
   __syncthreads();
-  for (int d = 1; d < kScanThreads; d <<= 1) {
-    Place p{0, 0, 1};
-    int pr = 0;
-    if (t >= d) { p = Place{sb[t - d], sa[t - d] < 0 ? 0 : sa[t - d], sa[t - d] < 0}; pr = srow[t - d]; }
-    __syncthreads();
-    if (t >= d) {
-      m = then(p, m);
-      rows += pr;
-      sb[t] = m.b; sa[t] = m.id ? -1 : m.a; srow[t] = rows;
-    }
-    __syncthreads();
-  }
-  // exclusive prefix: the inclusive value of thread t - 1
   int64_t off = 0;
   int row = 0;
-  if (t > 0) {
-    off = apply(Place{sb[t - 1], sa[t - 1] < 0 ? 0 : sa[t - 1], sa[t - 1] < 0}, 0);
-    row = srow[t - 1];
+  for (int w = 0; w < wave; ++w) {                       // the earlier waves' totals, in order
+    off = apply(Place{w_b[w], w_a[w] < 0 ? 0 : w_a[w], w_a[w] < 0}, off);
+    row += w_rows[w];
+  }
+  if (lane > 0) {
+    off = apply(Place{(int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo), pa < 0 ? 0 : pa, pa < 0}, off);
+    row += pr;
   }
   int ovf = 0;
   for (int sh = s0; sh < s1; ++sh) {
+    int order, nr, cnt[4];
+    summary(sh, order, nr, cnt);
     int32_t* rec = sh_rec(a, sh);
-    const int order = rec[kOrder];
     rec[kRowStart] = row;
     a.row_start[sh] = row;
-    row += rec[kRows];
+    row += nr;
     for (int q = 0; q < 4; ++q) {
       const int k = (order >> (4 * q)) & 0xF;
       if (k == 0xF) { rec[kRunStart + q] = -1; continue; }
       const int64_t start = place(off, k);
       if (start > kMaxOff) ++ovf;
       rec[kRunStart + q] = start > kMaxOff ? 0 : (int32_t)start;
-      off = start + run_bytes(k, rec[kCnt + k], a.dh);
+      off = start + run_bytes(k, cnt[k], a.dh);
     }
   }
   if (ovf) atomicAdd(&nflag, ovf);
