@@ -71,7 +71,9 @@ def test_page_header_and_sections():
     assert rc[:, 1].tolist() == [0, 0, 0]
 
 
-def test_page_sizes_match_survey():
+def test_page_sizes_match_the_pagebuilder_layout():
+    # header 8 B + G fp32 scales + ceil(16 G b / 8) code bytes + 16 G int8 radii
+    # (pagebuilder.py:8-33): tier 1 at dh 128 is 8 + 32 + 96 + 128 = 264
     assert fmt.page_nbytes(1, 16, 128) == 264
     assert fmt.page_nbytes(2, 16, 128) == 232
     assert fmt.page_nbytes(3, 16, 128) == 112
