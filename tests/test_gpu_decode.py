@@ -144,7 +144,7 @@ def test_decode_edge_cases(gpu):
     assert max_err(got[0, :gqa], np.broadcast_to(V[0][0, 0].astype(np.float32), (gqa, dh))) == 0.0
 
 
-@pytest.mark.parametrize("dh,gqa", [(128, 4), (64, 1), (128, 2), (128, 8)])
+@pytest.mark.parametrize("dh,gqa", [(128, 4), (64, 1), (128, 2), (128, 8), (128, 1), (64, 2), (64, 4), (64, 8)])
 def test_decode_partial_and_far_pages(gpu, dh, gqa):
     # Every tier with a partial last page (250 tokens: 15 full pages + 10);
     # pages whose tokens lie 10 positions apart (|pos - centre| up to 75: the
