@@ -20,7 +20,9 @@ Prints one JSON line (see the "roofline" and "cpu_baseline" objects).
 `--path modea` measures the Mode-A (LayerPool) decode instead, on the same
 attention shape with unpacked uint8 pools (fused_decode.sphkv_decode);
 `--path prefill` measures prefill paging of the same layer on the GPU (device
-page plan + fused encode / bitpack / V placement).  The default line is the
+page plan + fused encode / bitpack / V placement); `--path ragged` measures
+fused_decode_ragged (logits only) over the same layer's tier-1 and tier-2
+pages.  The default line is the
 angle-domain (Mode-B) decode above.
 """
 from __future__ import annotations
@@ -303,6 +305,87 @@ def bench_modea(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_ragged(args, dev):
+    """fused_decode_ragged (logits only, the reference's tiered call,
+    spherical_kv_pipeline.py:1860-1875): one step = one call per compressed
+    tier over config 2's pages of that tier, all kv heads.  Algorithmic bytes
+    per call: the tier's pages, positions and logits plus the cos / sin rows
+    (first halves) of the distinct positions.  CPU baseline: the oracle's fp64
+    restatement on a bounded sample of pages, scaled by page count."""
+    import fused_decode
+    import oracle
+    log("[bench] building config2 workload for fused_decode_ragged")
+    wl = synth.make_decode_workload(2)
+    pool, _, _ = ops.build_pool_gpu(wl, dev)
+    plan = wl.plan
+    cos_h, sin_h = fmt.rope_tables(max(wl.lengths) + 16, wl.dh, wl.rope_theta)
+    cos_t, sin_t = torch.as_tensor(cos_h, device=dev), torch.as_tensor(sin_h, device=dev)
+    q_h = wl.q[0].astype(np.float32)
+    q = torch.as_tensor(q_h, device=dev)
+    calls, host, nbytes, npages = [], [], 0, 0
+    for tid in (1, 2):
+        g, b = fmt.TIER_GEOMETRY[tid]
+        G = wl.dh // g
+        rows = np.nonzero(plan.tier == tid)[0]
+        heads = (plan.seq_head[rows] % plan.num_kv).astype(np.int32)
+        pos = plan.positions[rows].reshape(-1).astype(np.int32)
+        cb = wl.codebooks[tid].reshape(plan.num_kv * G, 2 ** b, g)
+        calls.append((pool.pages, torch.as_tensor(plan.ptable[rows], device=dev), torch.as_tensor(heads, device=dev),
+                      torch.as_tensor(pos, device=dev), cos_t, sin_t, q, wl.gqa, plan.num_kv,
+                      torch.as_tensor(cb, device=dev), wl.dh, G, g, b, 16))
+        host.append((rows, heads, pos, cb, G, g, b))
+        n_tok = int((pos >= 0).sum())
+        nbytes += (int(sum(fmt.page_nbytes(tid, int(n), wl.dh) for n in plan.count[rows])) + 4 * pos.size
+                   + 4 * wl.gqa * pos.size + 2 * 4 * (wl.dh // 2) * int(np.unique(pos[pos >= 0]).size))
+        npages += rows.size
+        log(f"[bench] tier {tid}: {rows.size} pages, {n_tok} tokens")
+
+    def step(i):
+        for c in calls:
+            fused_decode.fused_decode_ragged(*c)
+
+    settle(step)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] fused_decode_ragged {ms * 1e3:.2f} us per step (tiers 1 + 2)  {gbps:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        pages_h = pool.pages.cpu().numpy()
+        t0, done = time.perf_counter(), 0
+        for rows, heads, pos, cb, G, g, b in host:
+            k = min(rows.size, 150)
+            oracle.ragged_logits(pages_h, plan.ptable[rows[:k]], heads[:k], pos[:16 * k], cos_h, sin_h, q_h, wl.gqa,
+                                 cb, wl.dh, G, g, b, 16)
+            done += k
+        sec = time.perf_counter() - t0
+        cpu = {"value": round(sec / done * npages * 1e6, 1), "unit": "µs per step (extrapolated by pages)",
+               "cores": 1, "kind": "port",
+               "sample": f"{done} of {npages} pages (150 per tier); oracle.ragged_logits, fp64 numpy"}
+        log(f"[bench] CPU {cpu['value']} us per step")
+    line = {
+        "metric": "µs per fused_decode_ragged step (tier 1 + tier 2 logits), 8B shape, 32K ctx, 1 GPU",
+        "value": round(ms * 1e3, 3), "unit": "µs/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8 codes, fp32 tables and math", "data": "synthetic (config 2 spec of BASELINE.json)",
+        "config": {"workload": "config2 tier-1 and tier-2 pages (16 tokens), 8 kv heads, grp 4, dh 128",
+                   "pages": int(npages), "algorithmic_bytes_per_step": int(nbytes)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": "ragged_fast_kernel",
+                     "kernel_us": round(ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_prefill(args, dev):
     """One step = page one layer's retained K/V: device plan
     (plan_pages_gpu, including its one host synchronisation) + fused encode
@@ -407,7 +490,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
                     help="page placement: the config's own (random for configs 2-5) or sequential")
-    ap.add_argument("--path", default="modeb", choices=["modeb", "modea", "prefill"],
+    ap.add_argument("--path", default="modeb", choices=["modeb", "modea", "prefill", "ragged"],
                     help="modeb: the angle-domain paged decode (the headline); modea: LayerPool decode; "
                          "prefill: device page plan + fused encode")
     ap.add_argument("--page-size", type=int, default=16, help="Mode-A page size (16..128, multiple of 16)")
@@ -430,6 +513,9 @@ def main():
         return
     if args.path == "prefill":
         bench_prefill(args, dev)
+        return
+    if args.path == "ragged":
+        bench_ragged(args, dev)
         return
     if args.config == 3:
         print("bench.py: config 3 is the encode workload; use --path prefill --config 3", file=sys.stderr)

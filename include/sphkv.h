@@ -132,7 +132,8 @@ int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32
  *              [num_seqs*num_kv + 1] = first item of each (seq, head).
  *   q          fp16 [num_seqs, num_kv*gqa, dh];  out fp16, same shape.
  *   workspace  device scratch of sphkv_decode_paged_workspace_bytes() bytes.
- * gqa in {1, 2, 4, 8}; dh in {64, 128}; page_size == 16.
+ * gqa in {1, 2, 4, 8}; dh in {64, 128}; page_size == 16; pages_bytes a
+ * multiple of 4 (the pool is read in dwords: pad a back-to-back pool).
  */
 int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
                        const int32_t* vslot, const int32_t* positions, int32_t num_rows,

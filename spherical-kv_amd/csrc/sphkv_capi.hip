@@ -131,6 +131,10 @@ int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_
   if ((phases & sphkv::kPhasePartials) &&
       (pages_bytes < 0 || pages_bytes > 0x7FFFFF00LL || (int64_t)num_rows * 64 > 0x7FFFFF00LL))
     return fail(SPHKV_EINVAL, "%s: byte pool and pointer table must stay below 2 GiB", fn);
+  // the kernel reads the pool in dwords, and a buffer load returns zero for a
+  // dword that reaches past the pool's end
+  if ((phases & sphkv::kPhasePartials) && (pages_bytes & 3))
+    return fail(SPHKV_EINVAL, "%s: pages_bytes must be a multiple of 4 (pad the byte pool)", fn);
   // V pages are addressed with 64-bit offsets; vslot is int32, so a larger
   // pool could not be indexed in full
   if ((phases & sphkv::kPhasePartials) && (num_vpages < 0 || num_vpages > (int64_t)1 << 31))

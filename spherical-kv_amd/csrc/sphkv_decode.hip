@@ -1100,9 +1100,168 @@ __global__ __launch_bounds__(256) void ragged_logits_kernel(RaggedLaunch a) {
   }
 }
 
+// Fast form of the ragged kernel for page_size % 16 == 0, group size 16 or
+// 32 and grp <= 8 (the reference's call shapes).  One wave per 16 slots of a
+// page; lane = (slot t, dim quarter u) as in the decode kernel: the lane
+// rebuilds its token's key on its quarter's RoPE pairs (j, j + DH/2), j in
+// [DH/8 u, DH/8 (u + 1)), from two codes, two int8 radii, two fp32 scales and
+// two centroid runs, rotates it with the caller's cos / sin rows at the
+// token's position (first-half entries, HF layout), and the q.k sums run on
+// the fp32 4x4x1 MFMA (A = q of head slot t mod 4, B = the lane's own rotated
+// key; blocks = (quarter, token group)), then over the quarters with the row
+// swaps.  The loads form three round trips: the pointer-table row, head id
+// and positions; then the page's bytes (read whatever the token count says
+// -- the count only masks the output), the cos / sin rows and q; then the
+// centroid runs.  Page bytes are read with buffer loads (absent data reads
+// zeros; a buffer load returns zero for a dword that reaches past the pool,
+// so the pool's partial last dword is read once bytewise and substituted).
+// A page's validity rules are those of ragged_logits_kernel.
+template <int DH, int GS, int NHS>
+__global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
+  constexpr int NPL = DH / 8;                          // RoPE pairs per lane
+  constexpr int G = DH / GS;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cpp = a.page_size / 16;                    // 16-slot chunks per page
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + wave;
+  if (chunk >= (int64_t)a.num_pages * cpp) return;
+  const int p = uniform((int)(chunk / cpp)), c16 = uniform((int)(chunk % cpp));
+  const int t = lane & 15, u = lane >> 4, ts = 16 * c16 + t;
+  // round trip 1: the row, the head, the positions
+  const int64_t page_off = a.ptable[3 * (int64_t)p], th_off = a.ptable[3 * (int64_t)p + 1],
+                rad_off = a.ptable[3 * (int64_t)p + 2];
+  const int hk = a.head_ids[p];
+  const int pos_raw = a.positions[(int64_t)p * a.page_size + ts];
+  const int b = a.b_theta, C = 1 << b;
+  const rsrc_t rs = make_rsrc(a.pages, a.pages_bytes);
+  const int64_t pb = a.pages_bytes > 0x7FFFFFFF ? 0x7FFFFFFF : a.pages_bytes;
+  const int tail4 = (int)(pb & ~(int64_t)3);
+  // offsets inside the pool or kOOB (the validity checks come later)
+  auto in_pool = [&](int64_t o) { return (o >= 0 && o < pb) ? (int)o : kOOB; };
+  // round trip 2: count byte, the pool's partial last dword, codes, radii,
+  // scales; cos / sin at the position; q of the lane's head slots
+  const bool hdr_ok = page_off >= 0 && page_off + 2 <= a.pages_bytes;
+  const int cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(page_off + 1), 0, 0);
+  uint32_t tailw = 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? tail4 + i : kOOB, 0, 0) << (8 * i);
+  auto dword_at = [&](int64_t o4) {                    // o4: a multiple of 4 (or negative)
+    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
+    return o4 == tail4 ? tailw : w;
+  };
+  const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
+  const int gg[2] = {gi, gj};
+  uint32_t cwin[2][2], swin[2][2];
+  int rcode[2];
+  int64_t cbit[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    cbit[k] = th_off * 8 + (int64_t)(ts * G + gg[k]) * b;
+    const int64_t o4 = (cbit[k] >> 5) * 4;
+    cwin[k][0] = dword_at(o4);
+    cwin[k][1] = dword_at(o4 + 4);
+    rcode[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(rad_off + ts * G + gg[k]), 0, 0);
+    const int64_t so = page_off + kHeaderBytes + 4 * gg[k];
+    const int64_t s4 = so >= 0 ? (so >> 2) * 4 : -4;
+    swin[k][0] = dword_at(s4);
+    swin[k][1] = dword_at(s4 + 4);
+  }
+  const bool pos_ok = pos_raw >= 0 && pos_raw < a.max_pos;
+  const int pos = pos_ok ? pos_raw : 0;
+  const bool head_ok = hk >= 0 && hk < a.num_kv;
+  const int hq = head_ok ? hk : 0;
+  const float* cs = a.cos_tbl + (int64_t)pos * DH + d0;
+  const float* sn = a.sin_tbl + (int64_t)pos * DH + d0;
+  float4 cc[NPL / 4], ss[NPL / 4], q0[NHS][NPL / 4], q1[NHS][NPL / 4];
+#pragma unroll
+  for (int m = 0; m < NPL / 4; ++m) {
+    cc[m] = *reinterpret_cast<const float4*>(cs + 4 * m);
+    ss[m] = *reinterpret_cast<const float4*>(sn + 4 * m);
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) {
+      const int slot = 4 * hs + (t & 3);
+      const bool q_ok = slot < a.grp;
+      const float* qr = a.q + ((int64_t)hq * a.grp + (q_ok ? slot : 0)) * DH + d0 + 4 * m;
+      q0[hs][m] = q_ok ? *reinterpret_cast<const float4*>(qr) : float4{0.f, 0.f, 0.f, 0.f};
+      q1[hs][m] = q_ok ? *reinterpret_cast<const float4*>(qr + DH / 2) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // validity (ragged_logits_kernel's rules)
+  int n = hdr_ok ? min(cnt, a.page_size) : 0;
+  if (page_off + kHeaderBytes + 4 * G > a.pages_bytes || th_off < 0 || rad_off < 0 ||
+      th_off + ((int64_t)n * G * b + 7) / 8 > a.pages_bytes || rad_off + (int64_t)n * G > a.pages_bytes)
+    n = 0;
+  const bool valid = ts < n && pos_ok && head_ok;
+  // round trip 3: the centroid runs of the two codes
+  int code[2];
+  float rad[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    code[k] = (int)(__builtin_amdgcn_alignbit(cwin[k][1], cwin[k][0], (uint32_t)(cbit[k] & 31)) & (uint32_t)(C - 1));
+    const int64_t so = page_off + kHeaderBytes + 4 * gg[k];
+    const float sc = __builtin_bit_cast(float, __builtin_amdgcn_alignbyte(swin[k][1], swin[k][0], (uint32_t)(so & 3)));
+    rad[k] = (float)rcode[k] * sc * (1.0f / 127.0f);
+  }
+  const float* c1 = a.codebooks + ((int64_t)(hq * G + gi) * C + code[0]) * GS + off;
+  const float* c2 = a.codebooks + ((int64_t)(hq * G + gj) * C + code[1]) * GS + off;
+  floatx4 acc[NHS];
+#pragma unroll
+  for (int hs = 0; hs < NHS; ++hs) acc[hs] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < NPL / 4; ++m) {
+    const float4 cv1 = *reinterpret_cast<const float4*>(c1 + 4 * m);
+    const float4 cv2 = *reinterpret_cast<const float4*>(c2 + 4 * m);
+    const float k1[4] = {rad[0] * cv1.x, rad[0] * cv1.y, rad[0] * cv1.z, rad[0] * cv1.w};
+    const float k2[4] = {rad[1] * cv2.x, rad[1] * cv2.y, rad[1] * cv2.z, rad[1] * cv2.w};
+    const float co[4] = {cc[m].x, cc[m].y, cc[m].z, cc[m].w}, si[4] = {ss[m].x, ss[m].y, ss[m].z, ss[m].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x0 = k1[e] * co[e] - k2[e] * si[e];
+      const float x1 = k2[e] * co[e] + k1[e] * si[e];
+#pragma unroll
+      for (int hs = 0; hs < NHS; ++hs) {
+        const float4 qa4 = q0[hs][m], qb4 = q1[hs][m];
+        const float qa = e == 0 ? qa4.x : e == 1 ? qa4.y : e == 2 ? qa4.z : qa4.w;
+        const float qb = e == 0 ? qb4.x : e == 1 ? qb4.y : e == 2 ? qb4.z : qb4.w;
+        acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa, x0, acc[hs], 0, 0, 0);
+        acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qb, x1, acc[hs], 0, 0, 0);
+      }
+    }
+  }
+  // lane (t, u): acc[hs][i] = head slot 4 hs + i over quarter u's pairs.  Sum
+  // over the quarters so that lane u ends with head slot 4 hs + u
+  const int64_t total_slots = (int64_t)a.num_pages * a.page_size;
+  const float inv = 1.0f / __builtin_sqrtf((float)DH);
+#pragma unroll
+  for (int hs = 0; hs < NHS; ++hs) {
+    float s0 = acc[hs][0], s2 = acc[hs][2], s1 = acc[hs][1], s3 = acc[hs][3];
+    swap32(s0, s2);                                    // lower rows: slot 0 pair, upper: slot 2 pair
+    swap32(s1, s3);
+    float x = s0 + s2, y = s1 + s3;
+    swap16(x, y);                                      // even rows: slots 0 / 2, odd: 1 / 3
+    const float v = x + y;
+    const int i = 4 * hs + u;
+    if (i < a.grp)
+      a.logits_out[(int64_t)i * total_slots + (int64_t)p * a.page_size + ts] = valid ? v * inv : -INFINITY;
+  }
+}
+
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
-  if (L.num_pages > 0)
+  if (L.num_pages <= 0) return 0;
+  const bool fast = L.page_size % 16 == 0 && (L.group_size == 16 || L.group_size == 32) && L.grp <= 8 &&
+                    L.groups * L.group_size == L.dh;
+  if (fast) {
+    const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
+    const dim3 grid((unsigned)((chunks + 3) / 4));
+#define SPHKV_RAGGED(D, S, N) \
+    if (L.dh == D && L.group_size == S && (L.grp > 4) == (N == 2)) \
+      hipLaunchKernelGGL((ragged_fast_kernel<D, S, N>), grid, dim3(256), 0, stream, L);
+    SPHKV_RAGGED(128, 16, 1) SPHKV_RAGGED(128, 16, 2) SPHKV_RAGGED(128, 32, 1) SPHKV_RAGGED(128, 32, 2)
+    SPHKV_RAGGED(64, 16, 1) SPHKV_RAGGED(64, 16, 2) SPHKV_RAGGED(64, 32, 1) SPHKV_RAGGED(64, 32, 2)
+#undef SPHKV_RAGGED
+  } else {
     hipLaunchKernelGGL(ragged_logits_kernel, dim3((L.num_pages + 3) / 4), dim3(256), 0, stream, L);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

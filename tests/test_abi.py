@@ -74,6 +74,7 @@ def _decode_args(**kw):
     (dict(gqa=3), "gqa must be"),
     (dict(page_size=32), "page_size must be 16"),
     (dict(rope_theta=1.0), "rope_theta"),
+    (dict(pages_bytes=1970), "multiple of 4"),
     (dict(num_items=8), "workspace too small"),
     (dict(num_items=4, workspace_bytes=10 ** 9), "at least one work item"),
     (dict(num_items=16, workspace_bytes=10 ** 9, work_start=None), "null pointer"),

@@ -239,15 +239,18 @@ def test_ragged_logits_matches_oracle(gpu):
         assert max_err(got[fin], want[fin]) < 2e-4
 
 
-@pytest.mark.parametrize("tid,page_size,dh", [(1, 128, 128), (3, 128, 128), (3, 16, 128), (2, 128, 64)])
-def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh):
+@pytest.mark.parametrize("tid,page_size,dh,grp", [(1, 128, 128, 4), (3, 128, 128, 4), (3, 16, 128, 4), (2, 128, 64, 4),
+                                                  (1, 16, 128, 8), (3, 32, 64, 6), (2, 48, 128, 1), (1, 16, 64, 3),
+                                                  (1, 24, 128, 4), (2, 128, 128, 9)])
+def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, grp):
     # the reference's call shape: PAGE_SIZE = 128 pages (config.py:4,
     # spherical_kv_pipeline.py:1109-1125) and tier-3 decode pages (:1900-1910);
-    # pages laid out back to back as _build_per_head_pages does (:1198-1213)
+    # pages laid out back to back as _build_per_head_pages does (:1198-1213).
+    # page_size 24 and grp 9 take the general kernel, the rest the fast one.
     import fused_decode
     from oracle import paging
-    rng = np.random.default_rng(700 + tid + page_size + dh)
-    num_kv, grp, L = 2, 4, 300
+    rng = np.random.default_rng(700 + tid + page_size + dh + grp)
+    num_kv, L = 2, 300
     g, b = fmt.TIER_GEOMETRY[tid]
     G = dh // g
     cbs = synth.make_codebooks(rng, num_kv, dh, [tid])[tid]
@@ -277,7 +280,7 @@ def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh):
     cos_t, sin_t = fmt.rope_tables(4100, dh, 500000.0)
     q = rng.standard_normal((num_kv * grp, dh)).astype(np.float32)
     cb = cbs.reshape(num_kv * G, 2 ** b, g)
-    log(f"ragged tier {tid}, page_size {page_size}, dh {dh}: {ptable.shape[0]} pages")
+    log(f"ragged tier {tid}, page_size {page_size}, dh {dh}, grp {grp}: {ptable.shape[0]} pages")
     got = fused_decode.fused_decode_ragged(
         torch.as_tensor(pages, device=gpu), torch.as_tensor(ptable, device=gpu), torch.as_tensor(heads, device=gpu),
         torch.as_tensor(pos, device=gpu), torch.as_tensor(cos_t, device=gpu), torch.as_tensor(sin_t, device=gpu),
