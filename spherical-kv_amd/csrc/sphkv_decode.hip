@@ -1028,6 +1028,7 @@ int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream) {
 // One wave per page; lane = (slot t, dim quarter u); pages of one tier; RoPE
 // from the caller's HF-layout tables; fp32 VALU dot products with every q head
 // of the page's kv head.  Slots are processed 16 at a time.
+template <int DH>
 __global__ __launch_bounds__(256) void ragged_logits_kernel(RaggedLaunch a) {
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -1037,7 +1038,7 @@ __global__ __launch_bounds__(256) void ragged_logits_kernel(RaggedLaunch a) {
   const int64_t page_off = a.ptable[3 * p];
   const int64_t th_off = a.ptable[3 * p + 1];
   const int64_t rad_off = a.ptable[3 * p + 2];
-  const int G = a.groups, g = a.group_size, b = a.b_theta, dh = a.dh;
+  const int G = a.groups, g = a.group_size, b = a.b_theta, dh = DH;
   int n = (page_off >= 0 && page_off + 2 <= a.pages_bytes) ? (int)a.pages[page_off + 1] : 0;
   if (n > a.page_size) n = a.page_size;
   if (page_off + kHeaderBytes + 4 * G > a.pages_bytes || th_off < 0 || rad_off < 0 ||
@@ -1045,8 +1046,8 @@ __global__ __launch_bounds__(256) void ragged_logits_kernel(RaggedLaunch a) {
     n = 0;
   const int C = 1 << b;
   const int hk = a.head_ids[p];
-  const int dq = dh / 4;               // dims per lane
-  const int half_dh = dh / 2;
+  constexpr int dq = DH / 4;           // dims per lane
+  constexpr int half_dh = DH / 2;
   const int64_t total_slots = (int64_t)a.num_pages * a.page_size;
   for (int t0 = 0; t0 < a.page_size; t0 += 16) {
     const int t = t0 + t16;
@@ -1054,7 +1055,7 @@ __global__ __launch_bounds__(256) void ragged_logits_kernel(RaggedLaunch a) {
     const int pos = in_page ? a.positions[(int64_t)p * a.page_size + t] : -1;
     const bool valid = in_page && t < n && pos >= 0 && pos < a.max_pos && hk >= 0 && hk < a.num_kv;
     // lane covers RoPE pairs j = u*dq/2 .. +dq/2 of the first half and their partners
-    float kr[64];
+    float kr[DH / 4];
     const int j0 = u * (dq / 2);
     for (int jj = 0; jj < dq / 2; ++jj) {
       float x0 = 0.f, x1 = 0.f;
@@ -1260,7 +1261,10 @@ int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
     SPHKV_RAGGED(64, 16, 1) SPHKV_RAGGED(64, 16, 2) SPHKV_RAGGED(64, 32, 1) SPHKV_RAGGED(64, 32, 2)
 #undef SPHKV_RAGGED
   } else {
-    hipLaunchKernelGGL(ragged_logits_kernel, dim3((L.num_pages + 3) / 4), dim3(256), 0, stream, L);
+    if (L.dh == 128)
+      hipLaunchKernelGGL(ragged_logits_kernel<128>, dim3((L.num_pages + 3) / 4), dim3(256), 0, stream, L);
+    else
+      hipLaunchKernelGGL(ragged_logits_kernel<64>, dim3((L.num_pages + 3) / 4), dim3(256), 0, stream, L);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
