@@ -536,10 +536,7 @@ def plan_pages_gpu(tier_of: torch.Tensor, lens: torch.Tensor, num_kv: int, dh: i
                                     max_len, int(dh), work.data_ptr(), work.numel(), row_start.data_ptr(),
                                     totals.data_ptr(), _stream())
     check(rc, "sphkv_plan_pages_count")
-    meta_pin = torch.empty(meta.numel(), dtype=torch.int32, pin_memory=True)
-    meta_pin.copy_(meta, non_blocking=True)
-    torch.cuda.current_stream(dev).synchronize()
-    meta_h = meta_pin.numpy()
+    meta_h = meta.cpu().numpy()
     rows, nbytes, bad, ovf = (int(x) for x in meta_h[:4])
     if bad:
         raise ValueError(f"{bad} tokens carry a tier id outside {{0, 1, 2, 3, 0xFF}}")
