@@ -1148,7 +1148,7 @@ __global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
     tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? tail4 + i : kOOB, 0, 0) << (8 * i);
   auto dword_at = [&](int64_t o4) {                    // o4: a multiple of 4 (or negative)
     const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
-    return o4 == tail4 ? tailw : w;
+    return w | (o4 == tail4 ? tailw : 0u);             // the partial dword itself reads as zero
   };
   const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
   const int gg[2] = {gi, gj};
@@ -1247,11 +1247,251 @@ __global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
   }
 }
 
+// Pipelined form of the ragged kernel (same shapes as ragged_fast_kernel,
+// plus C <= 64 and q of every head within 32 KB): a persistent workgroup of
+// four waves takes a contiguous run of iterations, each iteration 4
+// consecutive 16-slot chunks (one per wave).  q of every head is staged in
+// LDS once, and the codebook of the head of each iteration's first chunk is
+// staged when that head changes (pages arrive grouped by head).  Per wave,
+// the loads of chunk i + 2's pointer-table row, head ids and positions, and
+// of chunk i + 1's page bytes and cos / sin rows, are in flight while chunk i
+// is computed (vector loads only: scalar loads share a wait counter with the
+// LDS reads and return out of order, so a wait for LDS data would wait for
+// them too).  The arithmetic per chunk is ragged_fast_kernel's.
+struct RagRow {          // round trip 1 of one chunk
+  uint32_t w0, w1, w2;   // pointer-table row (page_off, th_off, rad_off)
+  int hk, hb, pos;       // head of the chunk's page, head of the iteration's first chunk, slot position
+};
+struct RagPage {         // round trip 2 of one chunk, with its row's fields
+  uint32_t cnt, cw[2][2], sw[2][2];
+  int rc[2];
+  int page_off, th_off, rad_off, hk, hb, pos;
+};
+
+template <int DH, int GS, int NHS>
+__global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
+  constexpr int NPL = DH / 8, NM = NPL / 4;
+  constexpr int G = DH / GS;
+  extern __shared__ float rag_smem[];
+  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+  const int t = lane & 15, u = lane >> 4;
+  const int cpp = a.page_size / 16;
+  const int64_t nch = (int64_t)a.num_pages * cpp;
+  const int64_t niter = (nch + 3) / 4;
+  const int64_t per = (niter + gridDim.x - 1) / gridDim.x;
+  const int64_t it0 = (int64_t)blockIdx.x * per, it1 = min(it0 + per, niter);
+  if (it0 >= it1) return;                              // whole workgroup
+  const int b = a.b_theta, C = 1 << b;
+  const int nq = a.num_kv * a.grp;
+  float* q_s = rag_smem;                               // [num_kv * grp][DH]
+  float* cb_s = rag_smem + nq * DH;                    // [G][C][GS] of the staged head
+  const rsrc_t rs = make_rsrc(a.pages, a.pages_bytes);
+  const rsrc_t rt = make_rsrc(a.ptable, (int64_t)a.num_pages * 12);
+  const rsrc_t rh = make_rsrc(a.head_ids, (int64_t)a.num_pages * 4);
+  const rsrc_t rp = make_rsrc(a.positions, (int64_t)a.num_pages * a.page_size * 4);
+  const rsrc_t rcb = make_rsrc(a.codebooks, (int64_t)a.num_kv * G * C * GS * 4);
+  const int64_t pb = a.pages_bytes > 0x7FFFFFFF ? 0x7FFFFFFF : a.pages_bytes;
+  const int tail4 = (int)(pb & ~(int64_t)3);
+  uint32_t tailw = 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? tail4 + i : kOOB, 0, 0) << (8 * i);
+  for (int i = threadIdx.x; i < nq * DH / 4; i += 256)
+    reinterpret_cast<float4*>(q_s)[i] = reinterpret_cast<const float4*>(a.q)[i];
+  const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
+
+  auto row_of = [&](int64_t it) {                      // issue round trip 1 of this wave's chunk of iteration it
+    RagRow r;
+    const int64_t ch = 4 * it + wave, ch0 = 4 * it;
+    const bool act = it < it1 && ch < nch;
+    const int p = act ? (int)(ch / cpp) : 0, c16 = act ? (int)(ch % cpp) : 0;
+    const int p0 = it < it1 ? (int)(ch0 / cpp) : 0;
+    // unconditional loads (absent ones read zeros): a branch around a load
+    // would make the compiler's waits for the loads in flight conservative
+    const auto w = __builtin_amdgcn_raw_buffer_load_b96(rt, act ? 12 * p : kOOB, 0, 0);
+    r.w0 = (uint32_t)w[0]; r.w1 = (uint32_t)w[1]; r.w2 = (uint32_t)w[2];
+    r.hk = (int)__builtin_amdgcn_raw_buffer_load_b32(rh, act ? 4 * p : kOOB, 0, 0);
+    r.hb = (int)__builtin_amdgcn_raw_buffer_load_b32(rh, it < it1 ? 4 * p0 : kOOB, 0, 0);
+    r.pos = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, act ? 4 * (p * a.page_size + 16 * c16 + t) : kOOB, 0, 0);
+    return r;
+  };
+  auto in_pool = [&](int64_t o) { return (o >= 0 && o < pb) ? (int)o : kOOB; };
+  auto dword_at = [&](int64_t o4) {
+    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
+    return w | (o4 == tail4 ? tailw : 0u);             // the partial dword itself reads as zero
+  };
+  auto page_of = [&](const RagRow& r, int ts, float4 (&cc)[NM], float4 (&ss)[NM]) {   // issue round trip 2
+    RagPage g;
+    g.page_off = (int32_t)__builtin_amdgcn_readfirstlane(r.w0);
+    g.th_off = (int32_t)__builtin_amdgcn_readfirstlane(r.w1);
+    g.rad_off = (int32_t)__builtin_amdgcn_readfirstlane(r.w2);
+    g.hk = __builtin_amdgcn_readfirstlane(r.hk);
+    g.hb = __builtin_amdgcn_readfirstlane(r.hb);
+    g.pos = r.pos;
+    const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
+    g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(page_off + 1), 0, 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int64_t cbit = th_off * 8 + (int64_t)(ts * G + (k ? gj : gi)) * b;
+      const int64_t o4 = (cbit >> 5) * 4;
+      g.cw[k][0] = dword_at(o4);
+      g.cw[k][1] = dword_at(o4 + 4);
+      g.rc[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(rad_off + ts * G + (k ? gj : gi)), 0, 0);
+      const int64_t so = page_off + kHeaderBytes + 4 * (k ? gj : gi);
+      const int64_t s4 = so >= 0 ? (so >> 2) * 4 : -4;
+      g.sw[k][0] = dword_at(s4);
+      g.sw[k][1] = dword_at(s4 + 4);
+    }
+    const int pos = (r.pos >= 0 && r.pos < a.max_pos) ? r.pos : 0;
+    const float* cs = a.cos_tbl + (int64_t)pos * DH + d0;
+    const float* sn = a.sin_tbl + (int64_t)pos * DH + d0;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      cc[m] = *reinterpret_cast<const float4*>(cs + 4 * m);
+      ss[m] = *reinterpret_cast<const float4*>(sn + 4 * m);
+    }
+    return g;
+  };
+  const int64_t total_slots = (int64_t)a.num_pages * a.page_size;
+  const float inv = 1.0f / __builtin_sqrtf((float)DH);
+  int staged = -1;
+  auto compute = [&](auto cb_lds_f, int64_t it, const RagPage& g, const float4 (&cc)[NM], const float4 (&ss)[NM])
+                     __attribute__((always_inline)) {
+    constexpr bool CB_LDS = decltype(cb_lds_f)::value;
+    const int64_t ch = 4 * it + wave;
+    const int p = (int)(ch / cpp), ts = 16 * (int)(ch % cpp) + t;
+    const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
+    const int hk = g.hk;
+    const bool hdr_ok = page_off >= 0 && page_off + 2 <= a.pages_bytes;
+    int n = hdr_ok ? min((int)g.cnt, a.page_size) : 0;
+    if (page_off + kHeaderBytes + 4 * G > a.pages_bytes || th_off < 0 || rad_off < 0 ||
+        th_off + ((int64_t)n * G * b + 7) / 8 > a.pages_bytes || rad_off + (int64_t)n * G > a.pages_bytes)
+      n = 0;
+    const bool head_ok = hk >= 0 && hk < a.num_kv;
+    const bool valid = ts < n && g.pos >= 0 && g.pos < a.max_pos && head_ok;
+    const int hq = head_ok ? hk : 0;
+    int code[2];
+    float rad[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int64_t cbit = th_off * 8 + (int64_t)(ts * G + (k ? gj : gi)) * b;
+      code[k] = (int)(__builtin_amdgcn_alignbit(g.cw[k][1], g.cw[k][0], (uint32_t)(cbit & 31)) & (uint32_t)(C - 1));
+      const int64_t so = page_off + kHeaderBytes + 4 * (k ? gj : gi);
+      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_alignbyte(g.sw[k][1], g.sw[k][0], (uint32_t)(so & 3)));
+      rad[k] = (float)g.rc[k] * sc * (1.0f / 127.0f);
+    }
+    const int r1 = (gi * C + code[0]) * GS + off, r2 = (gj * C + code[1]) * GS + off;
+    const int hbase = hq * G * C * GS;                   // floats; the codebook stays below 2^29 floats
+    floatx4 acc[NHS];
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) acc[hs] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      // the staged head's rows from LDS, another head's with buffer loads
+      float4 cv1, cv2;
+      if constexpr (CB_LDS) {
+        cv1 = *reinterpret_cast<const float4*>(cb_s + r1 + 4 * m);
+        cv2 = *reinterpret_cast<const float4*>(cb_s + r2 + 4 * m);
+      } else {
+        cv1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r1 + 4 * m), 0, 0));
+        cv2 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r2 + 4 * m), 0, 0));
+      }
+      const float k1[4] = {rad[0] * cv1.x, rad[0] * cv1.y, rad[0] * cv1.z, rad[0] * cv1.w};
+      const float k2[4] = {rad[1] * cv2.x, rad[1] * cv2.y, rad[1] * cv2.z, rad[1] * cv2.w};
+      const float co[4] = {cc[m].x, cc[m].y, cc[m].z, cc[m].w}, si[4] = {ss[m].x, ss[m].y, ss[m].z, ss[m].w};
+      float4 q0[NHS], q1[NHS];
+#pragma unroll
+      for (int hs = 0; hs < NHS; ++hs) {
+        const int slot = 4 * hs + (t & 3);
+        const bool q_ok = slot < a.grp;
+        const int qo = (hq * a.grp + (q_ok ? slot : 0)) * DH + d0 + 4 * m;
+        q0[hs] = *reinterpret_cast<const float4*>(q_s + qo);
+        q1[hs] = *reinterpret_cast<const float4*>(q_s + qo + DH / 2);
+        if (!q_ok) { q0[hs] = float4{0.f, 0.f, 0.f, 0.f}; q1[hs] = q0[hs]; }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = k1[e] * co[e] - k2[e] * si[e];
+        const float x1 = k2[e] * co[e] + k1[e] * si[e];
+#pragma unroll
+        for (int hs = 0; hs < NHS; ++hs) {
+          const float qa = e == 0 ? q0[hs].x : e == 1 ? q0[hs].y : e == 2 ? q0[hs].z : q0[hs].w;
+          const float qb = e == 0 ? q1[hs].x : e == 1 ? q1[hs].y : e == 2 ? q1[hs].z : q1[hs].w;
+          acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa, x0, acc[hs], 0, 0, 0);
+          acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qb, x1, acc[hs], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) {
+      float s0 = acc[hs][0], s2 = acc[hs][2], s1 = acc[hs][1], s3 = acc[hs][3];
+      swap32(s0, s2);
+      swap32(s1, s3);
+      float x = s0 + s2, y = s1 + s3;
+      swap16(x, y);
+      const float v = x + y;
+      const int i = 4 * hs + u;
+      if (i < a.grp)
+        a.logits_out[(int64_t)i * total_slots + (int64_t)p * a.page_size + ts] = valid ? v * inv : -INFINITY;
+    }
+  };
+  // the codebook of head hb into LDS when it is not the staged one (a
+  // workgroup-uniform decision: hb is the head of the iteration's first chunk)
+  auto stage = [&](int hb) {
+    if (hb == staged || hb < 0 || hb >= a.num_kv || C > 64) return;
+    __syncthreads();                                   // every wave is done with the previous codebook
+    const float4* src = reinterpret_cast<const float4*>(a.codebooks + (int64_t)hb * G * C * GS);
+    for (int i = threadIdx.x; i < G * C * GS / 4; i += 256) reinterpret_cast<float4*>(cb_s)[i] = src[i];
+    __syncthreads();
+    staged = hb;
+  };
+
+  // pipeline: rows two iterations ahead, page bytes and tables one ahead;
+  // rows and pages each in two register sets used alternately (the loop is
+  // unrolled by two, so no register a load is still filling is copied)
+  auto ts_of = [&](int64_t it) { return 16 * (int)((4 * it + wave) % cpp) + t; };
+  RagRow ra = row_of(it0), rb = row_of(it0 + 1);
+  float4 cca[NM], ssa[NM], ccb[NM], ssb[NM];
+  RagPage ga = page_of(ra, ts_of(it0), cca, ssa), gb;
+  __syncthreads();                                     // q staged
+  for (int64_t it = it0; it < it1; it += 2) {
+    gb = page_of(rb, ts_of(it + 1), ccb, ssb);         // waits for rows it + 1 (and so for pages it)
+    ra = row_of(it + 2);
+    stage(ga.hb);
+    if (4 * it + wave < nch) {
+      if (ga.hk == staged) compute(Flag<true>(), it, ga, cca, ssa);
+      else compute(Flag<false>(), it, ga, cca, ssa);
+    }
+    if (it + 1 >= it1) break;
+    ga = page_of(ra, ts_of(it + 2), cca, ssa);
+    rb = row_of(it + 3);
+    stage(gb.hb);
+    if (4 * (it + 1) + wave < nch) {
+      if (gb.hk == staged) compute(Flag<true>(), it + 1, gb, ccb, ssb);
+      else compute(Flag<false>(), it + 1, gb, ccb, ssb);
+    }
+  }
+}
+
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
   if (L.num_pages <= 0) return 0;
   const bool fast = L.page_size % 16 == 0 && (L.group_size == 16 || L.group_size == 32) && L.grp <= 8 &&
                     L.groups * L.group_size == L.dh;
-  if (fast) {
+  const int64_t q_bytes = (int64_t)L.num_kv * L.grp * L.dh * 4;
+  const int64_t cb_bytes = (int64_t)L.dh * (1 << L.b_theta) * 4;
+  if (fast && L.b_theta <= 6 && q_bytes <= 32768 && cb_bytes <= 32768 &&
+      (int64_t)L.num_pages * L.page_size * 4 <= 0x7FFFFF00LL) {
+    const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
+    const int64_t iters = (chunks + 3) / 4;
+    const dim3 grid((unsigned)(iters < 512 ? iters : 512));
+    const size_t lds = (size_t)(q_bytes + cb_bytes);
+#define SPHKV_RAGGED(D, S, N) \
+    if (L.dh == D && L.group_size == S && (L.grp > 4) == (N == 2)) \
+      hipLaunchKernelGGL((ragged_pipe_kernel<D, S, N>), grid, dim3(256), lds, stream, L);
+    SPHKV_RAGGED(128, 16, 1) SPHKV_RAGGED(128, 16, 2) SPHKV_RAGGED(128, 32, 1) SPHKV_RAGGED(128, 32, 2)
+    SPHKV_RAGGED(64, 16, 1) SPHKV_RAGGED(64, 16, 2) SPHKV_RAGGED(64, 32, 1) SPHKV_RAGGED(64, 32, 2)
+#undef SPHKV_RAGGED
+  } else if (fast) {
     const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
     const dim3 grid((unsigned)((chunks + 3) / 4));
 #define SPHKV_RAGGED(D, S, N) \
