@@ -1261,11 +1261,12 @@ __global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
 struct RagRow {          // round trip 1 of one chunk
   uint32_t w0, w1, w2;   // pointer-table row (page_off, th_off, rad_off)
   int hk, hb, pos;       // head of the chunk's page, head of the iteration's first chunk, slot position
+  int p, c16;            // the chunk's page and 16-slot chunk within it
 };
 struct RagPage {         // round trip 2 of one chunk, with its row's fields
   uint32_t cnt, cw[2][2], sw[2][2];
   int rc[2];
-  int page_off, th_off, rad_off, hk, hb, pos;
+  int page_off, th_off, rad_off, hk, hb, pos, p, c16;
 };
 
 template <int DH, int GS, int NHS>
@@ -1277,10 +1278,43 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   const int t = lane & 15, u = lane >> 4;
   const int cpp = a.page_size / 16;
   const int64_t nch = (int64_t)a.num_pages * cpp;
-  const int64_t niter = (nch + 3) / 4;
-  const int64_t per = (niter + gridDim.x - 1) / gridDim.x;
-  const int64_t it0 = (int64_t)blockIdx.x * per, it1 = min(it0 + per, niter);
-  if (it0 >= it1) return;                              // whole workgroup
+  // Work split for L2 locality.  Chunks come grouped by head, each head's in
+  // ascending position, and every head covers about the same positions, so
+  // [0, nch) is cut into S = NX * K equal segments (K per XCD, K ~ heads)
+  // and XCD x (workgroups b with b mod NX = x; the dispatcher deals
+  // workgroups to the 8 XCDs in turn) takes segments x, x + NX, ...: about
+  // the same 1/NX of the positions of every head, so its L2 holds 1/NX of
+  // the cos / sin rows.  Its segments, concatenated, are cut into GPX equal
+  // runs, one per workgroup.  Any order of pages is still covered exactly
+  // once.  Lane k < K holds segment k's list range and chunk offset; a list
+  // position maps to a chunk by a ballot over that table.
+  const int NX = (gridDim.x % 8 == 0 && gridDim.x >= 64) ? 8 : 1;
+  const int K = NX == 8 ? min(max(a.num_kv, 1), 8) : 1;
+  const int S = NX * K, xcd = blockIdx.x % NX, GPX = gridDim.x / NX, wj = blockIdx.x / NX;
+  int64_t seg_end = 0, seg_base = 0;                   // lane k < K: list end and chunk - list offset of segment k
+  {
+    const int64_t sg = xcd + (int64_t)NX * lane;
+    const int64_t b0 = lane < K ? sg * nch / S : 0, b1 = lane < K ? (sg + 1) * nch / S : 0;
+    int64_t len = b1 - b0, incl = len;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    seg_end = incl;
+    seg_base = b0 - (incl - len);
+  }
+  const int64_t Lx = __shfl(seg_end, K - 1, 64);
+  const int64_t q0 = wj * Lx / GPX, q1 = (wj + 1) * Lx / GPX;
+  const int64_t it0 = 0, it1 = (q1 - q0 + 3) / 4;
+  if (it1 == 0) return;                                // whole workgroup
+  auto chunk_of = [&](int64_t q) {                     // list position (< Lx) -> chunk index
+    const uint64_t m = __builtin_amdgcn_ballot_w64(lane < K && seg_end > q);
+    const int k = m ? (int)__builtin_ctzll(m) : 0;
+    const int64_t base = ((int64_t)__builtin_amdgcn_readlane((int)(seg_base >> 32), k) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)seg_base, k);
+    return q + base;
+  };
   const int b = a.b_theta, C = 1 << b;
   const int nq = a.num_kv * a.grp;
   float* q_s = rag_smem;                               // [num_kv * grp][DH]
@@ -1302,10 +1336,13 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
 
   auto row_of = [&](int64_t it) {                      // issue round trip 1 of this wave's chunk of iteration it
     RagRow r;
-    const int64_t ch = 4 * it + wave, ch0 = 4 * it;
-    const bool act = it < it1 && ch < nch;
-    const int p = act ? (int)(ch / cpp) : 0, c16 = act ? (int)(ch % cpp) : 0;
-    const int p0 = it < it1 ? (int)(ch0 / cpp) : 0;
+    const int64_t q = q0 + 4 * it + wave;
+    const bool act = it < it1 && q < q1;
+    const int64_t ch = act ? chunk_of(q) : 0, ch0 = it < it1 ? chunk_of(q0 + 4 * it) : 0;
+    const int p = (int)(ch / cpp), c16 = (int)(ch % cpp);
+    const int p0 = (int)(ch0 / cpp);
+    r.p = p;
+    r.c16 = c16;
     // unconditional loads (absent ones read zeros): a branch around a load
     // would make the compiler's waits for the loads in flight conservative
     const auto w = __builtin_amdgcn_raw_buffer_load_b96(rt, act ? 12 * p : kOOB, 0, 0);
@@ -1328,6 +1365,8 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     g.hk = __builtin_amdgcn_readfirstlane(r.hk);
     g.hb = __builtin_amdgcn_readfirstlane(r.hb);
     g.pos = r.pos;
+    g.p = r.p;
+    g.c16 = r.c16;
     const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
     g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(page_off + 1), 0, 0);
 #pragma unroll
@@ -1358,8 +1397,7 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   auto compute = [&](auto cb_lds_f, int64_t it, const RagPage& g, const float4 (&cc)[NM], const float4 (&ss)[NM])
                      __attribute__((always_inline)) {
     constexpr bool CB_LDS = decltype(cb_lds_f)::value;
-    const int64_t ch = 4 * it + wave;
-    const int p = (int)(ch / cpp), ts = 16 * (int)(ch % cpp) + t;
+    const int p = g.p, ts = 16 * g.c16 + t;
     const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
     const int hk = g.hk;
     const bool hdr_ok = page_off >= 0 && page_off + 2 <= a.pages_bytes;
@@ -1449,24 +1487,23 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   // pipeline: rows two iterations ahead, page bytes and tables one ahead;
   // rows and pages each in two register sets used alternately (the loop is
   // unrolled by two, so no register a load is still filling is copied)
-  auto ts_of = [&](int64_t it) { return 16 * (int)((4 * it + wave) % cpp) + t; };
   RagRow ra = row_of(it0), rb = row_of(it0 + 1);
   float4 cca[NM], ssa[NM], ccb[NM], ssb[NM];
-  RagPage ga = page_of(ra, ts_of(it0), cca, ssa), gb;
+  RagPage ga = page_of(ra, 16 * ra.c16 + t, cca, ssa), gb;
   __syncthreads();                                     // q staged
   for (int64_t it = it0; it < it1; it += 2) {
-    gb = page_of(rb, ts_of(it + 1), ccb, ssb);         // waits for rows it + 1 (and so for pages it)
+    gb = page_of(rb, 16 * rb.c16 + t, ccb, ssb);       // waits for rows it + 1 (and so for pages it)
     ra = row_of(it + 2);
     stage(ga.hb);
-    if (4 * it + wave < nch) {
+    if (q0 + 4 * it + wave < q1) {
       if (ga.hk == staged) compute(Flag<true>(), it, ga, cca, ssa);
       else compute(Flag<false>(), it, ga, cca, ssa);
     }
     if (it + 1 >= it1) break;
-    ga = page_of(ra, ts_of(it + 2), cca, ssa);
+    ga = page_of(ra, 16 * ra.c16 + t, cca, ssa);
     rb = row_of(it + 3);
     stage(gb.hb);
-    if (4 * (it + 1) + wave < nch) {
+    if (q0 + 4 * (it + 1) + wave < q1) {
       if (gb.hk == staged) compute(Flag<true>(), it + 1, gb, ccb, ssb);
       else compute(Flag<false>(), it + 1, gb, ccb, ssb);
     }
