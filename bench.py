@@ -379,7 +379,7 @@ def bench_ragged(args, dev):
         "config": {"workload": "config2 tier-1 and tier-2 pages (16 tokens), 8 kv heads, grp 4, dh 128",
                    "pages": int(npages), "algorithmic_bytes_per_step": int(nbytes)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": "ragged_fast_kernel",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": "ragged_pipe_kernel",
                      "kernel_us": round(ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
