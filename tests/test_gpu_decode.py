@@ -209,16 +209,19 @@ def test_decode_masked_positions(gpu):
     assert max_err(got, want) <= TOL
 
 
-def test_ragged_logits_matches_oracle(gpu):
+@pytest.mark.parametrize("ctx", [3000, 8192])
+def test_ragged_logits_matches_oracle(gpu, ctx):
+    # 8192 tokens: > 2048 tier-1 chunks, so the pipelined kernel runs its full
+    # 512-workgroup grid with the XCD-aware work split
     import fused_decode
-    wl = synth.make_decode_workload(2, ctx_override=3000)
+    wl = synth.make_decode_workload(2, ctx_override=ctx)
     cpu = oracle.build_pool(wl)
     plan = wl.plan
     for tid, (g, b) in ((1, (16, 6)), (2, (16, 4))):
         rows = [p for p in range(plan.num_rows) if plan.tier[p] == tid]
         heads = (plan.seq_head[rows] % plan.num_kv).astype(np.int32)
         G = wl.dh // g
-        max_pos = 3100
+        max_pos = ctx + 100
         cos_t, sin_t = fmt.rope_tables(max_pos, wl.dh, wl.rope_theta)
         pos = plan.positions[rows].reshape(-1).astype(np.int32)
         q = wl.q[0].astype(np.float32)
@@ -239,18 +242,21 @@ def test_ragged_logits_matches_oracle(gpu):
         assert max_err(got[fin], want[fin]) < 2e-4
 
 
-@pytest.mark.parametrize("tid,page_size,dh,grp", [(1, 128, 128, 4), (3, 128, 128, 4), (3, 16, 128, 4), (2, 128, 64, 4),
-                                                  (1, 16, 128, 8), (3, 32, 64, 6), (2, 48, 128, 1), (1, 16, 64, 3),
-                                                  (1, 24, 128, 4), (2, 128, 128, 9)])
-def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, grp):
+@pytest.mark.parametrize("tid,page_size,dh,grp,num_kv", [
+    (1, 128, 128, 4, 2), (3, 128, 128, 4, 2), (3, 16, 128, 4, 2), (2, 128, 64, 4, 2), (1, 16, 128, 8, 2),
+    (3, 32, 64, 6, 2), (2, 48, 128, 1, 2), (1, 16, 64, 3, 2), (1, 24, 128, 4, 2), (2, 128, 128, 9, 2),
+    (1, 16, 128, 8, 9), (2, 32, 64, 5, 11)])
+def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, grp, num_kv):
     # the reference's call shape: PAGE_SIZE = 128 pages (config.py:4,
     # spherical_kv_pipeline.py:1109-1125) and tier-3 decode pages (:1900-1910);
     # pages laid out back to back as _build_per_head_pages does (:1198-1213).
-    # page_size 24 and grp 9 take the general kernel, the rest the fast one.
+    # page_size 24 and grp 9 take the general kernel; 9 heads x grp 8 at dh
+    # 128 (q 36 KB, over the LDS budget) the one-chunk-per-wave form; the rest
+    # the pipeline (11 heads: codebooks restaged at each head change).
     import fused_decode
     from oracle import paging
-    rng = np.random.default_rng(700 + tid + page_size + dh + grp)
-    num_kv, L = 2, 300
+    rng = np.random.default_rng(700 + tid + page_size + dh + grp + num_kv)
+    L = 300
     g, b = fmt.TIER_GEOMETRY[tid]
     G = dh // g
     cbs = synth.make_codebooks(rng, num_kv, dh, [tid])[tid]
