@@ -946,11 +946,98 @@ __global__ __launch_bounds__(256) void lut_logits_kernel(LutLogitsLaunch a) {
   }
 }
 
+// The same logits, one thread per (kv head, token) serving all kv_groups q
+// heads of that kv head: the token's codes and radius bytes are read once (8
+// bytes each at G_max = 8), the page's scales once, and the kv head's
+// q_lut rows are staged in LDS for the lookups.  A workgroup takes kLutTok
+// tokens of one kv head.  Same arithmetic, in the same order, per (q head,
+// token) as lut_logits_kernel.
+constexpr int kLutTok = 256;
+template <int GM>
+__global__ __launch_bounds__(256) void lut_logits_group_kernel(LutLogitsLaunch a) {
+  extern __shared__ float lut_s[];                     // [kv_groups][num_tiers][GM][cb_size_max]
+  const int nb = (a.max_ctx + kLutTok - 1) / kLutTok;
+  const int hkv = blockIdx.x / nb, n0 = (blockIdx.x % nb) * kLutTok;
+  const int cb = a.cb_size_max, T = a.num_tiers, kg = a.kv_groups;
+  const int rows = kg * T * GM * cb;
+  const float* src = a.q_lut + (int64_t)hkv * kg * T * GM * cb;   // q heads hkv * kg .. + kg - 1
+  for (int i = threadIdx.x; i < rows; i += 256) lut_s[i] = src[i];
+  __syncthreads();
+  const int ctx = a.ctx_lens[hkv];
+  // the thread's kLutTok / 256 tokens, their loads issued together
+  constexpr int NT = kLutTok / 256;
+  int phys[NT], tier[NT];
+  bool ok[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    const int n = n0 + threadIdx.x + 256 * k, lb = n / a.page_size;
+    ok[k] = n < a.max_ctx && n < ctx && lb < a.max_blocks;
+    const int64_t bi = (int64_t)hkv * a.max_blocks + (ok[k] ? lb : 0);
+    phys[k] = a.block_table[bi];
+    tier[k] = a.bits_table[bi];
+  }
+  uint32_t tw[NT][GM / 4], rw[NT][GM / 4];
+  float rsc[NT][GM];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    ok[k] = ok[k] && phys[k] >= 0 && phys[k] < a.num_pages && tier[k] >= 0 && tier[k] < T;
+    const int n = n0 + threadIdx.x + 256 * k;
+    const int slot = n - (n / a.page_size) * a.page_size;
+    const int64_t pg = ok[k] ? phys[k] : 0;
+    const int64_t e = (pg * a.page_size + slot) * GM;
+#pragma unroll
+    for (int w = 0; w < GM / 4; ++w) {
+      tw[k][w] = *reinterpret_cast<const uint32_t*>(a.theta_codes + e + 4 * w);
+      rw[k][w] = *reinterpret_cast<const uint32_t*>(a.radius_codes + e + 4 * w);
+    }
+#pragma unroll
+    for (int g4 = 0; g4 < GM / 4; ++g4) {
+      const float4 v = *reinterpret_cast<const float4*>(a.r_scales + pg * GM + 4 * g4);
+      rsc[k][4 * g4] = v.x; rsc[k][4 * g4 + 1] = v.y; rsc[k][4 * g4 + 2] = v.z; rsc[k][4 * g4 + 3] = v.w;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    const int n = n0 + threadIdx.x + 256 * k;
+    if (n >= a.max_ctx) continue;
+    for (int j = 0; j < kg; ++j) {
+      float out = -INFINITY;
+      if (ok[k]) {
+        const float* lt = lut_s + ((j * T + tier[k]) * GM) * cb;
+        float sum = 0.f;
+#pragma unroll
+        for (int g = 0; g < GM; ++g) {
+          const int code = (int)((tw[k][g >> 2] >> (8 * (g & 3))) & 0xFF);
+          const float rd = (float)((rw[k][g >> 2] >> (8 * (g & 3))) & 0xFF);
+          const float rh = rsc[k][g] * rd / 255.0f;
+          const float v = code < cb ? lt[g * cb + code] : 0.f;
+          sum = __builtin_fmaf(rh, v, sum);
+        }
+        out = sum * a.sm_scale;
+      }
+      a.logits_out[(int64_t)(hkv * kg + j) * a.max_ctx + n] = out;
+    }
+  }
+}
+
 int launch_lut_logits(const LutLogitsLaunch& L, hipStream_t stream) {
   const int64_t total = (int64_t)L.num_q * L.max_ctx;
-  if (total > 0) {
-    const int blocks = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
-    hipLaunchKernelGGL(lut_logits_kernel, dim3(blocks), dim3(256), 0, stream, L);
+  if (total <= 0) return 0;
+  const int64_t lds = (int64_t)L.kv_groups * L.num_tiers * L.G_max * L.cb_size_max * 4;
+  const int64_t blocks = (int64_t)L.num_kv * ((L.max_ctx + kLutTok - 1) / kLutTok);
+  // (code rows and page scales are read in 4- and 16-byte words: their bases must be aligned)
+  const bool aligned = ((uintptr_t)L.theta_codes % 4) == 0 && ((uintptr_t)L.radius_codes % 4) == 0 &&
+                       ((uintptr_t)L.r_scales % 16) == 0;
+  // (the grouped kernel reads row 0 of the tables for absent tokens: both must exist)
+  if ((L.G_max == 8 || L.G_max == 4) && aligned && lds <= 48 * 1024 && L.num_q == L.num_kv * L.kv_groups &&
+      blocks < (1 << 30) && L.max_blocks >= 1 && L.num_pages >= 1) {
+    if (L.G_max == 8)
+      hipLaunchKernelGGL(lut_logits_group_kernel<8>, dim3((unsigned)blocks), dim3(256), (size_t)lds, stream, L);
+    else
+      hipLaunchKernelGGL(lut_logits_group_kernel<4>, dim3((unsigned)blocks), dim3(256), (size_t)lds, stream, L);
+  } else {
+    const int nblk = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+    hipLaunchKernelGGL(lut_logits_kernel, dim3(nblk), dim3(256), 0, stream, L);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

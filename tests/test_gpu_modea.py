@@ -104,9 +104,12 @@ def test_decode_modea_matches_oracle(gpu, case):
     np.testing.assert_allclose(gl[~absent], L[~absent], rtol=1e-4)
 
 
-def test_lut_and_logits_match_oracle(gpu):
+@pytest.mark.parametrize("G_pad", [0, 12])
+def test_lut_and_logits_match_oracle(gpu, G_pad):
+    # G_max 8: the grouped kernel (one thread per kv head and token); G_max
+    # 12: the general one
     w = synth.make_modea_workload(seed=41, num_kv=4, kv_groups=4, dh=128, page_size=16, ctx=1000,
-                                  tiers=(1, 2, 3), fracs=(1, 1, 1), holes=0.1)
+                                  tiers=(1, 2, 3), fracs=(1, 1, 1), holes=0.1, G_pad=G_pad)
     dev = {k: _t(w[k], gpu) for k in ("q", "cb_flat", "tier_G", "tier_g", "theta", "radius", "r_scales",
                                        "block_table", "bits_table")}
     lut = new_fused_decode.build_q_lut(dev["q"], dev["cb_flat"], dev["tier_G"], dev["tier_g"], w["num_kv"],
