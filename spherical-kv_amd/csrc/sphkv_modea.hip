@@ -1103,9 +1103,96 @@ __global__ __launch_bounds__(256) void omega_ema_kernel(OmegaLaunch a) {
   }
 }
 
+// Single-pass form for kv_groups <= 8 and max_blocks <= 1024 * PPT: 1024
+// threads per kv head, each holding the (m, l) of its PPT pages for every q
+// head of the group in registers (read once; one 8-byte load per pair when
+// l directly follows m, as in partial_scratch), the group's maxima and sums
+// reduced together.  Same formula as omega_ema_kernel.
+template <int PPT>
+__global__ __launch_bounds__(1024) void omega_ema_fast_kernel(OmegaLaunch a, int adjacent) {
+  constexpr int KG = 8;
+  __shared__ float red[16][KG];
+  const int h = blockIdx.x, kg = a.kv_groups;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float mv[KG][PPT], lv[KG][PPT];
+#pragma unroll
+  for (int r = 0; r < KG; ++r) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int p = threadIdx.x + 1024 * i;
+      const bool ok = r < kg && p < a.max_blocks;
+      const int64_t o = (int64_t)(h * kg + (r < kg ? r : 0)) * a.q_stride + (int64_t)(ok ? p : 0) * a.page_stride;
+      float m = 0.f, l = 0.f;
+      if (adjacent) {
+        const float2 v = *reinterpret_cast<const float2*>(a.m + o);
+        m = v.x; l = v.y;
+      } else {
+        m = a.m[o]; l = a.l[o];
+      }
+      lv[r][i] = ok ? l : 0.f;
+      mv[r][i] = (ok && l > 0.f) ? m : -1e30f;          // invalid pages do not win the max
+    }
+  }
+  auto reduce = [&](float (&v)[KG], bool is_max) {     // every q head of the group at once
+#pragma unroll
+    for (int r = 0; r < KG; ++r)
+      for (int d = 32; d >= 1; d >>= 1) {
+        const float x = __shfl_xor(v[r], d, 64);
+        v[r] = is_max ? fmaxf(v[r], x) : v[r] + x;
+      }
+    __syncthreads();                                   // red is free
+    if (lane == 0)
+#pragma unroll
+      for (int r = 0; r < KG; ++r) red[wave][r] = v[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < KG; ++r) {
+      float t = red[0][r];
+      for (int w = 1; w < 16; ++w) t = is_max ? fmaxf(t, red[w][r]) : t + red[w][r];
+      v[r] = t;
+    }
+  };
+  float mx[KG], z[KG];
+#pragma unroll
+  for (int r = 0; r < KG; ++r) {
+    mx[r] = -1e30f;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) mx[r] = fmaxf(mx[r], mv[r][i]);
+  }
+  reduce(mx, true);
+#pragma unroll
+  for (int r = 0; r < KG; ++r) {
+    z[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) z[r] += expf(fmaxf(mv[r][i] - mx[r], -60.f)) * lv[r][i];
+  }
+  reduce(z, false);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int p = threadIdx.x + 1024 * i;
+    if (p >= a.max_blocks) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < KG; ++r)
+      if (r < kg) s += expf(fmaxf(mv[r][i] - mx[r], -60.f)) * lv[r][i] / fmaxf(z[r], 1e-12f);
+    const float mass = s / (float)kg;
+    const int64_t o = (int64_t)h * a.max_blocks + p;
+    a.omega_out[o] = a.omega_prev[o] * a.beta + mass * (1.f - a.beta);
+  }
+}
+
 int launch_omega(const OmegaLaunch& L, hipStream_t stream) {
-  if (L.num_kv > 0 && L.max_blocks > 0)
+  if (L.num_kv <= 0 || L.max_blocks <= 0) return 0;
+  // (an 8-byte (m, l) load needs l right after m and 8-byte alignment at every page)
+  const bool adjacent = L.l == L.m + 1 && ((uintptr_t)L.m % 8) == 0 && L.q_stride % 2 == 0 && L.page_stride % 2 == 0;
+  if (L.kv_groups <= 8 && L.max_blocks <= 4096) {
+    if (L.max_blocks <= 2048)
+      hipLaunchKernelGGL(omega_ema_fast_kernel<2>, dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+    else
+      hipLaunchKernelGGL(omega_ema_fast_kernel<4>, dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+  } else {
     hipLaunchKernelGGL(omega_ema_kernel, dim3(L.num_kv), dim3(256), 0, stream, L);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
