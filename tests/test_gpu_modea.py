@@ -179,3 +179,25 @@ def test_omega_ema_after_decode_matches_oracle(gpu):
     want1 = oracle.omega_ema(part[:, :, 0], part[:, :, 1], np.ones_like(prev), 4, 4, 0.9)
     np.testing.assert_allclose(first.cpu().numpy(), want1, rtol=1e-5, atol=1e-7)
     assert (first.cpu().numpy()[3] == np.float32(0.9)).all()   # head without pages: mass 0
+
+
+@pytest.mark.parametrize("num_kv,kv_groups,max_blocks,adjacent", [
+    (3, 4, 300, False), (2, 8, 3000, True), (2, 12, 100, True), (1, 2, 5000, True), (2, 1, 2048, False)])
+def test_omega_ema_kernel_forms(gpu, num_kv, kv_groups, max_blocks, adjacent):
+    # the single-pass kernel (kv_groups <= 8, max_blocks <= 4096; (m, l) read
+    # as one 8-byte word when l follows m, else separately) and the general one
+    import omega_ema
+    rng = np.random.default_rng(num_kv * 1000 + kv_groups * 10 + max_blocks)
+    nq = num_kv * kv_groups
+    m = (rng.standard_normal((nq, max_blocks)) * 4).astype(np.float32)
+    l = np.where(rng.random((nq, max_blocks)) < 0.8, rng.random((nq, max_blocks)) * 3, 0.0).astype(np.float32)
+    m[0, :] += 100.0                                  # exp arguments clamp at -60 for the others
+    prev = rng.random((num_kv, max_blocks)).astype(np.float32)
+    if adjacent:
+        ml = torch.from_numpy(np.stack([m, l], axis=-1)).to(gpu)
+        mt, lt = ml[..., 0], ml[..., 1]
+    else:
+        mt, lt = _t(m, gpu), _t(l, gpu)
+    got = omega_ema.omega_ema(mt, lt, _t(prev, gpu), num_kv, kv_groups, max_blocks, 0.9).cpu().numpy()
+    want = oracle.omega_ema(m, l, prev, num_kv, kv_groups, 0.9)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-7)
