@@ -251,6 +251,59 @@ def cpu_baseline_modea(w, budget_s: float = 20.0):
                                       f"numpy fp64 restatement of decode_kernel.cu:108-246"}
 
 
+def modea_aux(args, dev, w, d, part):
+    """The Mode-A step's companions on the same tables, µs per call (HIP
+    events, back-to-back calls): the omega EMA on the decode's (m, l)
+    (spherical_kv_pipeline.py:1690-1701), the q_lut build and LUT logits
+    (new_fused_decode.sphkv_logits), and the decode-time append of one token
+    per kv head (fused_decode.sphkv_encode_append)."""
+    import fused_decode
+    import new_fused_decode
+    import omega_ema
+    nq, mb = w["q"].shape[0], w["max_blocks"]
+    om = torch.rand((w["num_kv"], mb), device=dev)
+    om_out = torch.empty_like(om)
+    lut = new_fused_decode.build_q_lut(d["q"], d["cb_flat"], d["tier_G"], d["tier_g"], w["num_kv"], w["kv_groups"],
+                                       w["num_tiers"], w["G_max"], w["cb_max"], w["g_max"])
+    logits = torch.empty((nq, w["max_ctx"]), dtype=torch.float32, device=dev)
+    # append into spare copies of the pools (the decode's stay as they are)
+    th, rd, rs, vp = (d[k].clone() for k in ("theta", "radius", "r_scales", "v_pool"))
+    G, g = int(w["tier_G"][0]), int(w["tier_g"][0])
+    C = int(w["cb_max"])
+    dcb = d["cb_flat"][:, 0, :G, :C, :g].contiguous()
+    kk = torch.randn((w["num_kv"], w["dh"]), device=dev)
+    vv = torch.randn((w["num_kv"], w["dh"]), device=dev)
+    pids = torch.arange(w["num_kv"], dtype=torch.int64, device=dev)
+    ps = w["page_size"]
+    calls = {
+        "omega_ema": lambda i: omega_ema.omega_ema(part[..., 0], part[..., 1], om, w["num_kv"], w["kv_groups"], mb,
+                                                   0.9, out=om_out),
+        "build_q_lut": lambda i: new_fused_decode.build_q_lut(d["q"], d["cb_flat"], d["tier_G"], d["tier_g"],
+                                                              w["num_kv"], w["kv_groups"], w["num_tiers"],
+                                                              w["G_max"], w["cb_max"], w["g_max"]),
+        "sphkv_logits": lambda i: new_fused_decode.sphkv_logits(
+            lut, d["theta"], d["radius"], d["r_scales"], d["block_table"], d["bits_table"], d["ctx_lens"], logits,
+            nq, w["num_kv"], w["kv_groups"], w["num_tiers"], mb, ps, w["G_max"], w["cb_max"], w["sm_scale"],
+            w["max_ctx"]),
+        "sphkv_encode_append": lambda i: fused_decode.sphkv_encode_append(
+            kk, vv, dcb, th, rd, rs, vp, pids, i % ps, G, g, C, w["G_max"], w["dh"], ps, (i % ps) == 0),
+    }
+    res = {}
+    for name, f in calls.items():
+        for i in range(20):
+            f(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(100):
+            f(i)
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) * 10.0, 2)       # ms per 100 calls -> us per call
+    log(f"[bench] Mode-A companions, us per call: {res}")
+    return res
+
+
 def bench_modea(args, dev):
     import fused_decode
     log(f"[bench] building Mode-A workload (page_size {args.page_size})")
@@ -287,6 +340,7 @@ def bench_modea(args, dev):
     ms = e0.elapsed_time(e1) / args.steps
     gbps = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] Mode-A {ms * 1e3:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+    aux = modea_aux(args, dev, w, d, part)
     cpu = None if args.no_cpu_baseline else cpu_baseline_modea(w)
     line = {
         "metric": "µs/decode step + achieved HBM GB/s (Mode-A LayerPool decode), 8B shape, 32K ctx, 1 GPU",
@@ -300,6 +354,7 @@ def bench_modea(args, dev):
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
                      "kernel": "modea_fast_kernel + modea_merge_kernel", "kernel_us": round(ms * 1e3, 3)},
+        "aux_us_per_call": aux,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
