@@ -1103,14 +1103,14 @@ __global__ __launch_bounds__(256) void omega_ema_kernel(OmegaLaunch a) {
   }
 }
 
-// Single-pass form for kv_groups <= 8 and max_blocks <= 1024 * PPT: 1024
-// threads per kv head, each holding the (m, l) of its PPT pages for every q
-// head of the group in registers (read once; one 8-byte load per pair when
-// l directly follows m, as in partial_scratch), the group's maxima and sums
-// reduced together.  Same formula as omega_ema_kernel.
-template <int PPT>
+// Single-pass form for kv_groups <= KG (4 or 8) and max_blocks <= 1024 * PPT:
+// 1024 threads per kv head, each holding the (m, l) of its PPT pages for every
+// q head of the group in registers (read once; one 8-byte load per pair when
+// l directly follows m, as in partial_scratch; no load for q heads past
+// kv_groups), the group's maxima and sums reduced together.  Same formula as
+// omega_ema_kernel.
+template <int PPT, int KG>
 __global__ __launch_bounds__(1024) void omega_ema_fast_kernel(OmegaLaunch a, int adjacent) {
-  constexpr int KG = 8;
   __shared__ float red[16][KG];
   const int h = blockIdx.x, kg = a.kv_groups;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1123,7 +1123,8 @@ __global__ __launch_bounds__(1024) void omega_ema_fast_kernel(OmegaLaunch a, int
       const bool ok = r < kg && p < a.max_blocks;
       const int64_t o = (int64_t)(h * kg + (r < kg ? r : 0)) * a.q_stride + (int64_t)(ok ? p : 0) * a.page_stride;
       float m = 0.f, l = 0.f;
-      if (adjacent) {
+      if (r >= kg) {                                   // uniform: no q head r in this group
+      } else if (adjacent) {
         const float2 v = *reinterpret_cast<const float2*>(a.m + o);
         m = v.x; l = v.y;
       } else {
@@ -1185,11 +1186,16 @@ int launch_omega(const OmegaLaunch& L, hipStream_t stream) {
   if (L.num_kv <= 0 || L.max_blocks <= 0) return 0;
   // (an 8-byte (m, l) load needs l right after m and 8-byte alignment at every page)
   const bool adjacent = L.l == L.m + 1 && ((uintptr_t)L.m % 8) == 0 && L.q_stride % 2 == 0 && L.page_stride % 2 == 0;
-  if (L.kv_groups <= 8 && L.max_blocks <= 4096) {
+  if (L.kv_groups <= 4 && L.max_blocks <= 4096) {
     if (L.max_blocks <= 2048)
-      hipLaunchKernelGGL(omega_ema_fast_kernel<2>, dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+      hipLaunchKernelGGL((omega_ema_fast_kernel<2, 4>), dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
     else
-      hipLaunchKernelGGL(omega_ema_fast_kernel<4>, dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+      hipLaunchKernelGGL((omega_ema_fast_kernel<4, 4>), dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+  } else if (L.kv_groups <= 8 && L.max_blocks <= 4096) {
+    if (L.max_blocks <= 2048)
+      hipLaunchKernelGGL((omega_ema_fast_kernel<2, 8>), dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
+    else
+      hipLaunchKernelGGL((omega_ema_fast_kernel<4, 8>), dim3(L.num_kv), dim3(1024), 0, stream, L, (int)adjacent);
   } else {
     hipLaunchKernelGGL(omega_ema_kernel, dim3(L.num_kv), dim3(256), 0, stream, L);
   }

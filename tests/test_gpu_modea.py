@@ -182,9 +182,10 @@ def test_omega_ema_after_decode_matches_oracle(gpu):
 
 
 @pytest.mark.parametrize("num_kv,kv_groups,max_blocks,adjacent", [
-    (3, 4, 300, False), (2, 8, 3000, True), (2, 12, 100, True), (1, 2, 5000, True), (2, 1, 2048, False)])
+    (3, 4, 300, False), (2, 8, 3000, True), (2, 12, 100, True), (1, 2, 5000, True), (2, 1, 2048, False),
+    (2, 6, 1500, False), (3, 3, 4096, True)])
 def test_omega_ema_kernel_forms(gpu, num_kv, kv_groups, max_blocks, adjacent):
-    # the single-pass kernel (kv_groups <= 8, max_blocks <= 4096; (m, l) read
+    # the single-pass kernel (kv_groups <= 4 or <= 8, max_blocks <= 4096; (m, l) read
     # as one 8-byte word when l follows m, else separately) and the general one
     import omega_ema
     rng = np.random.default_rng(num_kv * 1000 + kv_groups * 10 + max_blocks)
