@@ -24,6 +24,8 @@ def _stream() -> int:
 def _dev(t, name, dtype):
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise ValueError(f"{name} must be a CUDA (HIP) tensor")
+    if t.dtype is dtype and t.is_contiguous():      # the usual case: no dispatcher call
+        return t
     return t.to(dtype).contiguous()
 
 
