@@ -135,6 +135,22 @@ __device__ __forceinline__ float lut_entry(const ModeALaunch& a, int hq, int tie
   const float* qg = a.q + (int64_t)hq * a.dh + g * gt;
   const float* cb = a.cb_flat + ((((int64_t)hkv * a.num_tiers + tier) * a.G_max + g) * a.cb_max + c) * a.g_max;
   float dot = 0.f;
+  if (gt == 16 && (((uintptr_t)qg | (uintptr_t)cb) & 15) == 0) {   // both rows as four 16-byte loads
+    float4 qv[4], cv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qv[j] = reinterpret_cast<const float4*>(qg)[j];
+      cv[j] = reinterpret_cast<const float4*>(cb)[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {                   // the same d order as the loop below
+      dot = __builtin_fmaf(qv[j].x, cv[j].x, dot);
+      dot = __builtin_fmaf(qv[j].y, cv[j].y, dot);
+      dot = __builtin_fmaf(qv[j].z, cv[j].z, dot);
+      dot = __builtin_fmaf(qv[j].w, cv[j].w, dot);
+    }
+    return dot;
+  }
   for (int d = 0; d < gt; ++d) dot = __builtin_fmaf(qg[d], cb[d], dot);   // decode_kernel.cu:187-189 order
   return dot;
 }
@@ -152,6 +168,18 @@ __global__ __launch_bounds__(256) void qlut_kernel(ModeALaunch a, float* lut) {
   __syncthreads();
   const int64_t per_q = (int64_t)a.num_tiers * a.G_max * a.cb_max;
   const int64_t total = (int64_t)a.num_q * per_q;
+  if (total < ((int64_t)1 << 31)) {                 // 32-bit index arithmetic (the usual table size)
+    const int pq = (int)per_q, per_t = a.G_max * a.cb_max;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < (int)total; i += gridDim.x * blockDim.x) {
+      const int hq = i / pq;
+      int r = i - hq * pq;
+      const int tier = r / per_t;
+      r -= tier * per_t;
+      const int g = r / a.cb_max, c = r - g * a.cb_max;
+      lut[i] = tier_ok(a, tier, tG, tg) ? lut_entry(a, hq, tier, g, c, tG, tg) : 0.f;
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int hq = (int)(i / per_q);
     int64_t r = i - hq * per_q;
