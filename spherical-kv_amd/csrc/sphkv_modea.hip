@@ -46,15 +46,20 @@ constexpr int kAppendMaxSims = 4096;     // G * C
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendLaunch a) {
   const int h = blockIdx.x;
   const int tid = threadIdx.x;
-  __shared__ float s_k[kAppendMaxDh];
-  __shared__ float s_norm[kAppendMaxDh], s_inv[kAppendMaxDh];
+  __shared__ __attribute__((aligned(16))) float s_k[kAppendMaxDh];
+  __shared__ float s_norm[kAppendMaxDh], s_inv[kAppendMaxDh], s_ratio[kAppendMaxDh];
+  __shared__ int s_code[kAppendMaxDh], s_resc[kAppendMaxDh];
   __shared__ float s_sim[kAppendMaxSims];
   const int64_t pid = a.pids[h];
+  // k and v do not depend on the page: their loads share pid's round trip
+  const float kx = tid < a.dh ? a.k_post[(int64_t)h * a.dh + tid] : 0.f;
+  const float vx = tid < a.dh ? a.v_new[(int64_t)h * a.dh + tid] : 0.f;
   if (pid < 0 || pid >= a.num_pages) return;        // no such pool page: nothing is written
   const int64_t row = pid * a.page_size + a.slot;   // (page, slot)
+  const float prev = tid < a.G && !a.is_new_page ? a.r_scales[pid * a.G_max + tid] : 0.f;   // running scale
   if (tid < a.dh) {
-    s_k[tid] = a.k_post[(int64_t)h * a.dh + tid];
-    a.v_pool[row * a.dh + tid] = (_Float16)a.v_new[(int64_t)h * a.dh + tid];   // round to nearest even
+    s_k[tid] = kx;
+    a.v_pool[row * a.dh + tid] = (_Float16)vx;      // round to nearest even
   }
   __syncthreads();
   // decode_kernel.cu:38-42: norm = sqrt(sum k^2 + 1e-16), inv = 1 / (norm + 1e-8)
@@ -75,45 +80,74 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendLaunch a) 
     const float inv = s_inv[grp];
     const float* cb = a.decode_cb + (((int64_t)h * a.G + grp) * a.C + c) * a.g;
     float sim = 0.f;
-    for (int d = 0; d < a.g; ++d) sim = __builtin_fmaf(kg[d] * inv, cb[d], sim);
+    if (a.g == 16 && ((uintptr_t)cb & 15) == 0) {  // the row as four 16-byte loads, same d order
+      floatx4 cv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cv[j] = reinterpret_cast<const floatx4*>(cb)[j];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sim = __builtin_fmaf(kg[4 * j + e] * inv, cv[j][e], sim);
+    } else {
+      for (int d = 0; d < a.g; ++d) sim = __builtin_fmaf(kg[d] * inv, cb[d], sim);
+    }
     s_sim[i] = sim;
   }
   __syncthreads();
-  if (tid < a.G) {
-    const int grp = tid;
+  // argmax per group, one wave per group: each lane keeps the first maximum of
+  // its codes (c = lane, lane + 64, ...), then the lanes agree on the largest
+  // value and, among equal values, the smallest code -- the first maximum of
+  // the ascending scan (decode_kernel.cu:47-55); NaN and values <= -1e30 never win
+  const int lane = tid & 63;
+  for (int grp = tid >> 6; grp < a.G; grp += kAppendThreads / 64) {
     float best = -1e30f;
-    int code = 0;
-    for (int c = 0; c < a.C; ++c) {
+    int code = -1;
+    for (int c = lane; c < a.C; c += 64) {
       const float v = s_sim[grp * a.C + c];
       if (v > best) { best = v; code = c; }
     }
-    a.theta_codes[row * a.G_max + grp] = (uint8_t)code;
-    // decode_kernel.cu:59-82: per-page running-max radius scale
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oc = __shfl_xor(code, o, 64);
+      if (ob > best || (ob == best && (unsigned)oc < (unsigned)code)) { best = ob; code = oc; }
+    }
+    if (lane == 0) s_code[grp] = code < 0 ? 0 : code;
+  }
+  __syncthreads();
+  // decode_kernel.cu:59-82: per-page running-max radius scale
+  if (tid < a.G) {
+    const int grp = tid;
+    a.theta_codes[row * a.G_max + grp] = (uint8_t)s_code[grp];
     const float nrm = s_norm[grp];
     float* rs = a.r_scales + pid * a.G_max + grp;
     float r_scale;
+    int resc = 0;
     if (a.is_new_page) {
       *rs = nrm;
       r_scale = nrm;
+    } else if (nrm > prev) {
+      s_ratio[grp] = prev / (nrm + 1e-8f);
+      resc = 1;
+      *rs = nrm;
+      r_scale = nrm;
     } else {
-      const float prev = *rs;
-      if (nrm > prev) {
-        const float ratio = prev / (nrm + 1e-8f);
-        for (int t = 0; t < a.slot; ++t) {
-          uint8_t* rc = a.radius_codes + (pid * a.page_size + t) * a.G_max + grp;
-          float x = (float)(*rc) * ratio;
-          x = fminf(fmaxf(roundf(x), 0.f), 255.f);
-          *rc = (uint8_t)x;
-        }
-        *rs = nrm;
-        r_scale = nrm;
-      } else {
-        r_scale = prev;
-      }
+      r_scale = prev;
     }
+    s_resc[grp] = resc;
     float rq = roundf(nrm / (r_scale + 1e-8f) * 255.0f);
     rq = fminf(fmaxf(rq, 0.f), 255.f);
     a.radius_codes[row * a.G_max + grp] = (uint8_t)rq;
+  }
+  __syncthreads();
+  // a rescaled group's earlier radius codes, one thread per (token, group)
+  for (int i = tid; i < a.slot * a.G; i += kAppendThreads) {
+    const int t = i / a.G, grp = i - t * a.G;
+    if (!s_resc[grp]) continue;
+    uint8_t* rc = a.radius_codes + (pid * a.page_size + t) * a.G_max + grp;
+    float x = (float)(*rc) * s_ratio[grp];
+    x = fminf(fmaxf(roundf(x), 0.f), 255.f);
+    *rc = (uint8_t)x;
   }
 }
 

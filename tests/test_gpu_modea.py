@@ -27,11 +27,17 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-@pytest.mark.parametrize("page_size", [16, 128])
-def test_encode_append_bitexact_over_a_sequence(gpu, page_size):
-    rng = np.random.default_rng(21 + page_size)
-    num_kv, dh, G, g, C, G_max = 8, 128, 8, 16, 64, 8
+@pytest.mark.parametrize("page_size,G,g,C,dup", [(16, 8, 16, 64, False), (128, 8, 16, 64, False),
+                                                  (16, 4, 32, 100, True)])
+def test_encode_append_bitexact_over_a_sequence(gpu, page_size, G, g, C, dup):
+    # g 16: centroid rows as 16-byte loads; g 32 with C 100: one element at a
+    # time, two codes per lane in the argmax, and (dup) every row c equal to
+    # row c + 50, so every argmax is a tie that the first maximum settles
+    rng = np.random.default_rng(21 + page_size + C)
+    num_kv, dh, G_max = 8, 128, 8
     x = rng.standard_normal((num_kv, G, C, g))
+    if dup:
+        x[:, :, C // 2:] = x[:, :, :C // 2]
     cb = (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
     n_pages = 3 * num_kv
     th = np.zeros((n_pages, page_size, G_max), np.uint8)
@@ -56,6 +62,8 @@ def test_encode_append_bitexact_over_a_sequence(gpu, page_size):
     assert (d_rd.cpu().numpy() == rd).all()
     assert (d_rs.cpu().numpy().view(np.uint32) == rs.view(np.uint32)).all()
     assert (d_vp.cpu().numpy().view(np.uint16) == vp.view(np.uint16)).all()
+    if dup:
+        assert th.max() < C // 2                        # the ties went to the first maximum
 
 
 CASES = [
@@ -133,6 +141,25 @@ def test_lut_and_logits_match_oracle(gpu, G_pad):
     err = max_err(got[~inf], want[~inf])
     log(f"lut logits max abs err {err:.3e}")
     assert err <= 1e-4
+
+
+def test_q_lut_row_load_forms_agree(gpu):
+    # 16-dim groups read as 16-byte loads when q and the centroid rows are
+    # 16-byte aligned, else one float at a time: same fma order, same bits
+    w = synth.make_modea_workload(seed=43, num_kv=2, kv_groups=4, dh=128, page_size=16, ctx=300,
+                                  tiers=(1, 2, 3), fracs=(1, 1, 1))
+    q = _t(w["q"], gpu)
+    qbuf = torch.empty(q.numel() + 1, dtype=torch.float32, device=gpu)
+    q_odd = qbuf[1:].view(q.shape)                    # data 4 bytes past a 16-byte boundary
+    q_odd.copy_(q)
+    assert q_odd.data_ptr() % 16 == 4
+    args = (_t(w["cb_flat"], gpu), _t(w["tier_G"], gpu), _t(w["tier_g"], gpu), w["num_kv"], w["kv_groups"],
+            w["num_tiers"], w["G_max"], w["cb_max"], w["g_max"])
+    a = new_fused_decode.build_q_lut(q, *args)
+    b = new_fused_decode.build_q_lut(q_odd, *args)
+    assert torch.equal(a, b)
+    want = oracle.q_lut(w["q"], w["cb_flat"], w["tier_G"], w["tier_g"], w["kv_groups"])
+    assert max_err(a.cpu().numpy(), want) <= 1e-4
 
 
 def test_modea_single_range_and_empty_tables(gpu):
