@@ -95,6 +95,12 @@ TRAFFIC_BYTES = {(2, "default"): 86461801}
 # 1024 SIMDs at 2.4 GHz.
 ENCODE_VALU_INSTS = {3: 6770579}
 ENCODE_TRAFFIC_BYTES = {3: 55598602}
+# HBM bytes per Mode-A decode (modea_fast_kernel, page_size 16; profiles/
+# modea_config2shape_counters.txt) and per fused_decode_ragged step (both
+# tiers' ragged_pipe_kernel launches; profiles/ragged_config2_hbm_traffic.txt),
+# FETCH_SIZE * 2 + WRITE_SIZE as above.
+MODEA_TRAFFIC_BYTES = {16: 80479122}
+RAGGED_TRAFFIC_BYTES = 47988605
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
@@ -352,7 +358,7 @@ def bench_modea(args, dev):
                                f"60/40 tier 1/2, random page placement", "pages": int(w["num_kv"] * mb),
                    "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": MODEA_TRAFFIC_BYTES.get(w["page_size"]),
                      "kernel": "modea_fast_kernel + modea_merge_kernel", "kernel_us": round(ms * 1e3, 3)},
         "aux_us_per_call": aux,
         "cpu_baseline": cpu,
@@ -434,7 +440,7 @@ def bench_ragged(args, dev):
         "config": {"workload": "config2 tier-1 and tier-2 pages (16 tokens), 8 kv heads, grp 4, dh 128",
                    "pages": int(npages), "algorithmic_bytes_per_step": int(nbytes)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": "ragged_pipe_kernel",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": RAGGED_TRAFFIC_BYTES, "kernel": "ragged_pipe_kernel",
                      "kernel_us": round(ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
