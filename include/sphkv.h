@@ -227,6 +227,89 @@ int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, 
                                 int32_t gqa, int32_t dh, uint16_t* out, void* stream);
 
 /*
+ * ---- Decode-time tail of the Mode-B path ---------------------------------
+ * A full decode step of the reference: _compressed_head_attention_batched
+ * (spherical_kv_pipeline.py:2057-2369; multi-head form _decode_layer_all_heads
+ * :1755-2055) scores the page-resident context, the tokens staged since the
+ * last decode page (:2248-2285, fp32 radii) and the step's own token (:2294-
+ * 2342, its pre-RoPE key encoded through the tier-3 codebook at current_pos)
+ * in one softmax (:2347-2348) and attn @ V (:2364-2367, the new token's V =
+ * v_new); then _append_decode_kv (:2389-2448) stages the new token (tier-3
+ * encode, N = 1) and, at page_size staged tokens, _flush_decode_page
+ * (:2449-2475) turns them into a tier-3 pagebuilder page
+ * (build_page_from_codes, pagebuilder.py:36-42) that later steps read as
+ * context.
+ *
+ * Tail state, per (sequence, kv head) sh = seq * num_kv + head, G3 = dh/32:
+ *   stg_r     fp32  [num_sh, 16, G3]   staged radii (unquantised)
+ *   stg_code  int32 [num_sh, 16, G3]   staged tier-3 codes
+ *   stg_v     fp16  [num_sh, 16, dh]   staged V rows
+ *   stg_pos   int32 [num_sh, 16]       staged positions
+ *   tail_state int32 [num_sh, 4]       (staged count 0..15, decode pages
+ *                                       flushed, tokens dropped for want of a
+ *                                       decode slot, 0); zero it to start
+ * Decode pages: sh's page k (k < dec_cap) is written at pages + dec_byte0 +
+ * (sh * dec_cap + k) * slot (slot = 16-byte aligned size of a 16-token tier-3
+ * page: 112 bytes at dh 128, 64 at dh 64), its V at V page dec_vpage0 +
+ * sh * dec_cap + k, and its positions into the pointer-table row after sh's
+ * last one; the work items of sh then cover that row (their end_row grows by
+ * one).  The pointer table, vslot and positions must be the decode-time
+ * layout of sphkv_tail_relayout, and the work list (work int32 [n, 4],
+ * work_start) must cover each sh's prefill rows in that layout.
+ */
+
+/*
+ * The decode-time pointer table: the prefill table (row_start int32
+ * [num_sh + 1] on the device, ptable, vslot, positions of num_rows rows) with
+ * dec_cap reserved rows after each (seq, head)'s rows: prefill row p of sh
+ * moves to p + sh * dec_cap, reserved row k of sh is row row_start[sh + 1] +
+ * sh * dec_cap + k, pointing at sh's decode page k (offsets as above, tier-3
+ * sections of 16 tokens), positions -1.  Outputs: ptable_d int32
+ * [num_rows + num_sh*dec_cap, 3], vslot_d, positions_d of as many rows.  No
+ * reference counterpart (the reference keeps each flushed page as its own
+ * tensor, spherical_kv_pipeline.py:2487-2495).
+ */
+int sphkv_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,
+                        const int32_t* vslot, const int32_t* positions, int32_t dec_cap, int64_t dec_byte0,
+                        int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d, int32_t* positions_d,
+                        void* stream);
+
+/*
+ * One decode step: sphkv_decode_paged over the decode-time table (prefill
+ * pages and flushed decode pages), with the staged tokens and the new token
+ * in the same softmax; then, when append = 1, the new token is staged (and a
+ * full page flushed).  k_new [num_sh, dh] pre-RoPE (fp16, or fp32 with
+ * k_is_fp32 = 1), v_new fp16 [num_sh, dh], cur_pos int32 [num_seqs] (the new
+ * token's position).  pages, positions, v_pool and work are written by a
+ * flush.  The new token's codes and radii are bit-exact with
+ * _encode_keys_with_codebooks on one token; the output is within the decode's
+ * tolerance of the reference formula.  Other arguments as sphkv_decode_paged.
+ */
+int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable, const int32_t* vslot,
+                      int32_t* positions, int32_t num_rows, uint16_t* v_pool, int64_t num_vpages,
+                      const float* cb1, const float* cb2, const float* cb3,
+                      int32_t* work, int32_t num_items, const int32_t* work_start,
+                      int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                      const uint16_t* q, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
+                      const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
+                      int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t append,
+                      uint16_t* out, void* workspace, int64_t workspace_bytes,
+                      int32_t dh, int32_t page_size, float sm_scale, double rope_theta, void* stream);
+
+/*
+ * _append_decode_kv alone (spherical_kv_pipeline.py:2389-2448, flush
+ * :2449-2475): stages every (seq, head)'s new token, flushing full pages, with
+ * no attention.  Arguments as sphkv_decode_step.
+ */
+int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions, int32_t num_rows,
+                        uint16_t* v_pool, int64_t num_vpages, const float* cb3,
+                        int32_t* work, int32_t num_items, const int32_t* work_start, int32_t num_seqs,
+                        int32_t num_kv, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
+                        const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
+                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t dh,
+                        int32_t page_size, void* stream);
+
+/*
  * Logits-only ragged kernel with the contract of the reference's missing
  * fused_decode_ragged (call sites spherical_kv_pipeline.py:1102-1125,
  * :1865-1870, :1906-1910): pages of one tier, RoPE from the caller's HF-layout

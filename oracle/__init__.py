@@ -24,6 +24,9 @@ Contents and the reference lines each part restates (reference repo paths):
                               / sqrt(dh)), softmax :2347-2348, attn @ V :2364-2367;
                               rotate_half :1004-1007.  Dense fp16 K tokens use
                               textbook attention <R(-t) q, k> / sqrt(dh).
+                              With a tail (oracle/tail.py) it also scores the
+                              decode pages, staged tokens and the step's own
+                              token (:2248-2342) in the same softmax.
   ragged_logits               the logits-only contract of fused_decode_ragged
                               (call sites spherical_kv_pipeline.py:1102-1125,
                               1865-1870) evaluated with the caller's cos/sin
@@ -259,9 +262,15 @@ def mode_b_logits(q: np.ndarray, pos: np.ndarray, cos_t: np.ndarray, sin_t: np.n
 
 
 def decode_mode_b(pool: Dict[str, np.ndarray], plan, codebooks: Dict[int, np.ndarray],
-                  q: np.ndarray, gqa: int, rope_theta: float, return_lse: bool = False):
+                  q: np.ndarray, gqa: int, rope_theta: float, return_lse: bool = False,
+                  tail=None, k_new=None, v_new=None, cur_pos=None):
     """fp64 Mode-B decode over a placed pool.  q [num_seqs, num_kv*gqa, dh]
-    (fp16 values).  Returns out [num_seqs, num_kv*gqa, dh] fp64."""
+    (fp16 values).  Returns out [num_seqs, num_kv*gqa, dh] fp64.
+
+    tail (oracle.tail.TailOracle): adds each (seq, head)'s decode pages and
+    staged tokens, and with k_new / v_new [num_seqs, num_kv, dh], cur_pos
+    [num_seqs] the step's own token, to the same softmax (a full decode step
+    of _compressed_head_attention_batched, spherical_kv_pipeline.py:2057-2369)."""
     dh, ps, num_kv = plan.dh, plan.page_size, plan.num_kv
     pages, v_pool = pool["pages"], pool["v_pool"]
     inv_freq = rope_inv_freq(dh, rope_theta)
@@ -289,6 +298,12 @@ def decode_mode_b(pool: Dict[str, np.ndarray], plan, codebooks: Dict[int, np.nda
                 cb = codebooks[tid][h].astype(np.float64)                  # [G, C, g]
                 cw = cb[np.arange(G)[None, :], codes]                       # [n, G, g]
                 logits.append(mode_b_logits(qh, pos, cos_t, sin_t, cw, r_hat, None, G, g))
+        if tail is not None:
+            step = (k_new[s, h], v_new[s, h], cur_pos[s]) if k_new is not None else (None, None, None)
+            lt, vt = tail.terms(s, h, qh, inv_freq, *step)
+            if lt.shape[1]:
+                logits.append(lt)
+                vs.append(vt)
         if not logits:
             continue
         lg = np.concatenate(logits, axis=1)

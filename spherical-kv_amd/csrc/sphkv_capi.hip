@@ -263,6 +263,124 @@ int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, 
                      dh, 16, 1.f, 0.0, stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Shared checks of the tail entries: the tail state, the decode-page region
+// and the step inputs.
+int tail_checks(const char* fn, int64_t pages_bytes, int32_t num_rows, int64_t num_vpages, const float* cb3,
+                int32_t num_seqs, int32_t num_kv, const void* k_new, const uint16_t* v_new, const int32_t* cur_pos,
+                const float* stg_r, const int32_t* stg_code, const uint16_t* stg_v, const int32_t* stg_pos,
+                const int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t dh) {
+  if (!cb3) return fail(SPHKV_EINVAL, "%s: the tier-3 codebook is required (decode tokens are tier 3)", fn);
+  if (!k_new || !v_new || !cur_pos || !stg_r || !stg_code || !stg_v || !stg_pos || !tail_state)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  if (dec_cap < 0 || dec_byte0 < 0 || dec_vpage0 < 0 || (dec_byte0 & 15))
+    return fail(SPHKV_EINVAL, "%s: dec_cap, dec_vpage0 and dec_byte0 must be >= 0, dec_byte0 16-byte aligned", fn);
+  const int64_t nres = (int64_t)num_seqs * num_kv * dec_cap;
+  if (dec_byte0 + nres * sphkv::tail_slot_bytes(dh) > pages_bytes)
+    return fail(SPHKV_EINVAL, "%s: the decode-page region (%lld pages of %d bytes from %lld) leaves the byte pool",
+                fn, (long long)nres, sphkv::tail_slot_bytes(dh), (long long)dec_byte0);
+  if ((int64_t)dec_vpage0 + nres > num_vpages)
+    return fail(SPHKV_EINVAL, "%s: the decode pages' V slots leave the V pool", fn);
+  if (num_rows < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  return SPHKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable, const int32_t* vslot,
+                      int32_t* positions, int32_t num_rows, uint16_t* v_pool, int64_t num_vpages,
+                      const float* cb1, const float* cb2, const float* cb3,
+                      int32_t* work, int32_t num_items, const int32_t* work_start,
+                      int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                      const uint16_t* q, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
+                      const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
+                      int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t append,
+                      uint16_t* out, void* workspace, int64_t workspace_bytes,
+                      int32_t dh, int32_t page_size, float sm_scale, double rope_theta, void* stream) {
+  const char* fn = "sphkv_decode_step";
+  // the page-resident part is checked exactly as sphkv_decode_paged's (no launch)
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (!gqa_ok(gqa)) return fail(SPHKV_EINVAL, "%s: gqa must be 1, 2, 4 or 8 (got %d)", fn, gqa);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
+  if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || num_rows < 0) return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (!(rope_theta > 1.0)) return fail(SPHKV_EINVAL, "%s: rope_theta must be > 1", fn);
+  if (pages_bytes < 0 || pages_bytes > 0x7FFFFF00LL || (int64_t)num_rows * 64 > 0x7FFFFF00LL)
+    return fail(SPHKV_EINVAL, "%s: byte pool and pointer table must stay below 2 GiB", fn);
+  if (pages_bytes & 3) return fail(SPHKV_EINVAL, "%s: pages_bytes must be a multiple of 4 (pad the byte pool)", fn);
+  if (num_vpages < 0 || num_vpages > (int64_t)1 << 31)
+    return fail(SPHKV_EINVAL, "%s: num_vpages must be in [0, 2^31] (int32 vslot)", fn);
+  if (append != 0 && append != 1) return fail(SPHKV_EINVAL, "%s: append must be 0 or 1", fn);
+  if (num_seqs == 0) return ok();
+  int rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, k_new, v_new, cur_pos, stg_r,
+                       stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap, dh);
+  if (rc != SPHKV_OK) return rc;
+  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
+  if (workspace_bytes < need)
+    return fail(SPHKV_EINVAL, "%s: workspace too small (%lld < %lld bytes)", fn, (long long)workspace_bytes,
+                (long long)need);
+  if (num_items < num_seqs * num_kv) return fail(SPHKV_EINVAL, "%s: need at least one work item per (seq, head)", fn);
+  if (!work_start || !workspace || !out || !q || !work || !pages || !ptable || !vslot || !positions || !v_pool)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::DecodeLaunch L{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
+                        cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q, out,
+                        static_cast<float*>(workspace), dh, sm_scale, rope_theta};
+  sphkv::TailLaunch T{k_new, k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state,
+                      pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0,
+                      sphkv::kTailDecode | (append ? sphkv::kTailAppend : 0)};
+  return launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
+}
+
+int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions, int32_t num_rows,
+                        uint16_t* v_pool, int64_t num_vpages, const float* cb3,
+                        int32_t* work, int32_t num_items, const int32_t* work_start, int32_t num_seqs,
+                        int32_t num_kv, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
+                        const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
+                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t dh,
+                        int32_t page_size, void* stream) {
+  const char* fn = "sphkv_decode_append";
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
+  if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || pages_bytes < 0 || num_vpages < 0)
+    return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (num_seqs == 0) return ok();
+  int rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, k_new, v_new, cur_pos, stg_r,
+                       stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap, dh);
+  if (rc != SPHKV_OK) return rc;
+  if (num_items < num_seqs * num_kv) return fail(SPHKV_EINVAL, "%s: need at least one work item per (seq, head)", fn);
+  if (!work || !work_start || !pages || !positions || !v_pool) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::DecodeLaunch L{pages, pages_bytes, nullptr, nullptr, positions, num_rows, v_pool, num_vpages,
+                        nullptr, nullptr, cb3, work, num_items, work_start, num_seqs, num_kv, 1, nullptr, nullptr,
+                        nullptr, dh, 1.f, 2.0};
+  sphkv::TailLaunch T{k_new, k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state,
+                      pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, sphkv::kTailAppend};
+  return launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
+}
+
+int sphkv_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,
+                        const int32_t* vslot, const int32_t* positions, int32_t dec_cap, int64_t dec_byte0,
+                        int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d, int32_t* positions_d,
+                        void* stream) {
+  const char* fn = "sphkv_tail_relayout";
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (num_sh < 0 || num_rows < 0 || dec_cap < 0 || dec_byte0 < 0 || dec_vpage0 < 0 || (dec_byte0 & 15))
+    return fail(SPHKV_EINVAL, "%s: bad size or a dec_byte0 that is not 16-byte aligned", fn);
+  const int64_t nres = (int64_t)num_sh * dec_cap;
+  if ((int64_t)num_rows + nres > 0x7FFFFFFFLL / 64 || dec_byte0 + nres * sphkv::tail_slot_bytes(dh) > 0x7FFFFF00LL ||
+      (int64_t)dec_vpage0 + nres > 0x7FFFFFFFLL)
+    return fail(SPHKV_EINVAL, "%s: the decode-time table, byte pool or V pool outgrows int32 indices", fn);
+  if ((int64_t)num_rows + nres == 0) return ok();
+  if (!row_start || !ptable_d || !vslot_d || !positions_d || (num_rows > 0 && (!ptable || !vslot || !positions)))
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  return launch_status(sphkv::launch_tail_relayout(row_start, num_sh, num_rows, ptable, vslot, positions, dec_cap,
+                                                   dec_byte0, dec_vpage0, dh, ptable_d, vslot_d, positions_d,
+                                                   (hipStream_t)stream), fn);
+}
+
 int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
                               const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
                               const float* cos_tbl, const float* sin_tbl, int32_t max_pos,

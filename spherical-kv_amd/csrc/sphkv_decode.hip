@@ -986,15 +986,433 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-time tail of the Mode-B step (spherical_kv_pipeline.py:2248-2342,
+// 2389-2475).  One 1024-thread workgroup per (sequence, kv head) sh; it is the
+// only reader and writer of sh's tail state within a launch.
+//
+//   * The step's new pre-RoPE key is encoded through the tier-3 codebook as
+//     one token (_encode_keys_with_codebooks on kn.unsqueeze(0), :2311-2313):
+//     fp32 radius and first-max code per 32-dim group, bit-exact with torch
+//     CPU (N*g*C = 256 < 400: ATen's naive loop, a multiply-then-add chain).
+//   * Decode (kTailDecode): the staged tokens (their fp32 radii, :2248-2285)
+//     and the new token at current_pos (:2315-2342) are scored with
+//     logit = sum_g r_g <q, R(pos) c_g> / sqrt(dh) (= the back-rotated query's
+//     form with the unit centroids), folded with the work items' partials into
+//     one log-sum-exp (the softmax over context + tail, :2347-2348) and
+//     attn @ V (:2364-2367, V of the new token = v_new).  Tail weights stay
+//     fp32.
+//   * Append (kTailAppend, _append_decode_kv :2389-2448): the new token goes
+//     to staging slot n (radii, codes, V, position); when that fills the page
+//     (n = 15) the 16 tokens become a tier-3 pagebuilder page
+//     (_flush_decode_page :2449-2475, build_page_from_codes: max-radius
+//     scales, int8 radius codes, LSB-first 3-bit codes) in sh's next decode
+//     slot, with its positions row and dim-major V page, the work items of sh
+//     take the new row (their end_row grows by one: the decode-time pointer
+//     table keeps dec_cap reserved rows right after each (seq, head)'s rows,
+//     their pointer-table rows and V slots set up front), and staging
+//     restarts empty.
+// Slots: wave w < 15 scores staged token w (w < n); wave 15 encodes and scores
+// the new token.
+struct TailArgs {
+  const void* k_new;        // [num_sh, DH] pre-RoPE, fp16 or fp32 (k_is_fp32)
+  const _Float16* v_new;    // [num_sh, DH]
+  const int32_t* cur_pos;   // [num_seqs]
+  float* stg_r;             // [num_sh, 16, DH/32]
+  int32_t* stg_code;        // [num_sh, 16, DH/32]
+  _Float16* stg_v;          // [num_sh, 16, DH]
+  int32_t* stg_pos;         // [num_sh, 16]
+  int32_t* state;           // [num_sh, 4]: staged count, decode pages, dropped tokens, 0
+  uint8_t* pages;
+  int32_t* positions;
+  _Float16* v_pool;
+  int32_t* work;            // [num_items, 4]: end_row of sh's items grows at a flush
+  int64_t dec_byte0;
+  int32_t dec_cap, dec_vpage0, k_is_fp32, mode, num_items, num_rows;
+};
+
+constexpr int kTailThreads = 1024;
+
+// Tier-3 radius of one 32-dim group x and its similarity with centroid row
+// cr, as torch CPU computes them for one token: norm = sqrt of the 8-lane
+// fmaf chains summed in order, dir = x / (norm + 1e-8), sim = sum_i dir_i *
+// c_i multiplied then added in order (explicit _rn operations: no
+// contraction).
+__device__ __forceinline__ float tail_sim32(const float* x, const float* cr, float& r_out) {
+  float acc[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) acc[l] = 0.f;
+#pragma unroll
+  for (int d = 0; d < 32; d += 8)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(x[d + l], x[d + l], acc[l]);
+  float b = acc[0];
+#pragma unroll
+  for (int l = 1; l < 8; ++l) b = __fadd_rn(b, acc[l]);
+  const float r = __builtin_sqrtf(b);
+  const float den = __fadd_rn(r, 1e-8f);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s = __fadd_rn(s, __fmul_rn(__fdiv_rn(x[i], den), cr[i]));
+  r_out = r;
+  return s;
+}
+
 template <int DH, int GQA>
-static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream) {
+__global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a, TailArgs t) {
+  constexpr int G3 = DH / 32, NJ = DH / 2, NS = kTailSlots;
+  constexpr int COLS = GQA * DH / 4;                   // float4 columns of one (seq, head)'s output
+  constexpr int IL = kTailThreads / COLS;              // item lanes
+  constexpr int UN = 4;                                // items per item lane per round trip
+  constexpr int PS = partial_stride<DH, GQA>();
+  static_assert(kTailThreads / 64 == NS, "one wave per tail slot");
+  static_assert(GQA * DH <= kTailThreads, "one thread per (head, dim)");
+  __shared__ float lg[NS][GQA];            // tail logits, log2 units (-inf: no token)
+  __shared__ float tr[NS][G3];             // tail radii (slot NS-1: the new token)
+  __shared__ int tc[NS][G3];               // tail codes
+  __shared__ int tp[NS];                   // tail positions
+  __shared__ float sims[G3][8];
+  __shared__ float tacc[GQA * DH];         // the tail's sum p V per (head, dim)
+  __shared__ float tml[GQA][2];            // the tail's (max, sum) per head
+  __shared__ float4 red_v[IL][COLS];
+  __shared__ float red_m[IL][COLS], red_l[IL][COLS];
+  __shared__ float scl[G3];
+  __shared__ __attribute__((aligned(16))) uint8_t pg[128];   // the flushed page
+
+  const int sh = blockIdx.x;
+  const int seq = sh / a.num_kv, h = sh % a.num_kv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool dec = (t.mode & kTailDecode) != 0;
+  const int32_t* stp = t.state + (int64_t)sh * kTailStateInts;
+  const int n_st = min(max(stp[0], 0), NS - 1);        // staged tokens
+  const int ndec = max(stp[1], 0);                     // decode pages flushed so far
+  const int pos_new = t.cur_pos[seq];
+  const float* cb3 = a.cb[3] + (int64_t)h * G3 * 8 * 32;
+
+  // ---- slot data: staged tokens (waves < n_st) and the new token's encode
+  //      (wave NS - 1, lane = (group, centroid)) --------------------------
+  if (wave < n_st) {
+    if (lane < G3) {
+      tr[wave][lane] = t.stg_r[((int64_t)sh * NS + wave) * G3 + lane];
+      tc[wave][lane] = min(max(t.stg_code[((int64_t)sh * NS + wave) * G3 + lane], 0), 7);
+    }
+    if (lane == 0) tp[wave] = t.stg_pos[(int64_t)sh * NS + wave];
+  } else if (wave == NS - 1) {
+    const int g = lane >> 3, c = lane & 7;
+    float r = 0.f;
+    if (g < G3) {
+      float x[32];
+      if (t.k_is_fp32) {
+        const float* src = static_cast<const float*>(t.k_new) + (int64_t)sh * DH + 32 * g;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = src[i];
+      } else {
+        const half8* src = reinterpret_cast<const half8*>(static_cast<const _Float16*>(t.k_new) + (int64_t)sh * DH + 32 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half8 hv = src[i];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)hv[e];
+        }
+      }
+      sims[g][c] = tail_sim32(x, cb3 + (g * 8 + c) * 32, r);
+    }
+    wave_lds_sync();
+    if (g < G3 && c == 0) {
+      // first maximum: the ascending scan with '>' (torch.argmax)
+      int best = 0;
+      float bs = sims[g][0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k)
+        if (sims[g][k] > bs) { bs = sims[g][k]; best = k; }
+      tr[NS - 1][g] = r;
+      tc[NS - 1][g] = best;
+    }
+    if (lane == 0) tp[NS - 1] = pos_new;
+  }
+  __syncthreads();
+
+  if (dec) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {        // malformed-page count: as the merge kernel
+      a.status[1] = a.status[0];
+      a.status[0] = 0u;
+    }
+    // ---- tail logits: wave w scores slot w; lane j = RoPE frequency --------
+    {
+      const bool present = wave < n_st || wave == NS - 1;
+      float part[GQA];
+      if (present) {
+        const int j = lane % NJ;
+        const bool act = lane < NJ;
+        const int g1 = j / 32, g2 = (j + NJ) / 32;
+        const float k1 = tr[wave][g1] * cb3[(g1 * 8 + tc[wave][g1]) * 32 + (j & 31)];
+        const float k2 = tr[wave][g2] * cb3[(g2 * 8 + tc[wave][g2]) * 32 + ((j + NJ) & 31)];
+        const double f = exp2(-(2.0 * j / DH) * a.log2_theta) * 0.15915494309189535;   // turns per token
+        const float2 z = turn_phasor((double)tp[wave] * f);
+        // R(pos) k_hat on the pair (j, j + NJ); <q, R(pos) k_hat> = <R(-pos) q, k_hat>
+        const float x0 = k1 * z.x - k2 * z.y, x1 = k2 * z.x + k1 * z.y;
+        const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+#pragma unroll
+        for (int hh = 0; hh < GQA; ++hh)
+          part[hh] = act ? (float)qh[hh * DH + j] * x0 + (float)qh[hh * DH + j + NJ] * x1 : 0.f;
+#pragma unroll
+        for (int hh = 0; hh < GQA; ++hh)
+#pragma unroll
+          for (int m = 32; m >= 1; m >>= 1) part[hh] += shfl_xor(part[hh], m);
+      }
+      if (lane == 0)
+#pragma unroll
+        for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = present ? part[hh] * a.scale_log2 : -INFINITY;
+    }
+    __syncthreads();
+    // ---- the tail's (max, sum, sum p V) per (head, dim), fp32 ---------------
+    {
+      const int i = threadIdx.x;
+      if (i < GQA * DH) {
+        const int hh = i / DH, d = i % DH;
+        float m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NS; ++w) m = fmaxf(m, lg[w][hh]);
+        float l = 0.f, acc = 0.f;
+        for (int w = 0; w < NS; ++w) {
+          const float x = lg[w][hh];
+          if (x == -INFINITY) continue;
+          const float p = __builtin_amdgcn_exp2f(x - m);
+          const _Float16 v = w == NS - 1 ? t.v_new[(int64_t)sh * DH + d] : t.stg_v[((int64_t)sh * NS + w) * DH + d];
+          l += p;
+          acc += p * (float)v;
+        }
+        tacc[i] = acc;
+        if (d == 0) {
+          tml[hh][0] = m;
+          tml[hh][1] = l;
+        }
+      }
+    }
+    // ---- log-sum-exp of the work items' partials and the tail --------------
+    {
+      const int ib = min(max(a.work_start[sh], 0), t.num_items);
+      const int ni = min(max(a.work_start[sh + 1], ib), t.num_items) - ib;
+      const int c = threadIdx.x % COLS, il = threadIdx.x / COLS;
+      const int f0 = 4 * c;
+      const int hh = f0 / DH;
+      float M = -INFINITY, Ls = 0.f;
+      float4 sum = {0.f, 0.f, 0.f, 0.f};
+      for (int it0 = il; it0 < ni; it0 += IL * UN) {
+        float4 v[UN];
+        float mi[UN], li[UN];
+#pragma unroll
+        for (int k = 0; k < UN; ++k) {
+          const int it = it0 + k * IL;
+          const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
+          mi[k] = it < ni ? pp[hh] : -INFINITY;
+          li[k] = pp[GQA + hh];
+          v[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
+        }
+        float Mn = M;
+#pragma unroll
+        for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, mi[k]);
+        if (Mn == -INFINITY) continue;
+        const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+        sum.x *= r; sum.y *= r; sum.z *= r; sum.w *= r;
+        Ls *= r;
+#pragma unroll
+        for (int k = 0; k < UN; ++k) {
+          const float f = (mi[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mi[k] - Mn);
+          Ls += f * li[k];
+          sum.x += f * v[k].x; sum.y += f * v[k].y; sum.z += f * v[k].z; sum.w += f * v[k].w;
+        }
+        M = Mn;
+      }
+      red_v[il][c] = sum;
+      red_m[il][c] = M;
+      red_l[il][c] = Ls;
+      __syncthreads();
+      if (il == 0) {
+        float Mx = tml[hh][0];
+        for (int k = 0; k < IL; ++k) Mx = fmaxf(Mx, red_m[k][c]);
+        float4 tot = {0.f, 0.f, 0.f, 0.f};
+        float Lt = 0.f;
+        if (Mx != -INFINITY) {
+          for (int k = 0; k < IL; ++k) {
+            const float mk = red_m[k][c];
+            if (mk == -INFINITY) continue;
+            const float f = __builtin_amdgcn_exp2f(mk - Mx);
+            const float4 x = red_v[k][c];
+            tot.x += f * x.x; tot.y += f * x.y; tot.z += f * x.z; tot.w += f * x.w;
+            Lt += f * red_l[k][c];
+          }
+          const float mt = tml[hh][0];
+          if (mt != -INFINITY) {
+            const float f = __builtin_amdgcn_exp2f(mt - Mx);
+            tot.x += f * tacc[f0]; tot.y += f * tacc[f0 + 1]; tot.z += f * tacc[f0 + 2]; tot.w += f * tacc[f0 + 3];
+            Lt += f * tml[hh][1];
+          }
+        }
+        const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+        half4 o;
+        o[0] = (_Float16)(tot.x * inv); o[1] = (_Float16)(tot.y * inv);
+        o[2] = (_Float16)(tot.z * inv); o[3] = (_Float16)(tot.w * inv);
+        *reinterpret_cast<half4*>(a.out + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH + f0) = o;
+      }
+    }
+  }
+  if (!(t.mode & kTailAppend)) return;
+
+  // ---- append the new token (_append_decode_kv) ----------------------------
+  __syncthreads();                                     // every read of sh's staging is done
+  const int i = threadIdx.x;
+  if (n_st < NS - 1) {
+    const int sl = n_st;
+    if (i < DH) t.stg_v[((int64_t)sh * NS + sl) * DH + i] = t.v_new[(int64_t)sh * DH + i];
+    if (i < G3) {
+      t.stg_r[((int64_t)sh * NS + sl) * G3 + i] = tr[NS - 1][i];
+      t.stg_code[((int64_t)sh * NS + sl) * G3 + i] = tc[NS - 1][i];
+    }
+    if (i == 0) {
+      t.stg_pos[(int64_t)sh * NS + sl] = pos_new;
+      t.state[(int64_t)sh * kTailStateInts] = sl + 1;
+    }
+    return;
+  }
+  if (ndec >= t.dec_cap) {                             // no decode slot left: the token is dropped
+    if (i == 0) t.state[(int64_t)sh * kTailStateInts + 2] = stp[2] + 1;
+    return;
+  }
+  // ---- the staged 15 tokens and the new one fill a page: flush it
+  //      (_flush_decode_page, build_page_from_codes, pagebuilder.py:8-42) -----
+  constexpr int TB = (NS * G3 * 3) / 8;                // theta bytes: 16 tokens x G3 codes x 3 bits
+  constexpr int PB = 8 + 4 * G3 + TB + NS * G3;        // page bytes
+  constexpr int SLOT = (PB + 15) & ~15;
+  const int k = sh * t.dec_cap + ndec;
+  const int ib = min(max(a.work_start[sh], 0), t.num_items);
+  const int ie = min(max(a.work_start[sh + 1], ib), t.num_items);
+  const int row = ie > ib ? t.work[4 * (int64_t)ib + 2] : -1;   // sh's next reserved row
+  if (row < 0 || row >= t.num_rows) {                  // no item or a corrupted list: drop
+    if (i == 0) t.state[(int64_t)sh * kTailStateInts + 2] = stp[2] + 1;
+    return;
+  }
+  if (i < G3) {                                        // r_scale[g] = max_n r[n, g]
+    float m = fabsf(tr[0][i]);
+    for (int n = 1; n < NS; ++n) {
+      const float x = fabsf(tr[n][i]);
+      if (x > m) m = x;
+    }
+    scl[i] = m;
+  }
+  __syncthreads();
+  if (i < SLOT) {
+    uint8_t byte = 0;
+    if (i == 0) byte = 3;                              // tier id
+    else if (i == 1) byte = NS;                        // count
+    else if (i >= 8 && i < 8 + 4 * G3) {
+      const uint32_t w = __builtin_bit_cast(uint32_t, scl[(i - 8) >> 2]);
+      byte = (uint8_t)(w >> (8 * ((i - 8) & 3)));
+    } else if (i >= 8 + 4 * G3 && i < 8 + 4 * G3 + TB) {
+      // LSB-first stream: bit j of item n*G3 + g at bit (n*G3 + g)*3 + j
+      const int b0 = 8 * (i - 8 - 4 * G3);
+#pragma unroll
+      for (int bb = 0; bb < 8; ++bb) {
+        const int gb = b0 + bb, item = gb / 3, j = gb % 3;
+        byte |= (uint8_t)(((tc[item / G3][item % G3] >> j) & 1) << bb);
+      }
+    } else if (i >= 8 + 4 * G3 + TB && i < PB) {
+      const int item = i - (8 + 4 * G3 + TB), n = item / G3, g = item % G3;
+      const float safe = scl[g] < 1e-8f ? 1e-8f : scl[g];
+      float qv = __builtin_rintf(__fmul_rn(__fdiv_rn(tr[n][g], safe), 127.0f));
+      qv = fminf(fmaxf(qv, -127.f), 127.f);
+      byte = (uint8_t)(int8_t)(int)qv;
+    }
+    pg[i] = byte;
+  }
+  __syncthreads();
+  if (i < SLOT / 4)
+    reinterpret_cast<uint32_t*>(t.pages + t.dec_byte0 + (int64_t)k * SLOT)[i] = reinterpret_cast<const uint32_t*>(pg)[i];
+  if (i < NS) t.positions[(int64_t)row * NS + i] = tp[i];
+  if (i < DH) {                                        // dim-major V page: element (token n, dim d) at d*16 + n
+    half8 lo, hi;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const _Float16 v = n == NS - 1 ? t.v_new[(int64_t)sh * DH + i] : t.stg_v[((int64_t)sh * NS + n) * DH + i];
+      if (n < 8) lo[n] = v; else hi[n - 8] = v;
+    }
+    half8* dst = reinterpret_cast<half8*>(t.v_pool + ((int64_t)t.dec_vpage0 + k) * (DH * NS) + (int64_t)i * NS);
+    dst[0] = lo;
+    dst[1] = hi;
+  }
+  for (int it = ib + i; it < ie; it += kTailThreads) t.work[4 * (int64_t)it + 2] = row + 1;   // sh's items take the row
+  if (i == 0) {
+    t.state[(int64_t)sh * kTailStateInts] = 0;
+    t.state[(int64_t)sh * kTailStateInts + 1] = ndec + 1;
+  }
+}
+
+// Decode-time pointer table (the layout sphkv_decode_step reads): the
+// prefill rows of (seq, head) sh, [row_start[sh], row_start[sh + 1]), move to
+// row p + sh * dec_cap, and dec_cap reserved rows follow them: reserved row k
+// of sh gets the pointer-table row of a full tier-3 page at bytes dec_byte0 +
+// (sh * dec_cap + k) * slot, V page dec_vpage0 + sh * dec_cap + k and
+// positions -1.  One thread per prefill row (its sh by binary search of
+// row_start) or per reserved row.
+__global__ __launch_bounds__(256) void tail_relayout_kernel(const int32_t* __restrict__ row_start, int32_t num_sh,
+                                                            int32_t num_rows, const int32_t* __restrict__ ptable,
+                                                            const int32_t* __restrict__ vslot,
+                                                            const int32_t* __restrict__ positions, int32_t dec_cap,
+                                                            int64_t dec_byte0, int32_t dec_vpage0, int32_t slot,
+                                                            int32_t G3, int32_t* __restrict__ ptable_d,
+                                                            int32_t* __restrict__ vslot_d,
+                                                            int32_t* __restrict__ positions_d) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nres = (int64_t)num_sh * dec_cap;
+  if (t < num_rows) {
+    const int p = (int)t;
+    int lo = 0, hi = num_sh;                           // last sh with row_start[sh] <= p
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (row_start[mid] <= p) lo = mid; else hi = mid;
+    }
+    const int64_t r = (int64_t)p + (int64_t)lo * dec_cap;   // < num_rows + nres: lo < num_sh
+    ptable_d[3 * r] = ptable[3 * (int64_t)p];
+    ptable_d[3 * r + 1] = ptable[3 * (int64_t)p + 1];
+    ptable_d[3 * r + 2] = ptable[3 * (int64_t)p + 2];
+    vslot_d[r] = vslot[p];
+    for (int i = 0; i < kTile; ++i) positions_d[r * kTile + i] = positions[(int64_t)p * kTile + i];
+  } else if (t < num_rows + nres) {
+    const int64_t q = t - num_rows;
+    const int sh = (int)(q / dec_cap), k = (int)(q % dec_cap);
+    const int64_t r = (int64_t)row_start[sh + 1] + (int64_t)sh * dec_cap + k;
+    if (r < 0 || r >= num_rows + nres) return;         // row_start not a table of num_rows rows
+    const int64_t off = dec_byte0 + q * slot;
+    ptable_d[3 * r] = (int32_t)off;
+    ptable_d[3 * r + 1] = (int32_t)(off + 8 + 4 * G3);
+    ptable_d[3 * r + 2] = (int32_t)(off + 8 + 4 * G3 + 6 * G3);
+    vslot_d[r] = (int32_t)(dec_vpage0 + q);
+    for (int i = 0; i < kTile; ++i) positions_d[r * kTile + i] = -1;
+  }
+}
+
+int launch_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,
+                         const int32_t* vslot, const int32_t* positions, int32_t dec_cap, int64_t dec_byte0,
+                         int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d,
+                         int32_t* positions_d, hipStream_t stream) {
+  const int64_t n = (int64_t)num_rows + (int64_t)num_sh * dec_cap;
+  if (n > 0)
+    hipLaunchKernelGGL(tail_relayout_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, row_start,
+                       num_sh, num_rows, ptable, vslot, positions, dec_cap, dec_byte0, dec_vpage0,
+                       tail_slot_bytes(dh), dh / 32, ptable_d, vslot_d, positions_d);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int DH, int GQA>
+static DecodeArgs decode_args(const DecodeLaunch& L) {
   DecodeArgs a;
   a.pages = L.pages; a.pages_bytes = L.pages_bytes; a.ptable = L.ptable; a.vslot = L.vslot;
   a.positions = L.positions; a.v_pool = reinterpret_cast<const _Float16*>(L.v_pool);
   a.num_vpages = L.num_vpages; a.cb[0] = nullptr; a.cb[1] = L.cb1; a.cb[2] = L.cb2; a.cb[3] = L.cb3;
   a.work = L.work; a.work_start = L.work_start; a.q = reinterpret_cast<const _Float16*>(L.q);
   a.out = reinterpret_cast<_Float16*>(L.out); a.partials = L.partials;
-  a.status = reinterpret_cast<uint32_t*>(L.partials + (int64_t)L.num_items * partial_stride<DH, GQA>());
+  a.status = L.partials ? reinterpret_cast<uint32_t*>(L.partials + (int64_t)L.num_items * partial_stride<DH, GQA>())
+                         : nullptr;
   a.num_kv = L.num_kv; a.num_rows = L.num_rows; a.num_sh = L.num_seqs * L.num_kv;
   a.pages32 = (int32_t)L.pages_bytes;
   a.pages_m8 = (int32_t)L.pages_bytes - 8;
@@ -1002,6 +1420,12 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   a.scale_log2 = L.sm_scale * 1.4426950408889634f;
   a.scale_log2_c = a.scale_log2 * (1.0f / 127.0f);
   a.log2_theta = __builtin_log2(L.rope_theta);
+  return a;
+}
+
+template <int DH, int GQA>
+static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream) {
+  const DecodeArgs a = decode_args<DH, GQA>(L);
   if (L.num_items > 0) {
     if (phases & kPhasePartials)
       hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream,
@@ -1017,6 +1441,33 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
 
 int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream) {
 #define SPHKV_DISPATCH(D, Q) if (L.dh == D && L.gqa == Q) return launch_decode_t<D, Q>(L, phases, stream);
+  SPHKV_DISPATCH(128, 1) SPHKV_DISPATCH(128, 2) SPHKV_DISPATCH(128, 4) SPHKV_DISPATCH(128, 8)
+  SPHKV_DISPATCH(64, 1) SPHKV_DISPATCH(64, 2) SPHKV_DISPATCH(64, 4) SPHKV_DISPATCH(64, 8)
+#undef SPHKV_DISPATCH
+  return -1;
+}
+
+template <int DH, int GQA>
+static int launch_decode_tail_t(const DecodeLaunch& L, const TailLaunch& T, hipStream_t stream) {
+  const DecodeArgs a = decode_args<DH, GQA>(L);
+  TailArgs t;
+  t.k_new = T.k_new; t.v_new = reinterpret_cast<const _Float16*>(T.v_new); t.cur_pos = T.cur_pos;
+  t.stg_r = T.stg_r; t.stg_code = T.stg_code; t.stg_v = reinterpret_cast<_Float16*>(T.stg_v);
+  t.stg_pos = T.stg_pos; t.state = T.state; t.pages = T.pages; t.positions = T.positions;
+  t.v_pool = reinterpret_cast<_Float16*>(T.v_pool); t.work = T.work; t.dec_byte0 = T.dec_byte0;
+  t.dec_cap = T.dec_cap; t.dec_vpage0 = T.dec_vpage0; t.k_is_fp32 = T.k_is_fp32;
+  t.mode = T.mode; t.num_items = L.num_items; t.num_rows = L.num_rows;
+  const int nsh = L.num_seqs * L.num_kv;
+  if ((T.mode & kTailDecode) && L.num_items > 0)
+    hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream,
+                       L.work, L.num_items, a);
+  if (nsh > 0)
+    hipLaunchKernelGGL((decode_tail_kernel<DH, GQA>), dim3(nsh), dim3(kTailThreads), 0, stream, a, t);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_decode_tail(const DecodeLaunch& L, const TailLaunch& T, hipStream_t stream) {
+#define SPHKV_DISPATCH(D, Q) if (L.dh == D && L.gqa == Q) return launch_decode_tail_t<D, Q>(L, T, stream);
   SPHKV_DISPATCH(128, 1) SPHKV_DISPATCH(128, 2) SPHKV_DISPATCH(128, 4) SPHKV_DISPATCH(128, 8)
   SPHKV_DISPATCH(64, 1) SPHKV_DISPATCH(64, 2) SPHKV_DISPATCH(64, 4) SPHKV_DISPATCH(64, 8)
 #undef SPHKV_DISPATCH

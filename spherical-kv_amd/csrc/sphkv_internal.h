@@ -30,6 +30,28 @@ struct DecodeLaunch {
   int32_t dh; float sm_scale; double rope_theta;
 };
 
+// Decode-time tail of the Mode-B path (spherical_kv_pipeline.py:2248-2342,
+// 2389-2475): per (sequence, kv head) up to kTailSlots - 1 staged tokens
+// (tier-3 codes, fp32 radii, fp16 V, positions) and the step's new token.
+// Decode page k of (seq, head) sh lives at bytes dec_byte0 + (sh * dec_cap +
+// k) * tail_slot_bytes(dh) and V page dec_vpage0 + sh * dec_cap + k; its
+// pointer-table row is the row after sh's last one (the work items' end_row),
+// reserved with those offsets when the decode-time table was laid out.
+constexpr int kTailSlots = 16;
+constexpr int kTailDecode = 1;      // score the tail in the step's softmax, write out
+constexpr int kTailAppend = 2;      // append the new token (flush a full page)
+constexpr int kTailStateInts = 4;   // per (seq, head): staged count, decode pages, dropped tokens, 0
+inline int tail_page_bytes(int dh) { return 8 + 26 * (dh / 32); }          // tier 3, 16 tokens
+inline int tail_slot_bytes(int dh) { return (tail_page_bytes(dh) + 15) & ~15; }
+
+struct TailLaunch {
+  const void* k_new; int32_t k_is_fp32; const uint16_t* v_new; const int32_t* cur_pos;
+  float* stg_r; int32_t* stg_code; uint16_t* stg_v; int32_t* stg_pos; int32_t* state;
+  uint8_t* pages; int32_t* positions; uint16_t* v_pool; int32_t* work;
+  int64_t dec_byte0; int32_t dec_cap, dec_vpage0;
+  int32_t mode;
+};
+
 struct RaggedLaunch {
   const uint8_t* pages; int64_t pages_bytes; const int32_t* ptable; const int32_t* head_ids;
   const int32_t* positions; int32_t num_pages; const float* cos_tbl; const float* sin_tbl;
@@ -120,6 +142,13 @@ int launch_encode(const EncodeLaunch& L, hipStream_t stream);
 constexpr int kPhasePartials = 1;
 constexpr int kPhaseMerge = 2;
 int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream);
+// The decode kernel over prefill + decode-page rows (mode & kTailDecode),
+// then the tail kernel: merge, tail terms, output, append / flush.
+int launch_decode_tail(const DecodeLaunch& L, const TailLaunch& T, hipStream_t stream);
+int launch_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,
+                         const int32_t* vslot, const int32_t* positions, int32_t dec_cap, int64_t dec_byte0,
+                         int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d,
+                         int32_t* positions_d, hipStream_t stream);
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream);
 
 // fp32 elements of one work item's partial: 16 (m, l, padding) + gqa * dh

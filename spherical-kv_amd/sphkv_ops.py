@@ -461,6 +461,184 @@ def merge_partials(pool: PagedPool, workspace: torch.Tensor, gqa: int,
     return out
 
 
+TAIL_SLOTS = 16          # staged tokens + the new one: one decode page
+
+
+def tail_slot_bytes(dh: int) -> int:
+    """Bytes of one decode-page slot: a 16-token tier-3 page, 16-byte aligned."""
+    return (fmt.page_nbytes(3, TAIL_SLOTS, dh) + 15) & ~15
+
+
+class DecodeTail:
+    """Decode-time state of a pool for full reference decode steps
+    (_compressed_head_attention_batched + _append_decode_kv,
+    spherical_kv_pipeline.py:2057-2475): per (sequence, kv head) the staged
+    tokens (tier-3 codes, fp32 radii, fp16 V, positions; at most 15), room
+    for `capacity` decode pages in the pool, and the decode-time pointer
+    table, positions, V slots and work list in which each (seq, head)'s
+    reserved rows follow its prefill rows (sphkv_tail_relayout).  A flush
+    writes the page, its positions and V, and extends that (seq, head)'s work
+    items by one row, all on the device.
+
+    Attaching grows the pool's byte pool and V pool (copies once) when they
+    have no room for the decode pages.  Every (seq, head) stages one token per
+    step, so the host tracks the staged count and flushed pages exactly and
+    raises before a step would need a decode slot past `capacity`."""
+
+    def __init__(self, pool: "PagedPool", capacity: int = 64, rows_per_item: Optional[int] = None):
+        plan = pool.plan
+        dev = pool.device
+        if capacity < 0:
+            raise ValueError("capacity must be >= 0")
+        if pool.codebooks.get(3) is None:
+            raise ValueError("decode steps need the tier-3 codebook (decode tokens are tier 3)")
+        self.pool, self.capacity = pool, int(capacity)
+        self.num_sh = num_sh = plan.num_seqs * plan.num_kv
+        dh = plan.dh
+        G3 = dh // 32
+        slot = tail_slot_bytes(dh)
+        nres = num_sh * self.capacity
+        # decode pages after the prefill pool's bytes and V pages
+        self.dec_byte0 = (plan.pages_bytes + 15) & ~15
+        self.dec_vpage0 = plan.num_vpages
+        need_b, need_v = self.dec_byte0 + nres * slot, plan.num_vpages + nres
+        if pool.pages.numel() < need_b:
+            grown = torch.zeros(need_b, dtype=torch.uint8, device=dev)
+            grown[:pool.pages.numel()].copy_(pool.pages)
+            pool.pages = grown
+        if pool.v_pool.shape[0] < need_v:
+            grown = torch.zeros((need_v, pool.v_pool.shape[1]), dtype=torch.float16, device=dev)
+            grown[:pool.v_pool.shape[0]].copy_(pool.v_pool)
+            pool.v_pool = grown
+        self.pages_bytes = int(pool.pages.numel())
+        self.num_vpages = int(pool.v_pool.shape[0])
+        # decode-time table: prefill rows of sh shifted by sh * capacity, then sh's reserved rows
+        self.num_rows = plan.num_rows + nres
+        rs = _row_start32(plan.row_start)
+        rs_dev = torch.as_tensor(rs, device=dev)
+        self.ptable = torch.empty((max(self.num_rows, 1), 3), dtype=torch.int32, device=dev)
+        self.vslot = torch.empty(max(self.num_rows, 1), dtype=torch.int32, device=dev)
+        self.positions = torch.empty((max(self.num_rows, 1), 16), dtype=torch.int32, device=dev)
+        rc = load().sphkv_tail_relayout(rs_dev.data_ptr(), num_sh, plan.num_rows, pool.ptable.data_ptr(),
+                                        pool.vslot.data_ptr(), pool.positions.data_ptr(), self.capacity,
+                                        self.dec_byte0, self.dec_vpage0, dh, self.ptable.data_ptr(),
+                                        self.vslot.data_ptr(), self.positions.data_ptr(), _stream())
+        check(rc, "sphkv_tail_relayout")
+        # the work list over the prefill rows, in the decode-time row numbering
+        if rows_per_item is None:
+            rows_per_item = auto_rows_per_item(rs, torch.cuda.get_device_properties(dev).multi_processor_count)
+        w, ws = make_work(rs, rows_per_item)
+        shift = w[:, 0].astype(np.int64) * self.capacity
+        w[:, 1] = (w[:, 1] + shift).astype(np.int32)
+        w[:, 2] = (w[:, 2] + shift).astype(np.int32)
+        self.work = torch.as_tensor(np.ascontiguousarray(w), device=dev)
+        self.work_start = torch.as_tensor(ws, device=dev)
+        self.num_items = int(w.shape[0])
+        # staging
+        self.stg_r = torch.zeros((num_sh, TAIL_SLOTS, G3), dtype=torch.float32, device=dev)
+        self.stg_code = torch.zeros((num_sh, TAIL_SLOTS, G3), dtype=torch.int32, device=dev)
+        self.stg_v = torch.zeros((num_sh, TAIL_SLOTS, dh), dtype=torch.float16, device=dev)
+        self.stg_pos = torch.zeros((num_sh, TAIL_SLOTS), dtype=torch.int32, device=dev)
+        self.state = torch.zeros((num_sh, 4), dtype=torch.int32, device=dev)
+        self.staged = 0          # tokens staged per (seq, head) (host mirror)
+        self.flushed = 0         # decode pages per (seq, head) (host mirror)
+
+    def workspace_bytes(self, gqa: int) -> int:
+        n = load().sphkv_decode_paged_workspace_bytes(self.num_items, gqa, self.pool.plan.dh)
+        if n < 0:
+            raise ValueError("bad gqa / dh for the decode workspace")
+        return int(n)
+
+    def _advance(self) -> None:
+        if self.staged == TAIL_SLOTS - 1 and self.flushed >= self.capacity:
+            raise ValueError(f"no decode-page slot left (capacity {self.capacity} pages per (seq, head))")
+
+    def _committed(self) -> None:
+        self.staged += 1
+        if self.staged == TAIL_SLOTS:
+            self.staged, self.flushed = 0, self.flushed + 1
+
+    def _step_inputs(self, k_new: torch.Tensor, v_new: torch.Tensor, cur_pos: torch.Tensor):
+        plan, dev = self.pool.plan, self.pool.device
+        if k_new.dtype not in (torch.float16, torch.float32):
+            raise TypeError("k_new must be fp16 or fp32")
+        _need(k_new, k_new.dtype, "k_new", dev)
+        _need(v_new, torch.float16, "v_new", dev)
+        _need(cur_pos, torch.int32, "cur_pos", dev)
+        want = (plan.num_seqs, plan.num_kv, plan.dh)
+        if tuple(k_new.shape) != want or tuple(v_new.shape) != want:
+            raise ValueError(f"k_new and v_new must be {want}")
+        if tuple(cur_pos.shape) != (plan.num_seqs,):
+            raise ValueError("cur_pos must be [num_seqs]")
+
+    def state_host(self) -> Dict[str, np.ndarray]:
+        """Copies of the tail state (waits for the current stream)."""
+        return {"state": self.state.cpu().numpy(), "stg_r": self.stg_r.cpu().numpy(),
+                "stg_code": self.stg_code.cpu().numpy(), "stg_v": self.stg_v.cpu().numpy(),
+                "stg_pos": self.stg_pos.cpu().numpy(), "work": self.work.cpu().numpy()}
+
+
+def decode_step(pool: "PagedPool", tail: DecodeTail, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                cur_pos: torch.Tensor, gqa: int, rope_theta: float, sm_scale: Optional[float] = None,
+                out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                append: bool = True) -> torch.Tensor:
+    """One reference decode step on the GPU (sphkv_decode_step): attention of
+    q over the prefill pages, the flushed decode pages, the staged tokens and
+    the new token (k_new pre-RoPE [num_seqs, num_kv, dh] fp16/fp32, v_new fp16,
+    cur_pos int32 [num_seqs]); then, with append, the new token is staged
+    (and a full page flushed).  Returns out fp16 [num_seqs, num_kv*gqa, dh]."""
+    plan = pool.plan
+    _check_q(pool, q, gqa)
+    tail._step_inputs(k_new, v_new, cur_pos)
+    if append:
+        tail._advance()
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.float16, "out", pool.device)
+    if out.shape != q.shape:
+        raise ValueError("out must match q")
+    wsb = tail.workspace_bytes(gqa)
+    if workspace is None:
+        workspace = torch.zeros(max(wsb, 4), dtype=torch.uint8, device=pool.device)
+    _need(workspace, torch.uint8, "workspace", pool.device)
+    if workspace.numel() < wsb:
+        raise ValueError(f"workspace needs {wsb} bytes, got {workspace.numel()}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(plan.dh)
+    c1, c2, c3 = pool.cb_ptrs()
+    rc = load().sphkv_decode_step(
+        pool.pages.data_ptr(), tail.pages_bytes, tail.ptable.data_ptr(), tail.vslot.data_ptr(),
+        tail.positions.data_ptr(), tail.num_rows, pool.v_pool.data_ptr(), tail.num_vpages, c1, c2, c3,
+        tail.work.data_ptr(), tail.num_items, tail.work_start.data_ptr(), plan.num_seqs, plan.num_kv, gqa,
+        q.data_ptr(), k_new.data_ptr(), 1 if k_new.dtype == torch.float32 else 0, v_new.data_ptr(),
+        cur_pos.data_ptr(), tail.stg_r.data_ptr(), tail.stg_code.data_ptr(), tail.stg_v.data_ptr(),
+        tail.stg_pos.data_ptr(), tail.state.data_ptr(), tail.dec_byte0, tail.dec_vpage0, tail.capacity,
+        1 if append else 0, out.data_ptr(), workspace.data_ptr(), workspace.numel(), plan.dh, plan.page_size,
+        float(sm_scale), float(rope_theta), _stream())
+    check(rc, "sphkv_decode_step")
+    if append:
+        tail._committed()
+    return out
+
+
+def decode_append(pool: "PagedPool", tail: DecodeTail, k_new: torch.Tensor, v_new: torch.Tensor,
+                  cur_pos: torch.Tensor) -> None:
+    """_append_decode_kv for every (seq, head) (sphkv_decode_append): stage the
+    new tokens, flushing full pages; no attention."""
+    plan = pool.plan
+    tail._step_inputs(k_new, v_new, cur_pos)
+    tail._advance()
+    rc = load().sphkv_decode_append(
+        pool.pages.data_ptr(), tail.pages_bytes, tail.positions.data_ptr(), tail.num_rows, pool.v_pool.data_ptr(),
+        tail.num_vpages, _ptr(pool.codebooks.get(3)), tail.work.data_ptr(), tail.num_items,
+        tail.work_start.data_ptr(), plan.num_seqs, plan.num_kv, k_new.data_ptr(),
+        1 if k_new.dtype == torch.float32 else 0, v_new.data_ptr(), cur_pos.data_ptr(), tail.stg_r.data_ptr(),
+        tail.stg_code.data_ptr(), tail.stg_v.data_ptr(), tail.stg_pos.data_ptr(), tail.state.data_ptr(),
+        tail.dec_byte0, tail.dec_vpage0, tail.capacity, plan.dh, plan.page_size, _stream())
+    check(rc, "sphkv_decode_append")
+    tail._committed()
+
+
 @dataclass
 class DevicePlan:
     """A page plan built on the GPU by plan_pages_gpu.  Per-row arrays stay on

@@ -229,6 +229,32 @@ def make_decode_workload(config: int, seed: Optional[int] = None, ctx_override: 
                     tier_of=tier_of, plan=plan)
 
 
+@dataclass
+class TailSteps:
+    """Inputs of T decode steps after a workload's context: the tier-3
+    codebook that decode tokens are encoded with, and per step the new
+    pre-RoPE keys and V rows of every (sequence, kv head), their positions
+    (each sequence continues from its length) and the step's queries."""
+    cb3: np.ndarray      # fp32 [num_kv, dh/32, 8, 32], unit rows
+    k: np.ndarray        # fp16 [T, num_seqs, num_kv, dh]
+    v: np.ndarray        # fp16 [T, num_seqs, num_kv, dh]
+    pos: np.ndarray      # int32 [T, num_seqs]
+    q: np.ndarray        # fp16 [T, num_seqs, num_kv*gqa, dh]
+
+
+def make_tail_steps(wl: Workload, steps: int, seed: int = 77) -> TailSteps:
+    """Decode-step inputs for wl (a generator of its own, so the workload's
+    draws are unchanged).  K of the new tokens: N(0,1) fp16."""
+    rng = np.random.default_rng(seed)
+    cb3 = make_codebooks(rng, wl.num_kv, wl.dh, [3])[3]
+    shp = (steps, wl.num_seqs, wl.num_kv, wl.dh)
+    k = rng.standard_normal(shp).astype(np.float16)
+    v = rng.standard_normal(shp).astype(np.float16)
+    pos = (np.asarray(wl.lengths, np.int64)[None, :] + np.arange(steps)[:, None]).astype(np.int32)
+    q = rng.standard_normal((steps, wl.num_seqs, wl.num_kv * wl.gqa, wl.dh)).astype(np.float16)
+    return TailSteps(cb3=cb3, k=k, v=v, pos=pos, q=q)
+
+
 def make_encode_workload(seed: int = 3, tokens: int = 8192, num_kv: int = 8, dh: int = 128) -> Workload:
     """Config 3: 8192 new pre-RoPE K tokens x 8 KV heads, N(0,1) x per-channel
     lognormal(0, 0.5), 1 % of channels x 8, per (head, token) 70/30 tier 1/2."""

@@ -17,6 +17,8 @@ Recorded with every encode case: torch version and the fp64 top-2 similarity
 margin of every group (a margin of a few 1e-7 is where summation order decides
 the argmax).  The t1_n1_tie* cases are single-token tier-1 pages built on
 near-ties: they pin the summation order of torch's N = 1 path (MKL M = 1).
+tail_golden.npz holds single-token tier-3 encodes (near-ties and ordinary
+tokens): the decode-time tail's encode of each new key.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -108,6 +110,51 @@ def tie_case(name, rng, dh=128, tries=4096):
             f"{name}__meta": np.array([1, 1, g, b, dh], np.int64)}
 
 
+def tie3_case(name, rng, dh=128, tries=4096):
+    """One single-token tier-3 encode (N = 1, g = 32, C = 8: the decode-time
+    encode of _append_decode_kv / the new token, spherical_kv_pipeline.py:
+    2311-2313, 2423-2425; N*g*C = 256 < 400 takes torch's naive bmm loop)
+    whose every group sits on a near-tie between two centroids, built as
+    tie_case builds the tier-1 ones."""
+    g, b = 32, 3
+    G, C = dh // g, 2 ** b
+    cb = rng.standard_normal((G, C, g))
+    cb = (cb / np.linalg.norm(cb, axis=-1, keepdims=True)).astype(np.float32)
+    K = np.zeros((1, dh), np.float16)
+    for gi in range(G):
+        a, bb = rng.choice(C, size=2, replace=False)
+        base = cb[gi, a].astype(np.float64) + cb[gi, bb].astype(np.float64)
+        base *= rng.uniform(1.0, 8.0) / np.linalg.norm(base)
+        cand = (base[None, :] * (1.0 + 2e-3 * rng.standard_normal((tries, g)))).astype(np.float16)
+        d = cand.astype(np.float64)
+        d /= np.linalg.norm(d, axis=-1, keepdims=True) + EPS
+        s = d @ cb[gi].astype(np.float64).T
+        top = np.sort(s, axis=-1)
+        pick = int(np.argmin(top[:, -1] - top[:, -2]))
+        K[0, gi * g:(gi + 1) * g] = cand[pick]
+    Kt = torch.from_numpy(K.astype(np.float32))
+    r, codes = t_encode(Kt, torch.from_numpy(cb), g, G)
+    return {f"{name}__K": K, f"{name}__cb": cb, f"{name}__r": r.numpy(), f"{name}__codes": codes.numpy(),
+            f"{name}__margin": margins(K, cb, g, G).astype(np.float64),
+            f"{name}__meta": np.array([1, 3, g, b, dh], np.int64)}
+
+
+def tail_fixtures():
+    """Single-token tier-3 encodes (the decode-time tail's), tails_golden.npz:
+    24 near-tie tokens at dh 128 and 12 at dh 64, plus 32 ordinary tokens."""
+    rng = np.random.default_rng(20261203)
+    out = {}
+    for i in range(24):
+        out.update(tie3_case(f"t3_n1_tie{i}", rng, dh=128))
+    for i in range(12):
+        out.update(tie3_case(f"t3_n1_tie_dh64_{i}", rng, dh=64))
+    for i in range(32):
+        out.update(encode_case(f"t3_n1_plain{i}", rng, 1, 3, 32, 3, dh=128 if i % 4 else 64,
+                               kind="config3" if i % 2 else "normal"))
+    out["torch_version"] = np.array(torch.__version__)
+    return out
+
+
 def decode_case(name, rng, n_tok, gqa, dh, theta=500000.0):
     """Torch fp32 restatement of the Mode-B reference decode on one KV head
     with one tier-1 block, positions spread over [0, 40000)."""
@@ -176,6 +223,7 @@ def main():
     dec.update(decode_case("d128_g8", rng, 100, 8, 128))
     dec["torch_version"] = np.array(torch.__version__)
     np.savez_compressed(os.path.join(HERE, "decode_golden.npz"), **dec)
+    np.savez_compressed(os.path.join(HERE, "tail_golden.npz"), **tail_fixtures())
     print("wrote", sorted(os.listdir(HERE)))
 
 
