@@ -540,6 +540,130 @@ def bench_prefill(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_step(args, dev):
+    """The headline: one full reference decode step per timed step
+    (_compressed_head_attention_batched + _append_decode_kv,
+    spherical_kv_pipeline.py:2057-2475) through the bound step plan: the
+    paged decode kernel over the context pages and the decode pages flushed
+    so far, then the tail kernel (log-sum-exp merge with the staged tokens
+    and the new token, output, append / flush).  The contexts grow by one
+    token per step; algorithmic bytes are counted per step from each pool's
+    exact tail state."""
+    log(f"[bench] building config{args.config} workload")
+    wl = synth.make_decode_workload(args.config, layout=args.layout,
+                                    kv_device=dev if args.config in (4, 5) else None)
+    n_in = 16                                        # rotating sets of new-token inputs
+    st = synth.make_tail_steps(wl, n_in)
+    wl.codebooks[3] = st.cb3
+    pool0, _, _ = ops.build_pool_gpu(wl, dev)
+    pools = [pool0] + [clone_pool(pool0) for _ in range(args.rotate - 1)]
+    R = len(pools)
+    appends = args.warmup + 2 * args.steps             # appending steps: warmup, timed, kernel-timed
+    per_pool = -(-appends // R)
+    cap = per_pool // ops.TAIL_SLOTS + 2
+    tails = [ops.DecodeTail(p, wl.gqa, wl.rope_theta, capacity=cap) for p in pools]
+    torch.cuda.synchronize()
+    num_sh = wl.num_seqs * wl.num_kv
+    q = torch.as_tensor(wl.q, device=dev)
+    out = torch.empty_like(q)
+    kin = torch.as_tensor(st.k, device=dev)
+    vin = torch.as_tensor(st.v, device=dev)
+    # positions: pool p's j-th appending step is at length + j
+    posbuf = torch.as_tensor((np.asarray(wl.lengths, np.int64)[None, :] + np.arange(per_pool + 1)[:, None])
+                             .astype(np.int32), device=dev)
+    runs = [t.runner() for t in tails]
+    kstride, pstride = kin[0].numel() * 2, wl.num_seqs * 4
+    qp, op, kp, vp, pp = q.data_ptr(), out.data_ptr(), kin.data_ptr(), vin.data_ptr(), posbuf.data_ptr()
+    done = [0] * R                                     # appending steps taken per pool
+
+    def step(i, mode=3):
+        p = i % R
+        j = done[p]
+        runs[p](qp, kp + (i % n_in) * kstride, 0, vp + (i % n_in) * kstride, pp + j * pstride, op, mode)
+        if mode & 2:
+            done[p] = j + 1
+
+    base = fmt.decode_bytes(wl.plan)
+    dh, G3 = wl.dh, wl.dh // 32
+    dec_page = fmt.page_nbytes(3, 16, dh) + 16 * dh * 2 + 64 + 12          # K page, V, positions, ptable row
+    stg_tok = 4 * G3 + 4 * G3 + 2 * dh + 4                                 # radii, codes, V, position
+    new_tok = 2 * dh * 2                                                   # k_new, v_new
+
+    def step_bytes(p):
+        j = done[p]
+        kern = base + num_sh * (j // 16) * dec_page
+        return kern, kern + num_sh * ((j % 16) * stg_tok + new_tok)
+
+    log(f"[bench] rows={wl.plan.num_rows} items={tails[0].num_items} pools={R} decode-page capacity={cap}")
+    # untimed settle without appending (the contexts do not grow)
+    settle(lambda i: step(i, 1))
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    tot_bytes = 0
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        tot_bytes += step_bytes(i % R)[1]
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    us = ms * 1e3
+    nbytes = tot_bytes / args.steps
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+
+    # the dominant kernel: the decode kernel of K more steps, each launch
+    # timed by its own kernel-only timestamps (hipExtLaunchKernel events)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for e0, e1 in evs:
+        e0.record()
+        e1.record()
+    torch.cuda.synchronize()
+    kb = 0
+    for i in range(args.steps):
+        kb += step_bytes(i % R)[0]
+        ops.time_next_decode_kernel(*evs[i])
+        step(i)
+    torch.cuda.synchronize()
+    kern_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / args.steps
+    kbytes = kb / args.steps
+    kern_gbps = kbytes / (kern_ms * 1e-3) / 1e9
+    log(f"[bench] decode_kernel {kern_ms * 1e3:.2f} us (kernel-only timestamps)  {kern_gbps:.1f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (torch restatement of the reference path)")
+        cpu = cpu_baseline(wl, pool0)
+        log(f"[bench] CPU {cpu['value']} us/step on {cpu['cores']} threads")
+    line = {
+        "metric": METRICS[args.config], "value": round(us, 3), "unit": "µs/decode step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 I/O; fp32 rotation, QK and softmax; P rounded to fp16 for the fp32-accumulated PV",
+        "data": "synthetic (seeded generator, config spec of BASELINE.json)",
+        "achieved_hbm_gbps": round(gbps, 1),
+        "config": {"workload": f"config{args.config}: {wl.num_q} q / {wl.num_kv} kv heads, dh {wl.dh}, "
+                               f"{wl.num_seqs} seq x {max(wl.lengths)} ctx, 16-token pages, tier mix of BASELINE; "
+                               f"full decode step: page context + staged tokens + new token, then the append",
+                   "num_seqs": wl.num_seqs, "ctx": max(wl.lengths), "pages": wl.plan.num_rows,
+                   "rotated_pools": R, "algorithmic_bytes_per_step": round(nbytes),
+                   "kernels_per_step": ["decode_kernel", "decode_tail_kernel"]},
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": measured_traffic(args.config, args.layout),
+                     "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
+                     "kernel_timing": "kernel-only start/stop timestamps of each launch (hipExtLaunchKernel), "
+                                      "the duration rocprofv3's kernel trace reports",
+                     "numerator": "algorithmic bytes of the kernel's launch (pages, dense K, V, positions, "
+                                  "pointer-table rows)",
+                     "step_frac": round(gbps / PEAK_HBM_GBPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -551,9 +675,10 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE)
     ap.add_argument("--layout", default="default", choices=["default", "sequential"],
                     help="page placement: the config's own (random for configs 2-5) or sequential")
-    ap.add_argument("--path", default="modeb", choices=["modeb", "modea", "prefill", "ragged"],
-                    help="modeb: the angle-domain paged decode (the headline); modea: LayerPool decode; "
-                         "prefill: device page plan + fused encode")
+    ap.add_argument("--path", default="step", choices=["step", "pages", "modea", "prefill", "ragged"],
+                    help="step: the full Mode-B decode step (page context + staged tokens + new token, then "
+                         "the append; the headline); pages: the page-resident decode alone; modea: LayerPool "
+                         "decode; prefill: device page plan + fused encode; ragged: fused_decode_ragged")
     ap.add_argument("--page-size", type=int, default=16, help="Mode-A page size (16..128, multiple of 16)")
     ap.add_argument("--calibrate", action="store_true",
                     help="after timing, run plain device copies of COPY_BYTES (torch copy_), the "
@@ -581,6 +706,10 @@ def main():
     if args.config == 3:
         print("bench.py: config 3 is the encode workload; use --path prefill --config 3", file=sys.stderr)
         sys.exit(2)
+
+    if args.path == "step":
+        bench_step(args, dev)
+        return
 
     log(f"[bench] building config{args.config} workload")
     # configs 4 and 5 draw their K / V on the device (gigabytes of rows)

@@ -227,6 +227,16 @@ int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, 
                                 int32_t gqa, int32_t dh, uint16_t* out, void* stream);
 
 /*
+ * Measurement hook, no reference counterpart: the next launch of the paged
+ * decode kernel on the calling thread (by sphkv_decode_paged, _checked,
+ * _partials, _noalloc or sphkv_decode_step) records its own start and stop
+ * time in the two hipEvent_t the caller created (hipExtLaunchKernel), so
+ * hipEventElapsedTime gives that kernel's duration without the gaps between
+ * launches, the figure rocprofv3's kernel trace reports.  NULL, NULL cancels.
+ */
+int sphkv_time_next_decode_kernel(void* start_event, void* stop_event);
+
+/*
  * ---- Decode-time tail of the Mode-B path ---------------------------------
  * A full decode step of the reference: _compressed_head_attention_batched
  * (spherical_kv_pipeline.py:2057-2369; multi-head form _decode_layer_all_heads
@@ -295,6 +305,32 @@ int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable
                       int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t append,
                       uint16_t* out, void* workspace, int64_t workspace_bytes,
                       int32_t dh, int32_t page_size, float sm_scale, double rope_theta, void* stream);
+
+/*
+ * A bound decode step (no reference counterpart: the reference re-derives
+ * its tensors in Python every step).  sphkv_step_plan_create validates every
+ * static argument of sphkv_decode_step once (same meaning; staged / flushed
+ * give the tail's current counts, 0 for a fresh tail) and keeps them with
+ * the host's mirror of the tail counts; sphkv_step_plan_run then takes only
+ * the per-step inputs: mode 1 = decode (no append), 2 = append only
+ * (sphkv_decode_append), 3 = decode and append.  A run that would need a
+ * decode page past dec_cap fails (SPHKV_EINVAL) before launching.  Runs of
+ * one plan must be issued from one thread at a time.
+ */
+typedef struct sphkv_step_plan sphkv_step_plan;
+int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable, const int32_t* vslot,
+                           int32_t* positions, int32_t num_rows, uint16_t* v_pool, int64_t num_vpages,
+                           const float* cb1, const float* cb2, const float* cb3,
+                           int32_t* work, int32_t num_items, const int32_t* work_start,
+                           int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                           float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos, int32_t* tail_state,
+                           int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t staged, int32_t flushed,
+                           void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
+                           double rope_theta, sphkv_step_plan** plan_out);
+int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_new, int32_t k_is_fp32,
+                        const uint16_t* v_new, const int32_t* cur_pos, uint16_t* out, int32_t mode, void* stream);
+int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed);
+void sphkv_step_plan_destroy(sphkv_step_plan* plan);
 
 /*
  * _append_decode_kv alone (spherical_kv_pipeline.py:2389-2448, flush

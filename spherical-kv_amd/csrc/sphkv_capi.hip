@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <new>
 
 #include "../../include/sphkv.h"
 #include "sphkv_internal.h"
@@ -359,6 +360,111 @@ int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions,
   sphkv::TailLaunch T{k_new, k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state,
                       pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, sphkv::kTailAppend};
   return launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"
+
+// A bound decode step: every static argument of sphkv_decode_step, validated
+// once, and the host's mirror of the tail counts (every (seq, head) stages
+// one token per appending step).
+struct sphkv_step_plan {
+  sphkv::DecodeLaunch L;
+  sphkv::TailLaunch T;
+  int64_t workspace_bytes;
+  int32_t staged, flushed;
+};
+
+extern "C" {
+
+int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable, const int32_t* vslot,
+                           int32_t* positions, int32_t num_rows, uint16_t* v_pool, int64_t num_vpages,
+                           const float* cb1, const float* cb2, const float* cb3,
+                           int32_t* work, int32_t num_items, const int32_t* work_start,
+                           int32_t num_seqs, int32_t num_kv, int32_t gqa,
+                           float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos, int32_t* tail_state,
+                           int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t staged, int32_t flushed,
+                           void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
+                           double rope_theta, sphkv_step_plan** plan_out) {
+  const char* fn = "sphkv_step_plan_create";
+  if (!plan_out) return fail(SPHKV_EINVAL, "%s: null plan_out", fn);
+  *plan_out = nullptr;
+  // the step's per-call inputs are checked for presence at run time; here a
+  // stand-in address lets the shared checks run
+  static const uint16_t probe[1] = {0};
+  int rc = sphkv_decode_step(nullptr, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages, cb1,
+                             cb2, cb3, work, num_items, work_start, 0, num_kv, gqa, probe, probe, 0, probe,
+                             nullptr, stg_r, stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap,
+                             1, nullptr, workspace, workspace_bytes, dh, page_size, sm_scale, rope_theta, nullptr);
+  if (rc != SPHKV_OK) return rc;                    // size / shape checks (num_seqs = 0: no launch)
+  if (num_seqs <= 0) return fail(SPHKV_EINVAL, "%s: num_seqs must be > 0", fn);
+  rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, probe, probe,
+                   reinterpret_cast<const int32_t*>(probe), stg_r, stg_code, stg_v, stg_pos, tail_state, dec_byte0,
+                   dec_vpage0, dec_cap, dh);
+  if (rc != SPHKV_OK) return rc;
+  const int64_t need = sphkv_decode_paged_workspace_bytes(num_items, gqa, dh);
+  if (workspace_bytes < need)
+    return fail(SPHKV_EINVAL, "%s: workspace too small (%lld < %lld bytes)", fn, (long long)workspace_bytes,
+                (long long)need);
+  if (num_items < num_seqs * num_kv) return fail(SPHKV_EINVAL, "%s: need at least one work item per (seq, head)", fn);
+  if (!work_start || !workspace || !work || !pages || !ptable || !vslot || !positions || !v_pool)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  if (staged < 0 || staged >= sphkv::kTailSlots || flushed < 0 || flushed > dec_cap)
+    return fail(SPHKV_EINVAL, "%s: staged must be 0..15 and flushed 0..dec_cap", fn);
+  auto* p = new (std::nothrow) sphkv_step_plan;
+  if (!p) return fail(SPHKV_EINVAL, "%s: out of host memory", fn);
+  p->L = sphkv::DecodeLaunch{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
+                             cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, nullptr, nullptr,
+                             static_cast<float*>(workspace), dh, sm_scale, rope_theta};
+  p->T = sphkv::TailLaunch{nullptr, 0, nullptr, nullptr, stg_r, stg_code, stg_v, stg_pos, tail_state,
+                           pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, 0};
+  p->workspace_bytes = workspace_bytes;
+  p->staged = staged;
+  p->flushed = flushed;
+  *plan_out = p;
+  return ok();
+}
+
+int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_new, int32_t k_is_fp32,
+                        const uint16_t* v_new, const int32_t* cur_pos, uint16_t* out, int32_t mode, void* stream) {
+  const char* fn = "sphkv_step_plan_run";
+  if (!plan) return fail(SPHKV_EINVAL, "%s: null plan", fn);
+  if (mode < 1 || mode > 3) return fail(SPHKV_EINVAL, "%s: mode must be 1 (decode), 2 (append) or 3 (both)", fn);
+  const bool dec = mode & sphkv::kTailDecode, app = mode & sphkv::kTailAppend;
+  if (!k_new || !v_new || !cur_pos || (dec && (!q || !out))) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  if (app && plan->staged == sphkv::kTailSlots - 1 && plan->flushed >= plan->T.dec_cap)
+    return fail(SPHKV_EINVAL, "%s: no decode-page slot left (capacity %d pages per (seq, head))", fn,
+                plan->T.dec_cap);
+  sphkv::DecodeLaunch L = plan->L;
+  L.q = q;
+  L.out = out;
+  sphkv::TailLaunch T = plan->T;
+  T.k_new = k_new;
+  T.k_is_fp32 = k_is_fp32 ? 1 : 0;
+  T.v_new = v_new;
+  T.cur_pos = cur_pos;
+  T.mode = mode;
+  const int rc = launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
+  if (rc == SPHKV_OK && app && ++plan->staged == sphkv::kTailSlots) {
+    plan->staged = 0;
+    ++plan->flushed;
+  }
+  return rc;
+}
+
+int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed) {
+  if (!plan || !staged || !flushed) return fail(SPHKV_EINVAL, "sphkv_step_plan_counts: null argument");
+  *staged = plan->staged;
+  *flushed = plan->flushed;
+  return ok();
+}
+
+void sphkv_step_plan_destroy(sphkv_step_plan* plan) { delete plan; }
+
+int sphkv_time_next_decode_kernel(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(SPHKV_EINVAL, "sphkv_time_next_decode_kernel: give both events or neither");
+  sphkv::set_decode_timing(static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+  return ok();
 }
 
 int sphkv_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,

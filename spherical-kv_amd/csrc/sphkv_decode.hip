@@ -48,10 +48,32 @@
 //      convex combination of V rows;
 //   6. O[h][d] += P[h][t] V[t][d] on MFMA (4x4x4 f16, 16 blocks of 4 dims),
 //      V read in the pool's MFMA operand order.
+#include <hip/hip_ext.h>
+
 #include "sphkv_common.h"
 #include "sphkv_internal.h"
 
 namespace sphkv {
+
+// Events the next decode_kernel launch on this thread records its own start
+// and stop in (hipExtLaunchKernel), then forgets (sphkv_time_next_decode_kernel).
+thread_local hipEvent_t g_time_start = nullptr, g_time_stop = nullptr;
+
+void set_decode_timing(hipEvent_t start, hipEvent_t stop) {
+  g_time_start = start;
+  g_time_stop = stop;
+}
+
+// decode_kernel launch, with the kernel-only timestamps when they were asked for
+template <typename K, typename... A>
+static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t stream, A... args) {
+  if (g_time_start && g_time_stop) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, g_time_start, g_time_stop, 0, args...);
+    g_time_start = g_time_stop = nullptr;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+  }
+}
 
 struct DecodeArgs {
   const uint8_t* pages;
@@ -1033,31 +1055,6 @@ struct TailArgs {
 
 constexpr int kTailThreads = 1024;
 
-// Tier-3 radius of one 32-dim group x and its similarity with centroid row
-// cr, as torch CPU computes them for one token: norm = sqrt of the 8-lane
-// fmaf chains summed in order, dir = x / (norm + 1e-8), sim = sum_i dir_i *
-// c_i multiplied then added in order (explicit _rn operations: no
-// contraction).
-__device__ __forceinline__ float tail_sim32(const float* x, const float* cr, float& r_out) {
-  float acc[8];
-#pragma unroll
-  for (int l = 0; l < 8; ++l) acc[l] = 0.f;
-#pragma unroll
-  for (int d = 0; d < 32; d += 8)
-#pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(x[d + l], x[d + l], acc[l]);
-  float b = acc[0];
-#pragma unroll
-  for (int l = 1; l < 8; ++l) b = __fadd_rn(b, acc[l]);
-  const float r = __builtin_sqrtf(b);
-  const float den = __fadd_rn(r, 1e-8f);
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) s = __fadd_rn(s, __fmul_rn(__fdiv_rn(x[i], den), cr[i]));
-  r_out = r;
-  return s;
-}
-
 template <int DH, int GQA>
 __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a, TailArgs t) {
   constexpr int G3 = DH / 32, NJ = DH / 2, NS = kTailSlots;
@@ -1065,13 +1062,17 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   constexpr int IL = kTailThreads / COLS;              // item lanes
   constexpr int UN = 4;                                // items per item lane per round trip
   constexpr int PS = partial_stride<DH, GQA>();
+  constexpr int NCB = G3 * 8 * 32;                     // tier-3 codebook floats of one kv head
   static_assert(kTailThreads / 64 == NS, "one wave per tail slot");
-  static_assert(GQA * DH <= kTailThreads, "one thread per (head, dim)");
+  static_assert(GQA * DH <= kTailThreads && NCB <= kTailThreads && NS * DH / 8 <= kTailThreads, "thread maps");
+  __shared__ float cbs[NCB];               // the head's tier-3 codebook
+  __shared__ __attribute__((aligned(16))) _Float16 vs[NS][DH];   // V of the tail slots
   __shared__ float lg[NS][GQA];            // tail logits, log2 units (-inf: no token)
   __shared__ float tr[NS][G3];             // tail radii (slot NS-1: the new token)
   __shared__ int tc[NS][G3];               // tail codes
   __shared__ int tp[NS];                   // tail positions
   __shared__ float sims[G3][8];
+  __shared__ float kn[DH];                 // the new token's pre-RoPE key
   __shared__ float tacc[GQA * DH];         // the tail's sum p V per (head, dim)
   __shared__ float tml[GQA][2];            // the tail's (max, sum) per head
   __shared__ float4 red_v[IL][COLS];
@@ -1081,190 +1082,237 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
 
   const int sh = blockIdx.x;
   const int seq = sh / a.num_kv, h = sh % a.num_kv;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
   const bool dec = (t.mode & kTailDecode) != 0;
   const int32_t* stp = t.state + (int64_t)sh * kTailStateInts;
   const int n_st = min(max(stp[0], 0), NS - 1);        // staged tokens
   const int ndec = max(stp[1], 0);                     // decode pages flushed so far
   const int pos_new = t.cur_pos[seq];
-  const float* cb3 = a.cb[3] + (int64_t)h * G3 * 8 * 32;
+  const float* cb3 = a.cb[3] + (int64_t)h * NCB;
 
-  // ---- slot data: staged tokens (waves < n_st) and the new token's encode
-  //      (wave NS - 1, lane = (group, centroid)) --------------------------
-  if (wave < n_st) {
-    if (lane < G3) {
-      tr[wave][lane] = t.stg_r[((int64_t)sh * NS + wave) * G3 + lane];
-      tc[wave][lane] = min(max(t.stg_code[((int64_t)sh * NS + wave) * G3 + lane], 0), 7);
+  // ---- every load that depends only on sh is issued first ------------------
+  // the work items' partials (one round trip after the item range)
+  const int ib = min(max(a.work_start[sh], 0), t.num_items);
+  const int ie = min(max(a.work_start[sh + 1], ib), t.num_items);
+  const int ni = ie - ib;
+  const int c = i % COLS, il = i / COLS;
+  const int f0 = 4 * c, hc = f0 / DH;                  // first float of this column, its head
+  float4 pv[UN];
+  float pm[UN], pl[UN];
+  if (dec) {
+#pragma unroll
+    for (int k = 0; k < UN; ++k) {
+      const int it = il + k * IL;
+      const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
+      pm[k] = it < ni ? pp[hc] : -INFINITY;
+      pl[k] = pp[GQA + hc];
+      pv[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
     }
-    if (lane == 0) tp[wave] = t.stg_pos[(int64_t)sh * NS + wave];
-  } else if (wave == NS - 1) {
-    const int g = lane >> 3, c = lane & 7;
-    float r = 0.f;
-    if (g < G3) {
+  }
+  // codebook (one float per thread), V of the tail slots (16 bytes per
+  // thread), staged radii / codes / positions
+  const float cbv = i < NCB ? cb3[i] : 0.f;
+  half8 vrow;
+  if (i < NS * DH / 8) {
+    const int w = i / (DH / 8), c8 = i % (DH / 8);
+    const _Float16* src = w == NS - 1 ? t.v_new + (int64_t)sh * DH : t.stg_v + ((int64_t)sh * NS + w) * DH;
+    vrow = *reinterpret_cast<const half8*>(src + 8 * c8);
+  }
+  float sr = 0.f;
+  int sc = 0, sp = 0;
+  if (i < (NS - 1) * G3) {
+    sr = t.stg_r[(int64_t)sh * NS * G3 + i];
+    sc = t.stg_code[(int64_t)sh * NS * G3 + i];
+  }
+  if (i < NS - 1) sp = t.stg_pos[(int64_t)sh * NS + i];
+  // this lane's query pair (j, j + NJ) of every head (the logits)
+  const int j = lane % NJ;
+  float qa[GQA], qb[GQA];
+  if (dec) {
+    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+#pragma unroll
+    for (int hh = 0; hh < GQA; ++hh) {
+      qa[hh] = (float)qh[hh * DH + j];
+      qb[hh] = (float)qh[hh * DH + j + NJ];
+    }
+  }
+  // the new token's key, fp32 (the encode reads it from LDS)
+  float kv = 0.f;
+  if (i < DH)
+    kv = t.k_is_fp32 ? static_cast<const float*>(t.k_new)[(int64_t)sh * DH + i]
+                     : (float)static_cast<const _Float16*>(t.k_new)[(int64_t)sh * DH + i];
+  // RoPE frequency of lane j in turns per token (formed while the loads fly)
+  const double fj = exp2(-(2.0 * j / DH) * a.log2_theta) * 0.15915494309189535;
+
+  // ---- shared tables ---------------------------------------------------------
+  if (i < NCB) cbs[i] = cbv;
+  if (i < NS * DH / 8) *reinterpret_cast<half8*>(&vs[i / (DH / 8)][8 * (i % (DH / 8))]) = vrow;
+  if (i < (NS - 1) * G3) {
+    tr[i / G3][i % G3] = sr;
+    tc[i / G3][i % G3] = min(max(sc, 0), 7);
+  }
+  if (i < NS - 1) tp[i] = sp;
+  if (i < DH) kn[i] = kv;
+  if (i == 0) tp[NS - 1] = pos_new;
+  __syncthreads();
+  if (wave == NS - 1) {
+    // the new token through the tier-3 codebook (_encode_keys_with_codebooks
+    // on one token, torch CPU order; N*g*C = 256 < 400 takes ATen's naive
+    // loop: multiply, then add, in order); lane = (group eg, centroid ec)
+    const int eg = lane >> 3, ec = lane & 7;
+    float r_enc = 0.f;
+    if (eg < G3) {
       float x[32];
-      if (t.k_is_fp32) {
-        const float* src = static_cast<const float*>(t.k_new) + (int64_t)sh * DH + 32 * g;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = src[i];
-      } else {
-        const half8* src = reinterpret_cast<const half8*>(static_cast<const _Float16*>(t.k_new) + (int64_t)sh * DH + 32 * g);
+      for (int k = 0; k < 32; ++k) x[k] = kn[32 * eg + k];
+      r_enc = torch_norm(x, 32);
+      group_directions<32>(x, __fadd_rn(r_enc, 1e-8f), !t.k_is_fp32, x);    // x becomes dir
+      const float* cr = cbs + (eg * 8 + ec) * 32;
+      float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const half8 hv = src[i];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)hv[e];
-        }
-      }
-      sims[g][c] = tail_sim32(x, cb3 + (g * 8 + c) * 32, r);
+      for (int k = 0; k < 32; ++k) s = __fadd_rn(s, __fmul_rn(x[k], cr[k]));
+      sims[eg][ec] = s;
     }
     wave_lds_sync();
-    if (g < G3 && c == 0) {
+    if (eg < G3 && ec == 0) {
       // first maximum: the ascending scan with '>' (torch.argmax)
       int best = 0;
-      float bs = sims[g][0];
+      float bs = sims[eg][0];
 #pragma unroll
       for (int k = 1; k < 8; ++k)
-        if (sims[g][k] > bs) { bs = sims[g][k]; best = k; }
-      tr[NS - 1][g] = r;
-      tc[NS - 1][g] = best;
+        if (sims[eg][k] > bs) { bs = sims[eg][k]; best = k; }
+      tr[NS - 1][eg] = r_enc;
+      tc[NS - 1][eg] = best;
     }
-    if (lane == 0) tp[NS - 1] = pos_new;
+    wave_lds_sync();
   }
-  __syncthreads();
 
   if (dec) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) {        // malformed-page count: as the merge kernel
+    if (blockIdx.x == 0 && i == 0) {                   // malformed-page count: as the merge kernel
       a.status[1] = a.status[0];
       a.status[0] = 0u;
     }
-    // ---- tail logits: wave w scores slot w; lane j = RoPE frequency --------
+    // ---- tail logits: wave w scores slot w; lane j = RoPE frequency ---------
     {
       const bool present = wave < n_st || wave == NS - 1;
-      float part[GQA];
       if (present) {
-        const int j = lane % NJ;
         const bool act = lane < NJ;
         const int g1 = j / 32, g2 = (j + NJ) / 32;
-        const float k1 = tr[wave][g1] * cb3[(g1 * 8 + tc[wave][g1]) * 32 + (j & 31)];
-        const float k2 = tr[wave][g2] * cb3[(g2 * 8 + tc[wave][g2]) * 32 + ((j + NJ) & 31)];
-        const double f = exp2(-(2.0 * j / DH) * a.log2_theta) * 0.15915494309189535;   // turns per token
-        const float2 z = turn_phasor((double)tp[wave] * f);
-        // R(pos) k_hat on the pair (j, j + NJ); <q, R(pos) k_hat> = <R(-pos) q, k_hat>
+        const float k1 = tr[wave][g1] * cbs[(g1 * 8 + tc[wave][g1]) * 32 + (j & 31)];
+        const float k2 = tr[wave][g2] * cbs[(g2 * 8 + tc[wave][g2]) * 32 + ((j + NJ) & 31)];
+        const float2 z = turn_phasor((double)tp[wave] * fj);
+        // R(pos) k_hat on the pair (j, j + NJ): <q, R(pos) k_hat> = <R(-pos) q, k_hat>
         const float x0 = k1 * z.x - k2 * z.y, x1 = k2 * z.x + k1 * z.y;
-        const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+        float part[GQA];
 #pragma unroll
-        for (int hh = 0; hh < GQA; ++hh)
-          part[hh] = act ? (float)qh[hh * DH + j] * x0 + (float)qh[hh * DH + j + NJ] * x1 : 0.f;
+        for (int hh = 0; hh < GQA; ++hh) part[hh] = act ? qa[hh] * x0 + qb[hh] * x1 : 0.f;
 #pragma unroll
         for (int hh = 0; hh < GQA; ++hh)
 #pragma unroll
           for (int m = 32; m >= 1; m >>= 1) part[hh] += shfl_xor(part[hh], m);
-      }
-      if (lane == 0)
+        if (lane == 0)
 #pragma unroll
-        for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = present ? part[hh] * a.scale_log2 : -INFINITY;
-    }
-    __syncthreads();
-    // ---- the tail's (max, sum, sum p V) per (head, dim), fp32 ---------------
-    {
-      const int i = threadIdx.x;
-      if (i < GQA * DH) {
-        const int hh = i / DH, d = i % DH;
-        float m = -INFINITY;
+          for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = part[hh] * a.scale_log2;
+      } else if (lane == 0) {
 #pragma unroll
-        for (int w = 0; w < NS; ++w) m = fmaxf(m, lg[w][hh]);
-        float l = 0.f, acc = 0.f;
-        for (int w = 0; w < NS; ++w) {
-          const float x = lg[w][hh];
-          if (x == -INFINITY) continue;
-          const float p = __builtin_amdgcn_exp2f(x - m);
-          const _Float16 v = w == NS - 1 ? t.v_new[(int64_t)sh * DH + d] : t.stg_v[((int64_t)sh * NS + w) * DH + d];
-          l += p;
-          acc += p * (float)v;
-        }
-        tacc[i] = acc;
-        if (d == 0) {
-          tml[hh][0] = m;
-          tml[hh][1] = l;
-        }
+        for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = -INFINITY;
       }
     }
-    // ---- log-sum-exp of the work items' partials and the tail --------------
+    // ---- the work items' log-sum-exp (partials already in registers) ---------
     {
-      const int ib = min(max(a.work_start[sh], 0), t.num_items);
-      const int ni = min(max(a.work_start[sh + 1], ib), t.num_items) - ib;
-      const int c = threadIdx.x % COLS, il = threadIdx.x / COLS;
-      const int f0 = 4 * c;
-      const int hh = f0 / DH;
       float M = -INFINITY, Ls = 0.f;
       float4 sum = {0.f, 0.f, 0.f, 0.f};
-      for (int it0 = il; it0 < ni; it0 += IL * UN) {
-        float4 v[UN];
-        float mi[UN], li[UN];
+      for (int it0 = il, r0 = 0; it0 < ni; it0 += IL * UN, ++r0) {
+        if (r0 > 0) {                                  // more than IL * UN items: next round trip
 #pragma unroll
-        for (int k = 0; k < UN; ++k) {
-          const int it = it0 + k * IL;
-          const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
-          mi[k] = it < ni ? pp[hh] : -INFINITY;
-          li[k] = pp[GQA + hh];
-          v[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
+          for (int k = 0; k < UN; ++k) {
+            const int it = it0 + k * IL;
+            const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
+            pm[k] = it < ni ? pp[hc] : -INFINITY;
+            pl[k] = pp[GQA + hc];
+            pv[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
+          }
         }
         float Mn = M;
 #pragma unroll
-        for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, mi[k]);
+        for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, pm[k]);
         if (Mn == -INFINITY) continue;
         const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
         sum.x *= r; sum.y *= r; sum.z *= r; sum.w *= r;
         Ls *= r;
 #pragma unroll
         for (int k = 0; k < UN; ++k) {
-          const float f = (mi[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mi[k] - Mn);
-          Ls += f * li[k];
-          sum.x += f * v[k].x; sum.y += f * v[k].y; sum.z += f * v[k].z; sum.w += f * v[k].w;
+          const float f = (pm[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[k] - Mn);
+          Ls += f * pl[k];
+          sum.x += f * pv[k].x; sum.y += f * pv[k].y; sum.z += f * pv[k].z; sum.w += f * pv[k].w;
         }
         M = Mn;
       }
       red_v[il][c] = sum;
       red_m[il][c] = M;
       red_l[il][c] = Ls;
-      __syncthreads();
-      if (il == 0) {
-        float Mx = tml[hh][0];
-        for (int k = 0; k < IL; ++k) Mx = fmaxf(Mx, red_m[k][c]);
-        float4 tot = {0.f, 0.f, 0.f, 0.f};
-        float Lt = 0.f;
-        if (Mx != -INFINITY) {
-          for (int k = 0; k < IL; ++k) {
-            const float mk = red_m[k][c];
-            if (mk == -INFINITY) continue;
-            const float f = __builtin_amdgcn_exp2f(mk - Mx);
-            const float4 x = red_v[k][c];
-            tot.x += f * x.x; tot.y += f * x.y; tot.z += f * x.z; tot.w += f * x.w;
-            Lt += f * red_l[k][c];
-          }
-          const float mt = tml[hh][0];
-          if (mt != -INFINITY) {
-            const float f = __builtin_amdgcn_exp2f(mt - Mx);
-            tot.x += f * tacc[f0]; tot.y += f * tacc[f0 + 1]; tot.z += f * tacc[f0 + 2]; tot.w += f * tacc[f0 + 3];
-            Lt += f * tml[hh][1];
-          }
-        }
-        const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-        half4 o;
-        o[0] = (_Float16)(tot.x * inv); o[1] = (_Float16)(tot.y * inv);
-        o[2] = (_Float16)(tot.z * inv); o[3] = (_Float16)(tot.w * inv);
-        *reinterpret_cast<half4*>(a.out + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH + f0) = o;
+    }
+    __syncthreads();
+    // ---- the tail's (max, sum, sum p V) per (head, dim), fp32 ---------------
+    if (i < GQA * DH) {
+      const int hh = i / DH, d = i % DH;
+      float m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NS; ++w) m = fmaxf(m, lg[w][hh]);
+      float l = 0.f, acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < NS; ++w) {
+        const float xw = lg[w][hh];
+        const float p = xw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(xw - m);
+        l += p;
+        acc += p * (float)vs[w][d];
       }
+      tacc[i] = acc;
+      if (d == 0) {
+        tml[hh][0] = m;
+        tml[hh][1] = l;
+      }
+    }
+    __syncthreads();
+    if (il == 0) {
+      float Mx = tml[hc][0];
+      for (int k = 0; k < IL; ++k) Mx = fmaxf(Mx, red_m[k][c]);
+      float4 tot = {0.f, 0.f, 0.f, 0.f};
+      float Lt = 0.f;
+      if (Mx != -INFINITY) {
+        for (int k = 0; k < IL; ++k) {
+          const float mk = red_m[k][c];
+          if (mk == -INFINITY) continue;
+          const float f = __builtin_amdgcn_exp2f(mk - Mx);
+          const float4 xk = red_v[k][c];
+          tot.x += f * xk.x; tot.y += f * xk.y; tot.z += f * xk.z; tot.w += f * xk.w;
+          Lt += f * red_l[k][c];
+        }
+        const float mt = tml[hc][0];
+        if (mt != -INFINITY) {
+          const float f = __builtin_amdgcn_exp2f(mt - Mx);
+          tot.x += f * tacc[f0]; tot.y += f * tacc[f0 + 1]; tot.z += f * tacc[f0 + 2]; tot.w += f * tacc[f0 + 3];
+          Lt += f * tml[hc][1];
+        }
+      }
+      const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+      half4 o;
+      o[0] = (_Float16)(tot.x * inv); o[1] = (_Float16)(tot.y * inv);
+      o[2] = (_Float16)(tot.z * inv); o[3] = (_Float16)(tot.w * inv);
+      *reinterpret_cast<half4*>(a.out + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH + f0) = o;
     }
   }
   if (!(t.mode & kTailAppend)) return;
 
   // ---- append the new token (_append_decode_kv) ----------------------------
-  __syncthreads();                                     // every read of sh's staging is done
-  const int i = threadIdx.x;
+  // (every staged value was read into LDS before the first barrier; this one
+  // orders the new token's encode, wave NS - 1, before the reads below)
+  __syncthreads();
   if (n_st < NS - 1) {
     const int sl = n_st;
-    if (i < DH) t.stg_v[((int64_t)sh * NS + sl) * DH + i] = t.v_new[(int64_t)sh * DH + i];
+    if (i < DH / 8)
+      *reinterpret_cast<half8*>(t.stg_v + ((int64_t)sh * NS + sl) * DH + 8 * i) =
+          *reinterpret_cast<const half8*>(&vs[NS - 1][8 * i]);
     if (i < G3) {
       t.stg_r[((int64_t)sh * NS + sl) * G3 + i] = tr[NS - 1][i];
       t.stg_code[((int64_t)sh * NS + sl) * G3 + i] = tc[NS - 1][i];
@@ -1285,8 +1333,6 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   constexpr int PB = 8 + 4 * G3 + TB + NS * G3;        // page bytes
   constexpr int SLOT = (PB + 15) & ~15;
   const int k = sh * t.dec_cap + ndec;
-  const int ib = min(max(a.work_start[sh], 0), t.num_items);
-  const int ie = min(max(a.work_start[sh + 1], ib), t.num_items);
   const int row = ie > ib ? t.work[4 * (int64_t)ib + 2] : -1;   // sh's next reserved row
   if (row < 0 || row >= t.num_rows) {                  // no item or a corrupted list: drop
     if (i == 0) t.state[(int64_t)sh * kTailStateInts + 2] = stp[2] + 1;
@@ -1295,8 +1341,8 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   if (i < G3) {                                        // r_scale[g] = max_n r[n, g]
     float m = fabsf(tr[0][i]);
     for (int n = 1; n < NS; ++n) {
-      const float x = fabsf(tr[n][i]);
-      if (x > m) m = x;
+      const float xn = fabsf(tr[n][i]);
+      if (xn > m) m = xn;
     }
     scl[i] = m;
   }
@@ -1313,8 +1359,8 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
       const int b0 = 8 * (i - 8 - 4 * G3);
 #pragma unroll
       for (int bb = 0; bb < 8; ++bb) {
-        const int gb = b0 + bb, item = gb / 3, j = gb % 3;
-        byte |= (uint8_t)(((tc[item / G3][item % G3] >> j) & 1) << bb);
+        const int gb = b0 + bb, item = gb / 3, jb = gb % 3;
+        byte |= (uint8_t)(((tc[item / G3][item % G3] >> jb) & 1) << bb);
       }
     } else if (i >= 8 + 4 * G3 + TB && i < PB) {
       const int item = i - (8 + 4 * G3 + TB), n = item / G3, g = item % G3;
@@ -1333,8 +1379,7 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
     half8 lo, hi;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
-      const _Float16 v = n == NS - 1 ? t.v_new[(int64_t)sh * DH + i] : t.stg_v[((int64_t)sh * NS + n) * DH + i];
-      if (n < 8) lo[n] = v; else hi[n - 8] = v;
+      if (n < 8) lo[n] = vs[n][i]; else hi[n - 8] = vs[n][i];
     }
     half8* dst = reinterpret_cast<half8*>(t.v_pool + ((int64_t)t.dec_vpage0 + k) * (DH * NS) + (int64_t)i * NS);
     dst[0] = lo;
@@ -1428,8 +1473,8 @@ static int launch_decode_t(const DecodeLaunch& L, int phases, hipStream_t stream
   const DecodeArgs a = decode_args<DH, GQA>(L);
   if (L.num_items > 0) {
     if (phases & kPhasePartials)
-      hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream,
-                         L.work, L.num_items, a);
+      launch_timed(decode_kernel<DH, GQA>, dim3(L.num_items), dim3(decode_waves<GQA>() * 64), stream, L.work,
+                   L.num_items, a);
     const int nsh = L.num_seqs * L.num_kv;
     if ((phases & kPhaseMerge) && nsh > 0)
       hipLaunchKernelGGL((decode_merge_kernel<DH, GQA>), dim3(nsh * ((GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128))),
@@ -1459,8 +1504,8 @@ static int launch_decode_tail_t(const DecodeLaunch& L, const TailLaunch& T, hipS
   t.mode = T.mode; t.num_items = L.num_items; t.num_rows = L.num_rows;
   const int nsh = L.num_seqs * L.num_kv;
   if ((T.mode & kTailDecode) && L.num_items > 0)
-    hipLaunchKernelGGL((decode_kernel<DH, GQA>), dim3(L.num_items), dim3(decode_waves<GQA>() * 64), 0, stream,
-                       L.work, L.num_items, a);
+    launch_timed(decode_kernel<DH, GQA>, dim3(L.num_items), dim3(decode_waves<GQA>() * 64), stream, L.work,
+                 L.num_items, a);
   if (nsh > 0)
     hipLaunchKernelGGL((decode_tail_kernel<DH, GQA>), dim3(nsh), dim3(kTailThreads), 0, stream, a, t);
   return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -65,45 +65,6 @@ __device__ __forceinline__ void load_group(const EncodeArgs& a, int64_t row, int
   }
 }
 
-// torch CPU fp32 L2 norm of a contiguous group (ATen vectorised last-dim
-// reduction, 8 lanes, fused multiply-add accumulation, lanes summed in order).
-__device__ __forceinline__ float torch_norm(const float* x, int g) {
-  float acc[8];
-  for (int l = 0; l < 8; ++l) acc[l] = 0.f;
-  for (int d = 0; d < g; d += 8)
-    for (int l = 0; l < 8; ++l) acc[l] = __builtin_fmaf(x[d + l], x[d + l], acc[l]);
-  float b = acc[0];
-  for (int l = 1; l < 8; ++l) b = __fadd_rn(b, acc[l]);
-  return __builtin_sqrtf(b);  // correctly rounded expansion (v_sqrt_f32 alone is not)
-}
-
-// dir[i] = x[i] / den, correctly rounded, for the GG values of one group
-// (den = the group's norm + 1e-8 > 0).  The division's own sequence is a
-// reciprocal of den refined once, then the quotient refined twice, framed by
-// operand scaling and a special-value fixup; with fp16 inputs (x = 0 or
-// 2^-24 <= |x| <= den) and a finite den, neither the scaling nor the fixup
-// changes anything (no operand or quotient is denormal or near overflow), so
-// the same steps run with the reciprocal shared by the group and give the
-// same bits.  (The fixup gives a zero quotient the sign of x; copysign does
-// here.)  Other inputs divide each value on its own.
-template <int GG>
-__device__ __forceinline__ void group_directions(const float* x, float den, bool fp16_in, float* dir) {
-  if (fp16_in && den < 1e30f) {
-    const float r0 = __builtin_amdgcn_rcpf(den);
-    const float r = __builtin_fmaf(__builtin_fmaf(-den, r0, 1.0f), r0, r0);
-#pragma unroll
-    for (int i = 0; i < GG; ++i) {
-      const float q = __fmul_rn(x[i], r);
-      const float q1 = __builtin_fmaf(__builtin_fmaf(-den, q, x[i]), r, q);
-      const float q2 = __builtin_fmaf(__builtin_fmaf(-den, q1, x[i]), r, q1);
-      dir[i] = __builtin_copysignf(q2, x[i]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < GG; ++i) dir[i] = __fdiv_rn(x[i], den);
-  }
-}
-
 typedef const float __attribute__((address_space(4)))* cb_ptr;   // read through the scalar cache
 
 constexpr int kEncWaves = 8;       // waves per workgroup: one per group in the argmax phase

@@ -145,6 +145,9 @@ int launch_decode(const DecodeLaunch& L, int phases, hipStream_t stream);
 // The decode kernel over prefill + decode-page rows (mode & kTailDecode),
 // then the tail kernel: merge, tail terms, output, append / flush.
 int launch_decode_tail(const DecodeLaunch& L, const TailLaunch& T, hipStream_t stream);
+// The next decode_kernel launch on this thread records its start / stop in
+// these events (kernel-only timestamps, hipExtLaunchKernel).
+void set_decode_timing(hipEvent_t start, hipEvent_t stop);
 int launch_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_rows, const int32_t* ptable,
                          const int32_t* vslot, const int32_t* positions, int32_t dec_cap, int64_t dec_byte0,
                          int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d,

@@ -38,6 +38,13 @@ SIGNATURES = {
                                                   I32, I32, I32, P, P, I32, I32, F32, F64, P]),
     "sphkv_decode_paged_checked": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P,
                                                   I32, I32, I32, P, P, P, I64, I32, I32, F32, F64, P]),
+    "sphkv_time_next_decode_kernel": (ctypes.c_int, [P, P]),
+    "sphkv_step_plan_create": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P, I32, I32, I32,
+                                              P, P, P, P, P, I64, I32, I32, I32, I32, P, I64, I32, I32, F32, F64,
+                                              P]),
+    "sphkv_step_plan_run": (ctypes.c_int, [P, P, P, I32, P, P, P, I32, P]),
+    "sphkv_step_plan_counts": (ctypes.c_int, [P, P, P]),
+    "sphkv_step_plan_destroy": (None, [P]),
     "sphkv_tail_relayout": (ctypes.c_int, [P, I32, I32, P, P, P, I32, I64, I32, I32, P, P, P, P]),
     "sphkv_decode_step": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P, I32, I32, I32,
                                          P, P, I32, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, I64,

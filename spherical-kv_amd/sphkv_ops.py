@@ -472,27 +472,32 @@ def tail_slot_bytes(dh: int) -> int:
 class DecodeTail:
     """Decode-time state of a pool for full reference decode steps
     (_compressed_head_attention_batched + _append_decode_kv,
-    spherical_kv_pipeline.py:2057-2475): per (sequence, kv head) the staged
-    tokens (tier-3 codes, fp32 radii, fp16 V, positions; at most 15), room
-    for `capacity` decode pages in the pool, and the decode-time pointer
-    table, positions, V slots and work list in which each (seq, head)'s
-    reserved rows follow its prefill rows (sphkv_tail_relayout).  A flush
-    writes the page, its positions and V, and extends that (seq, head)'s work
-    items by one row, all on the device.
+    spherical_kv_pipeline.py:2057-2475) of one layer (gqa, RoPE theta and
+    sm_scale fixed): per (sequence, kv head) the staged tokens (tier-3 codes,
+    fp32 radii, fp16 V, positions; at most 15), room for `capacity` decode
+    pages in the pool, and the decode-time pointer table, positions, V slots
+    and work list in which each (seq, head)'s reserved rows follow its
+    prefill rows (sphkv_tail_relayout).  A flush writes the page, its
+    positions and V, and extends that (seq, head)'s work items by one row, all
+    on the device.
 
-    Attaching grows the pool's byte pool and V pool (copies once) when they
-    have no room for the decode pages.  Every (seq, head) stages one token per
-    step, so the host tracks the staged count and flushed pages exactly and
-    raises before a step would need a decode slot past `capacity`."""
+    The static arguments are bound once in a C step plan
+    (sphkv_step_plan_create), which also keeps the host's mirror of the
+    staged / flushed counts and refuses a step that would need a decode page
+    past `capacity`.  Attaching grows the pool's byte pool and V pool (copies
+    once) when they have no room for the decode pages."""
 
-    def __init__(self, pool: "PagedPool", capacity: int = 64, rows_per_item: Optional[int] = None):
+    def __init__(self, pool: "PagedPool", gqa: int, rope_theta: float, capacity: int = 64,
+                 sm_scale: Optional[float] = None, rows_per_item: Optional[int] = None):
+        import ctypes
         plan = pool.plan
         dev = pool.device
         if capacity < 0:
             raise ValueError("capacity must be >= 0")
         if pool.codebooks.get(3) is None:
             raise ValueError("decode steps need the tier-3 codebook (decode tokens are tier 3)")
-        self.pool, self.capacity = pool, int(capacity)
+        self.pool, self.capacity, self.gqa, self.rope_theta = pool, int(capacity), int(gqa), float(rope_theta)
+        self.sm_scale = float(1.0 / math.sqrt(plan.dh) if sm_scale is None else sm_scale)
         self.num_sh = num_sh = plan.num_seqs * plan.num_kv
         dh = plan.dh
         G3 = dh // 32
@@ -519,10 +524,11 @@ class DecodeTail:
         self.ptable = torch.empty((max(self.num_rows, 1), 3), dtype=torch.int32, device=dev)
         self.vslot = torch.empty(max(self.num_rows, 1), dtype=torch.int32, device=dev)
         self.positions = torch.empty((max(self.num_rows, 1), 16), dtype=torch.int32, device=dev)
-        rc = load().sphkv_tail_relayout(rs_dev.data_ptr(), num_sh, plan.num_rows, pool.ptable.data_ptr(),
-                                        pool.vslot.data_ptr(), pool.positions.data_ptr(), self.capacity,
-                                        self.dec_byte0, self.dec_vpage0, dh, self.ptable.data_ptr(),
-                                        self.vslot.data_ptr(), self.positions.data_ptr(), _stream())
+        lib = load()
+        rc = lib.sphkv_tail_relayout(rs_dev.data_ptr(), num_sh, plan.num_rows, pool.ptable.data_ptr(),
+                                     pool.vslot.data_ptr(), pool.positions.data_ptr(), self.capacity,
+                                     self.dec_byte0, self.dec_vpage0, dh, self.ptable.data_ptr(),
+                                     self.vslot.data_ptr(), self.positions.data_ptr(), _stream())
         check(rc, "sphkv_tail_relayout")
         # the work list over the prefill rows, in the decode-time row numbering
         if rows_per_item is None:
@@ -531,7 +537,8 @@ class DecodeTail:
         shift = w[:, 0].astype(np.int64) * self.capacity
         w[:, 1] = (w[:, 1] + shift).astype(np.int32)
         w[:, 2] = (w[:, 2] + shift).astype(np.int32)
-        self.work = torch.as_tensor(np.ascontiguousarray(w), device=dev)
+        self._work0 = np.ascontiguousarray(w)
+        self.work = torch.as_tensor(self._work0, device=dev)
         self.work_start = torch.as_tensor(ws, device=dev)
         self.num_items = int(w.shape[0])
         # staging
@@ -540,23 +547,72 @@ class DecodeTail:
         self.stg_v = torch.zeros((num_sh, TAIL_SLOTS, dh), dtype=torch.float16, device=dev)
         self.stg_pos = torch.zeros((num_sh, TAIL_SLOTS), dtype=torch.int32, device=dev)
         self.state = torch.zeros((num_sh, 4), dtype=torch.int32, device=dev)
-        self.staged = 0          # tokens staged per (seq, head) (host mirror)
-        self.flushed = 0         # decode pages per (seq, head) (host mirror)
-
-    def workspace_bytes(self, gqa: int) -> int:
-        n = load().sphkv_decode_paged_workspace_bytes(self.num_items, gqa, self.pool.plan.dh)
+        n = lib.sphkv_decode_paged_workspace_bytes(self.num_items, self.gqa, dh)
         if n < 0:
             raise ValueError("bad gqa / dh for the decode workspace")
-        return int(n)
+        self.workspace = torch.zeros(max(int(n), 4), dtype=torch.uint8, device=dev)
+        self._plan = None
+        self._bind(0, 0)
 
-    def _advance(self) -> None:
-        if self.staged == TAIL_SLOTS - 1 and self.flushed >= self.capacity:
-            raise ValueError(f"no decode-page slot left (capacity {self.capacity} pages per (seq, head))")
+    def _bind(self, staged: int, flushed: int) -> None:
+        import ctypes
+        lib = load()
+        if self._plan is not None:
+            lib.sphkv_step_plan_destroy(self._plan)
+            self._plan = None
+        pool, plan = self.pool, self.pool.plan
+        c1, c2, c3 = pool.cb_ptrs()
+        h = ctypes.c_void_p()
+        rc = lib.sphkv_step_plan_create(
+            pool.pages.data_ptr(), self.pages_bytes, self.ptable.data_ptr(), self.vslot.data_ptr(),
+            self.positions.data_ptr(), self.num_rows, pool.v_pool.data_ptr(), self.num_vpages, c1, c2, c3,
+            self.work.data_ptr(), self.num_items, self.work_start.data_ptr(), plan.num_seqs, plan.num_kv, self.gqa,
+            self.stg_r.data_ptr(), self.stg_code.data_ptr(), self.stg_v.data_ptr(), self.stg_pos.data_ptr(),
+            self.state.data_ptr(), self.dec_byte0, self.dec_vpage0, self.capacity, staged, flushed,
+            self.workspace.data_ptr(), self.workspace.numel(), plan.dh, plan.page_size, self.sm_scale,
+            self.rope_theta, ctypes.byref(h))
+        check(rc, "sphkv_step_plan_create")
+        self._plan = h.value
+        self._run = lib.sphkv_step_plan_run
 
-    def _committed(self) -> None:
-        self.staged += 1
-        if self.staged == TAIL_SLOTS:
-            self.staged, self.flushed = 0, self.flushed + 1
+    def __del__(self):
+        try:
+            if self._plan is not None:
+                load().sphkv_step_plan_destroy(self._plan)
+        except Exception:
+            pass
+
+    def counts(self) -> Tuple[int, int]:
+        """(staged tokens, flushed decode pages) per (seq, head)."""
+        import ctypes
+        a, b = ctypes.c_int32(), ctypes.c_int32()
+        check(load().sphkv_step_plan_counts(self._plan, ctypes.byref(a), ctypes.byref(b)), "sphkv_step_plan_counts")
+        return int(a.value), int(b.value)
+
+    @property
+    def staged(self) -> int:
+        return self.counts()[0]
+
+    @property
+    def flushed(self) -> int:
+        return self.counts()[1]
+
+    def reset(self) -> None:
+        """Empty tail: no staged tokens, no decode pages (the work list's rows
+        back to the prefill rows).  Asynchronous, current stream."""
+        self.state.zero_()
+        self.work.copy_(torch.as_tensor(self._work0), non_blocking=False)
+        self._bind(0, 0)
+
+    def runner(self):
+        """The fastest call of a step: fn(q_ptr, k_ptr, k_is_fp32, v_ptr, pos_ptr, out_ptr, mode) with raw
+        device addresses (mode 1 decode, 2 append, 3 both) on the current stream; one ctypes call."""
+        run, plan = self._run, self._plan
+        stream = _stream()
+
+        def fn(q, k, k32, v, pos, out, mode):
+            check(run(plan, q, k, k32, v, pos, out, mode, stream), "sphkv_step_plan_run")
+        return fn
 
     def _step_inputs(self, k_new: torch.Tensor, v_new: torch.Tensor, cur_pos: torch.Tensor):
         plan, dev = self.pool.plan, self.pool.device
@@ -571,6 +627,15 @@ class DecodeTail:
         if tuple(cur_pos.shape) != (plan.num_seqs,):
             raise ValueError("cur_pos must be [num_seqs]")
 
+    def _call(self, q, k_new, v_new, cur_pos, out, mode: int) -> None:
+        rc = self._run(self._plan, _ptr(q), k_new.data_ptr(), 1 if k_new.dtype == torch.float32 else 0,
+                       v_new.data_ptr(), cur_pos.data_ptr(), _ptr(out), mode, _stream())
+        if rc != 0:
+            msg = load().sphkv_last_error().decode(errors="replace")
+            if "no decode-page slot" in msg:
+                raise ValueError(msg)
+            check(rc, "sphkv_step_plan_run")
+
     def state_host(self) -> Dict[str, np.ndarray]:
         """Copies of the tail state (waits for the current stream)."""
         return {"state": self.state.cpu().numpy(), "stg_r": self.stg_r.cpu().numpy(),
@@ -579,64 +644,45 @@ class DecodeTail:
 
 
 def decode_step(pool: "PagedPool", tail: DecodeTail, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-                cur_pos: torch.Tensor, gqa: int, rope_theta: float, sm_scale: Optional[float] = None,
-                out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
-                append: bool = True) -> torch.Tensor:
-    """One reference decode step on the GPU (sphkv_decode_step): attention of
-    q over the prefill pages, the flushed decode pages, the staged tokens and
-    the new token (k_new pre-RoPE [num_seqs, num_kv, dh] fp16/fp32, v_new fp16,
+                cur_pos: torch.Tensor, out: Optional[torch.Tensor] = None, append: bool = True) -> torch.Tensor:
+    """One reference decode step on the GPU (sphkv_decode_step through the
+    tail's step plan): attention of q fp16 [num_seqs, num_kv*gqa, dh] over the
+    prefill pages, the flushed decode pages, the staged tokens and the new
+    token (k_new pre-RoPE [num_seqs, num_kv, dh] fp16/fp32, v_new fp16,
     cur_pos int32 [num_seqs]); then, with append, the new token is staged
-    (and a full page flushed).  Returns out fp16 [num_seqs, num_kv*gqa, dh]."""
-    plan = pool.plan
-    _check_q(pool, q, gqa)
+    (and a full page flushed).  Returns out fp16, q's shape."""
+    if tail.pool is not pool:
+        raise ValueError("the tail belongs to another pool")
+    _check_q(pool, q, tail.gqa)
     tail._step_inputs(k_new, v_new, cur_pos)
-    if append:
-        tail._advance()
     if out is None:
         out = torch.empty_like(q)
     _need(out, torch.float16, "out", pool.device)
     if out.shape != q.shape:
         raise ValueError("out must match q")
-    wsb = tail.workspace_bytes(gqa)
-    if workspace is None:
-        workspace = torch.zeros(max(wsb, 4), dtype=torch.uint8, device=pool.device)
-    _need(workspace, torch.uint8, "workspace", pool.device)
-    if workspace.numel() < wsb:
-        raise ValueError(f"workspace needs {wsb} bytes, got {workspace.numel()}")
-    if sm_scale is None:
-        sm_scale = 1.0 / math.sqrt(plan.dh)
-    c1, c2, c3 = pool.cb_ptrs()
-    rc = load().sphkv_decode_step(
-        pool.pages.data_ptr(), tail.pages_bytes, tail.ptable.data_ptr(), tail.vslot.data_ptr(),
-        tail.positions.data_ptr(), tail.num_rows, pool.v_pool.data_ptr(), tail.num_vpages, c1, c2, c3,
-        tail.work.data_ptr(), tail.num_items, tail.work_start.data_ptr(), plan.num_seqs, plan.num_kv, gqa,
-        q.data_ptr(), k_new.data_ptr(), 1 if k_new.dtype == torch.float32 else 0, v_new.data_ptr(),
-        cur_pos.data_ptr(), tail.stg_r.data_ptr(), tail.stg_code.data_ptr(), tail.stg_v.data_ptr(),
-        tail.stg_pos.data_ptr(), tail.state.data_ptr(), tail.dec_byte0, tail.dec_vpage0, tail.capacity,
-        1 if append else 0, out.data_ptr(), workspace.data_ptr(), workspace.numel(), plan.dh, plan.page_size,
-        float(sm_scale), float(rope_theta), _stream())
-    check(rc, "sphkv_decode_step")
-    if append:
-        tail._committed()
+    tail._call(q, k_new, v_new, cur_pos, out, 3 if append else 1)
     return out
 
 
 def decode_append(pool: "PagedPool", tail: DecodeTail, k_new: torch.Tensor, v_new: torch.Tensor,
                   cur_pos: torch.Tensor) -> None:
-    """_append_decode_kv for every (seq, head) (sphkv_decode_append): stage the
-    new tokens, flushing full pages; no attention."""
-    plan = pool.plan
+    """_append_decode_kv for every (seq, head) (sphkv_decode_append's work,
+    through the tail's step plan): stage the new tokens, flushing full pages;
+    no attention."""
+    if tail.pool is not pool:
+        raise ValueError("the tail belongs to another pool")
     tail._step_inputs(k_new, v_new, cur_pos)
-    tail._advance()
-    rc = load().sphkv_decode_append(
-        pool.pages.data_ptr(), tail.pages_bytes, tail.positions.data_ptr(), tail.num_rows, pool.v_pool.data_ptr(),
-        tail.num_vpages, _ptr(pool.codebooks.get(3)), tail.work.data_ptr(), tail.num_items,
-        tail.work_start.data_ptr(), plan.num_seqs, plan.num_kv, k_new.data_ptr(),
-        1 if k_new.dtype == torch.float32 else 0, v_new.data_ptr(), cur_pos.data_ptr(), tail.stg_r.data_ptr(),
-        tail.stg_code.data_ptr(), tail.stg_v.data_ptr(), tail.stg_pos.data_ptr(), tail.state.data_ptr(),
-        tail.dec_byte0, tail.dec_vpage0, tail.capacity, plan.dh, plan.page_size, _stream())
-    check(rc, "sphkv_decode_append")
-    tail._committed()
+    tail._call(None, k_new, v_new, cur_pos, None, 2)
+
+
+def time_next_decode_kernel(start: "torch.cuda.Event", stop: "torch.cuda.Event") -> None:
+    """The next paged-decode kernel launch on this thread records its own
+    start and stop in these timing events (kernel-only timestamps,
+    sphkv_time_next_decode_kernel)."""
+    for e in (start, stop):
+        if not e.cuda_event:
+            e.record()
+    check(load().sphkv_time_next_decode_kernel(start.cuda_event, stop.cuda_event), "sphkv_time_next_decode_kernel")
 
 
 @dataclass

@@ -28,7 +28,7 @@ def _setup(gpu, config=2, ctx=4096, steps=40, capacity=4, seqs=None):
     st = synth.make_tail_steps(wl, steps)
     wl.codebooks[3] = st.cb3
     pool, cpu = pool_from_oracle(wl, gpu)
-    tail = ops.DecodeTail(pool, capacity=capacity)
+    tail = ops.DecodeTail(pool, wl.gqa, wl.rope_theta, capacity=capacity)
     orc = TailOracle(wl.num_seqs, wl.num_kv, wl.dh, st.cb3)
     return wl, st, pool, cpu, tail, orc
 
@@ -108,8 +108,7 @@ def test_decode_step_matches_oracle(gpu, config, ctx, seqs):
     worst = 0.0
     for t in range(steps):
         q, k, v, p = st.q[t], st.k[t], st.v[t], st.pos[t]
-        out = ops.decode_step(pool, tail, _dev(q, gpu), _dev(k, gpu), _dev(v, gpu), _dev(p, gpu), wl.gqa,
-                              wl.rope_theta)
+        out = ops.decode_step(pool, tail, _dev(q, gpu), _dev(k, gpu), _dev(v, gpu), _dev(p, gpu))
         if t in (0, 1, 2, 14, 15, 16, 17, 31, 32, 33):
             got = out.float().cpu().numpy()
             want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, q, wl.gqa, wl.rope_theta, tail=orc,
@@ -137,7 +136,7 @@ def test_decode_step_full_config2(gpu):
     qd = _dev(q, gpu)
     for t in range(steps):
         k, v, p = st.k[t], st.v[t], st.pos[t]
-        out = ops.decode_step(pool, tail, qd, _dev(k, gpu), _dev(v, gpu), _dev(p, gpu), wl.gqa, wl.rope_theta)
+        out = ops.decode_step(pool, tail, qd, _dev(k, gpu), _dev(v, gpu), _dev(p, gpu))
         if t in (0, 1, 15, 16):
             got = out.float().cpu().numpy()
             want = step_with_context(ctx_out, ctx_lse, orc, q, wl.gqa, wl.rope_theta, k, v, p)
@@ -156,8 +155,8 @@ def test_decode_step_without_append_leaves_state(gpu):
         ops.decode_append(pool, tail, _dev(st.k[t], gpu), _dev(st.v[t], gpu), _dev(st.pos[t], gpu))
     before = tail.state_host()
     args = [_dev(x, gpu) for x in (st.q[5], st.k[5], st.v[5], st.pos[5])]
-    a = ops.decode_step(pool, tail, *args, wl.gqa, wl.rope_theta, append=False).cpu().numpy()
-    b = ops.decode_step(pool, tail, *args, wl.gqa, wl.rope_theta, append=False).cpu().numpy()
+    a = ops.decode_step(pool, tail, *args, append=False).cpu().numpy()
+    b = ops.decode_step(pool, tail, *args, append=False).cpu().numpy()
     after = tail.state_host()
     assert (a.view(np.uint16) == b.view(np.uint16)).all()
     for key in before:
