@@ -255,9 +255,16 @@ int sphkv_time_next_decode_kernel(void* start_event, void* stop_event);
  *   stg_code  int32 [num_sh, 16, G3]   staged tier-3 codes
  *   stg_v     fp16  [num_sh, 16, dh]   staged V rows
  *   stg_pos   int32 [num_sh, 16]       staged positions
- *   tail_state int32 [num_sh, 4]       (staged count 0..15, decode pages
- *                                       flushed, tokens dropped for want of a
- *                                       decode slot, 0); zero it to start
+ *   tail_state int32 [num_sh, 2, 4]    two copies of (staged count 0..15,
+ *                                       decode pages flushed, tokens dropped
+ *                                       for want of a decode slot, 0); zero
+ *                                       it to start.  A step reads copy
+ *                                       step_parity, and an appending step
+ *                                       writes the other copy (so the
+ *                                       workgroups of one launch never see
+ *                                       each other's update): pass
+ *                                       step_parity = appending steps so far
+ *                                       mod 2
  * Decode pages: sh's page k (k < dec_cap) is written at pages + dec_byte0 +
  * (sh * dec_cap + k) * slot (slot = 16-byte aligned size of a 16-token tier-3
  * page: 112 bytes at dh 128, 64 at dh 64), its V at V page dec_vpage0 +
@@ -303,15 +310,15 @@ int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable
                       const uint16_t* q, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
                       const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
                       int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t append,
-                      uint16_t* out, void* workspace, int64_t workspace_bytes,
+                      int32_t step_parity, uint16_t* out, void* workspace, int64_t workspace_bytes,
                       int32_t dh, int32_t page_size, float sm_scale, double rope_theta, void* stream);
 
 /*
  * A bound decode step (no reference counterpart: the reference re-derives
  * its tensors in Python every step).  sphkv_step_plan_create validates every
  * static argument of sphkv_decode_step once (same meaning; staged / flushed
- * give the tail's current counts, 0 for a fresh tail) and keeps them with
- * the host's mirror of the tail counts; sphkv_step_plan_run then takes only
+ * give the tail's current counts and step_parity, 0 for a fresh tail) and
+ * keeps them with the host's mirror of the tail counts and parity; sphkv_step_plan_run then takes only
  * the per-step inputs: mode 1 = decode (no append), 2 = append only
  * (sphkv_decode_append), 3 = decode and append.  A run that would need a
  * decode page past dec_cap fails (SPHKV_EINVAL) before launching.  Runs of
@@ -325,11 +332,11 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
                            int32_t num_seqs, int32_t num_kv, int32_t gqa,
                            float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos, int32_t* tail_state,
                            int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t staged, int32_t flushed,
-                           void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
-                           double rope_theta, sphkv_step_plan** plan_out);
+                           int32_t step_parity, void* workspace, int64_t workspace_bytes, int32_t dh,
+                           int32_t page_size, float sm_scale, double rope_theta, sphkv_step_plan** plan_out);
 int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_new, int32_t k_is_fp32,
                         const uint16_t* v_new, const int32_t* cur_pos, uint16_t* out, int32_t mode, void* stream);
-int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed);
+int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed, int32_t* step_parity);
 void sphkv_step_plan_destroy(sphkv_step_plan* plan);
 
 /*
@@ -342,8 +349,8 @@ int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions,
                         int32_t* work, int32_t num_items, const int32_t* work_start, int32_t num_seqs,
                         int32_t num_kv, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
                         const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
-                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t dh,
-                        int32_t page_size, void* stream);
+                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap,
+                        int32_t step_parity, int32_t dh, int32_t page_size, void* stream);
 
 /*
  * Logits-only ragged kernel with the contract of the reference's missing

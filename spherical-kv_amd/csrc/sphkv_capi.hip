@@ -301,7 +301,7 @@ int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable
                       const uint16_t* q, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
                       const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
                       int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t append,
-                      uint16_t* out, void* workspace, int64_t workspace_bytes,
+                      int32_t step_parity, uint16_t* out, void* workspace, int64_t workspace_bytes,
                       int32_t dh, int32_t page_size, float sm_scale, double rope_theta, void* stream) {
   const char* fn = "sphkv_decode_step";
   // the page-resident part is checked exactly as sphkv_decode_paged's (no launch)
@@ -316,6 +316,7 @@ int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable
   if (num_vpages < 0 || num_vpages > (int64_t)1 << 31)
     return fail(SPHKV_EINVAL, "%s: num_vpages must be in [0, 2^31] (int32 vslot)", fn);
   if (append != 0 && append != 1) return fail(SPHKV_EINVAL, "%s: append must be 0 or 1", fn);
+  if (step_parity != 0 && step_parity != 1) return fail(SPHKV_EINVAL, "%s: step_parity must be 0 or 1", fn);
   if (num_seqs == 0) return ok();
   int rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, k_new, v_new, cur_pos, stg_r,
                        stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap, dh);
@@ -332,7 +333,7 @@ int sphkv_decode_step(uint8_t* pages, int64_t pages_bytes, const int32_t* ptable
                         static_cast<float*>(workspace), dh, sm_scale, rope_theta};
   sphkv::TailLaunch T{k_new, k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state,
                       pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0,
-                      sphkv::kTailDecode | (append ? sphkv::kTailAppend : 0)};
+                      sphkv::kTailDecode | (append ? sphkv::kTailAppend : 0), step_parity};
   return launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
 }
 
@@ -341,13 +342,14 @@ int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions,
                         int32_t* work, int32_t num_items, const int32_t* work_start, int32_t num_seqs,
                         int32_t num_kv, const void* k_new, int32_t k_is_fp32, const uint16_t* v_new,
                         const int32_t* cur_pos, float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos,
-                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t dh,
-                        int32_t page_size, void* stream) {
+                        int32_t* tail_state, int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap,
+                        int32_t step_parity, int32_t dh, int32_t page_size, void* stream) {
   const char* fn = "sphkv_decode_append";
   if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
   if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
   if (num_seqs < 0 || num_kv <= 0 || num_items < 0 || pages_bytes < 0 || num_vpages < 0)
     return fail(SPHKV_EINVAL, "%s: negative size", fn);
+  if (step_parity != 0 && step_parity != 1) return fail(SPHKV_EINVAL, "%s: step_parity must be 0 or 1", fn);
   if (num_seqs == 0) return ok();
   int rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, k_new, v_new, cur_pos, stg_r,
                        stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap, dh);
@@ -358,7 +360,8 @@ int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions,
                         nullptr, nullptr, cb3, work, num_items, work_start, num_seqs, num_kv, 1, nullptr, nullptr,
                         nullptr, dh, 1.f, 2.0};
   sphkv::TailLaunch T{k_new, k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state,
-                      pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, sphkv::kTailAppend};
+                      pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, sphkv::kTailAppend,
+                      step_parity};
   return launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
 }
 
@@ -371,7 +374,7 @@ struct sphkv_step_plan {
   sphkv::DecodeLaunch L;
   sphkv::TailLaunch T;
   int64_t workspace_bytes;
-  int32_t staged, flushed;
+  int32_t staged, flushed, parity;
 };
 
 extern "C" {
@@ -383,8 +386,8 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
                            int32_t num_seqs, int32_t num_kv, int32_t gqa,
                            float* stg_r, int32_t* stg_code, uint16_t* stg_v, int32_t* stg_pos, int32_t* tail_state,
                            int64_t dec_byte0, int32_t dec_vpage0, int32_t dec_cap, int32_t staged, int32_t flushed,
-                           void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
-                           double rope_theta, sphkv_step_plan** plan_out) {
+                           int32_t step_parity, void* workspace, int64_t workspace_bytes, int32_t dh,
+                           int32_t page_size, float sm_scale, double rope_theta, sphkv_step_plan** plan_out) {
   const char* fn = "sphkv_step_plan_create";
   if (!plan_out) return fail(SPHKV_EINVAL, "%s: null plan_out", fn);
   *plan_out = nullptr;
@@ -394,7 +397,8 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
   int rc = sphkv_decode_step(nullptr, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages, cb1,
                              cb2, cb3, work, num_items, work_start, 0, num_kv, gqa, probe, probe, 0, probe,
                              nullptr, stg_r, stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0, dec_cap,
-                             1, nullptr, workspace, workspace_bytes, dh, page_size, sm_scale, rope_theta, nullptr);
+                             1, step_parity, nullptr, workspace, workspace_bytes, dh, page_size, sm_scale, rope_theta,
+                             nullptr);
   if (rc != SPHKV_OK) return rc;                    // size / shape checks (num_seqs = 0: no launch)
   if (num_seqs <= 0) return fail(SPHKV_EINVAL, "%s: num_seqs must be > 0", fn);
   rc = tail_checks(fn, pages_bytes, num_rows, num_vpages, cb3, num_seqs, num_kv, probe, probe,
@@ -416,10 +420,11 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
                              cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, nullptr, nullptr,
                              static_cast<float*>(workspace), dh, sm_scale, rope_theta};
   p->T = sphkv::TailLaunch{nullptr, 0, nullptr, nullptr, stg_r, stg_code, stg_v, stg_pos, tail_state,
-                           pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, 0};
+                           pages, positions, v_pool, work, dec_byte0, dec_cap, dec_vpage0, 0, 0};
   p->workspace_bytes = workspace_bytes;
   p->staged = staged;
   p->flushed = flushed;
+  p->parity = step_parity;
   *plan_out = p;
   return ok();
 }
@@ -443,18 +448,23 @@ int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_
   T.v_new = v_new;
   T.cur_pos = cur_pos;
   T.mode = mode;
+  T.parity = plan->parity;
   const int rc = launch_status(sphkv::launch_decode_tail(L, T, (hipStream_t)stream), fn);
-  if (rc == SPHKV_OK && app && ++plan->staged == sphkv::kTailSlots) {
-    plan->staged = 0;
-    ++plan->flushed;
+  if (rc == SPHKV_OK && app) {
+    plan->parity ^= 1;
+    if (++plan->staged == sphkv::kTailSlots) {
+      plan->staged = 0;
+      ++plan->flushed;
+    }
   }
   return rc;
 }
 
-int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed) {
-  if (!plan || !staged || !flushed) return fail(SPHKV_EINVAL, "sphkv_step_plan_counts: null argument");
+int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed, int32_t* step_parity) {
+  if (!plan || !staged || !flushed || !step_parity) return fail(SPHKV_EINVAL, "sphkv_step_plan_counts: null argument");
   *staged = plan->staged;
   *flushed = plan->flushed;
+  *step_parity = plan->parity;
   return ok();
 }
 

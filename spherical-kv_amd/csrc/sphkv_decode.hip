@@ -1010,8 +1010,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 
 // ---------------------------------------------------------------------------
 // Decode-time tail of the Mode-B step (spherical_kv_pipeline.py:2248-2342,
-// 2389-2475).  One 1024-thread workgroup per (sequence, kv head) sh; it is the
-// only reader and writer of sh's tail state within a launch.
+// 2389-2475).  One 256-thread workgroup per (sequence, kv head) sh and slice
+// of up to 128 floats of its GQA*DH output (the slice's q heads' tail logits,
+// the log-sum-exp of the slice's columns); slice 0 also appends.  The tail
+// counts come in two copies: a step reads copy `parity` and an appending
+// step writes the other, so the slices of one sh never see each other's
+// update.
 //
 //   * The step's new pre-RoPE key is encoded through the tier-3 codebook as
 //     one token (_encode_keys_with_codebooks on kn.unsqueeze(0), :2311-2313):
@@ -1034,8 +1038,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 //     table keeps dec_cap reserved rows right after each (seq, head)'s rows,
 //     their pointer-table rows and V slots set up front), and staging
 //     restarts empty.
-// Slots: wave w < 15 scores staged token w (w < n); wave 15 encodes and scores
-// the new token.
+// Slots: waves 0..2 score the staged tokens (slot w < n), wave 3 encodes
+// and scores the new token (slot 15).
 struct TailArgs {
   const void* k_new;        // [num_sh, DH] pre-RoPE, fp16 or fp32 (k_is_fp32)
   const _Float16* v_new;    // [num_sh, DH]
@@ -1044,74 +1048,59 @@ struct TailArgs {
   int32_t* stg_code;        // [num_sh, 16, DH/32]
   _Float16* stg_v;          // [num_sh, 16, DH]
   int32_t* stg_pos;         // [num_sh, 16]
-  int32_t* state;           // [num_sh, 4]: staged count, decode pages, dropped tokens, 0
+  int32_t* state;           // [num_sh, 2, 4]: two copies of (staged count, decode pages, dropped tokens, 0)
   uint8_t* pages;
   int32_t* positions;
   _Float16* v_pool;
   int32_t* work;            // [num_items, 4]: end_row of sh's items grows at a flush
   int64_t dec_byte0;
-  int32_t dec_cap, dec_vpage0, k_is_fp32, mode, num_items, num_rows;
+  int32_t dec_cap, dec_vpage0, k_is_fp32, mode, num_items, num_rows, parity;
 };
 
-constexpr int kTailThreads = 1024;
+constexpr int kTailThreads = 256;
 
 template <int DH, int GQA>
 __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a, TailArgs t) {
   constexpr int G3 = DH / 32, NJ = DH / 2, NS = kTailSlots;
-  constexpr int COLS = GQA * DH / 4;                   // float4 columns of one (seq, head)'s output
+  constexpr int SL = GQA * DH < 128 ? GQA * DH : 128;  // output floats of one workgroup (a slice)
+  constexpr int NSL = (GQA * DH) / SL;                 // slices per (seq, head)
+  constexpr int HPS = SL / DH;                         // q heads per slice
+  constexpr int COLS = SL / 4;                         // float4 columns of a slice
   constexpr int IL = kTailThreads / COLS;              // item lanes
   constexpr int UN = 4;                                // items per item lane per round trip
   constexpr int PS = partial_stride<DH, GQA>();
   constexpr int NCB = G3 * 8 * 32;                     // tier-3 codebook floats of one kv head
-  static_assert(kTailThreads / 64 == NS, "one wave per tail slot");
-  static_assert(GQA * DH <= kTailThreads && NCB <= kTailThreads && NS * DH / 8 <= kTailThreads, "thread maps");
+  constexpr int FPL = NJ / 16;                         // RoPE frequencies per lane in the logits
+  static_assert(kTailThreads == 256 && HPS >= 1 && NCB <= 4 * kTailThreads && (FPL == 4 || FPL == 2),
+                "thread maps");
   __shared__ float cbs[NCB];               // the head's tier-3 codebook
-  __shared__ __attribute__((aligned(16))) _Float16 vs[NS][DH];   // V of the tail slots
-  __shared__ float lg[NS][GQA];            // tail logits, log2 units (-inf: no token)
-  __shared__ float tr[NS][G3];             // tail radii (slot NS-1: the new token)
+  __shared__ __attribute__((aligned(16))) _Float16 vs[NS][DH];   // V of the tail slots (slot NS-1: new token)
+  __shared__ double ftab[NJ];              // RoPE frequencies, turns per token
+  __shared__ float lg[NS][HPS];            // tail logits of the slice's heads, log2 units (-inf: none)
+  __shared__ float tr[NS][G3];             // tail radii
   __shared__ int tc[NS][G3];               // tail codes
   __shared__ int tp[NS];                   // tail positions
   __shared__ float sims[G3][8];
-  __shared__ float kn[DH];                 // the new token's pre-RoPE key
-  __shared__ float tacc[GQA * DH];         // the tail's sum p V per (head, dim)
-  __shared__ float tml[GQA][2];            // the tail's (max, sum) per head
   __shared__ float4 red_v[IL][COLS];
   __shared__ float red_m[IL][COLS], red_l[IL][COLS];
   __shared__ float scl[G3];
   __shared__ __attribute__((aligned(16))) uint8_t pg[128];   // the flushed page
 
-  const int sh = blockIdx.x;
+  const int sh = blockIdx.x / NSL, slice = blockIdx.x % NSL;
   const int seq = sh / a.num_kv, h = sh % a.num_kv;
+  const int h0 = slice * HPS;                          // first q head (of the kv head's GQA) in the slice
   const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
   const bool dec = (t.mode & kTailDecode) != 0;
-  const int32_t* stp = t.state + (int64_t)sh * kTailStateInts;
-  const int n_st = min(max(stp[0], 0), NS - 1);        // staged tokens
-  const int ndec = max(stp[1], 0);                     // decode pages flushed so far
-  const int pos_new = t.cur_pos[seq];
   const float* cb3 = a.cb[3] + (int64_t)h * NCB;
 
-  // ---- every load that depends only on sh is issued first ------------------
-  // the work items' partials (one round trip after the item range)
-  const int ib = min(max(a.work_start[sh], 0), t.num_items);
-  const int ie = min(max(a.work_start[sh + 1], ib), t.num_items);
-  const int ni = ie - ib;
-  const int c = i % COLS, il = i / COLS;
-  const int f0 = 4 * c, hc = f0 / DH;                  // first float of this column, its head
-  float4 pv[UN];
-  float pm[UN], pl[UN];
-  if (dec) {
+  // ---- loads: the tail's first (they depend on nothing), then the counts,
+  //      the item range and the items' partials --------------------------------
+  float4 cbv[NCB / 4 / kTailThreads > 0 ? NCB / 4 / kTailThreads : 1];
 #pragma unroll
-    for (int k = 0; k < UN; ++k) {
-      const int it = il + k * IL;
-      const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
-      pm[k] = it < ni ? pp[hc] : -INFINITY;
-      pl[k] = pp[GQA + hc];
-      pv[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
-    }
-  }
-  // codebook (one float per thread), V of the tail slots (16 bytes per
-  // thread), staged radii / codes / positions
-  const float cbv = i < NCB ? cb3[i] : 0.f;
+  for (int k = 0; k < NCB / 4 / kTailThreads; ++k)
+    cbv[k] = reinterpret_cast<const float4*>(cb3)[i + k * kTailThreads];
+  const bool cb_part = NCB / 4 < kTailThreads && i < NCB / 4;          // dh 64: 128 float4s
+  if (cb_part) cbv[0] = reinterpret_cast<const float4*>(cb3)[i];
   half8 vrow;
   if (i < NS * DH / 8) {
     const int w = i / (DH / 8), c8 = i % (DH / 8);
@@ -1125,56 +1114,111 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
     sc = t.stg_code[(int64_t)sh * NS * G3 + i];
   }
   if (i < NS - 1) sp = t.stg_pos[(int64_t)sh * NS + i];
-  // this lane's query pair (j, j + NJ) of every head (the logits)
-  const int j = lane % NJ;
-  float qa[GQA], qb[GQA];
-  if (dec) {
-    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH;
+  // the new token's encode (wave 3, lane = (group eg, centroid ec)): its
+  // group's 32 key values and its centroid row
+  const int eg = lane >> 3, ec = lane & 7;
+  const bool enc_lane = wave == 3 && eg < G3;
+  float x[32], crow[32];
+  if (enc_lane) {
+    if (t.k_is_fp32) {
+      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(t.k_new) + (int64_t)sh * DH + 32 * eg);
 #pragma unroll
-    for (int hh = 0; hh < GQA; ++hh) {
-      qa[hh] = (float)qh[hh * DH + j];
-      qb[hh] = (float)qh[hh * DH + j + NJ];
+      for (int k = 0; k < 8; ++k) {
+        const float4 w = src[k];
+        x[4 * k] = w.x; x[4 * k + 1] = w.y; x[4 * k + 2] = w.z; x[4 * k + 3] = w.w;
+      }
+    } else {
+      const half8* src = reinterpret_cast<const half8*>(static_cast<const _Float16*>(t.k_new) + (int64_t)sh * DH + 32 * eg);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const half8 hv = src[k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[8 * k + e] = (float)hv[e];
+      }
+    }
+    const float4* cr = reinterpret_cast<const float4*>(cb3 + (eg * 8 + ec) * 32);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 w = cr[k];
+      crow[4 * k] = w.x; crow[4 * k + 1] = w.y; crow[4 * k + 2] = w.z; crow[4 * k + 3] = w.w;
     }
   }
-  // the new token's key, fp32 (the encode reads it from LDS)
-  float kv = 0.f;
-  if (i < DH)
-    kv = t.k_is_fp32 ? static_cast<const float*>(t.k_new)[(int64_t)sh * DH + i]
-                     : (float)static_cast<const _Float16*>(t.k_new)[(int64_t)sh * DH + i];
-  // RoPE frequency of lane j in turns per token (formed while the loads fly)
-  const double fj = exp2(-(2.0 * j / DH) * a.log2_theta) * 0.15915494309189535;
+  // the logits' lane map: slot 4 * wave + (lane >> 4), frequencies
+  // FPL * (lane & 15) .. + FPL - 1; this lane's query values on them
+  const int jc = lane & 15, j0 = FPL * jc;
+  float qa[HPS][FPL], qb[HPS][FPL];
+  if (dec) {
+    const _Float16* qh = a.q + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA + h0) * DH;
+#pragma unroll
+    for (int hh = 0; hh < HPS; ++hh)
+#pragma unroll
+      for (int f = 0; f < FPL; ++f) {
+        qa[hh][f] = (float)qh[hh * DH + j0 + f];
+        qb[hh][f] = (float)qh[hh * DH + j0 + f + NJ];
+      }
+  }
+  // the counts, the new token's position and the item range through vector
+  // loads (vmcnt): scalar loads share their counter with LDS, and the LDS
+  // waits below would then wait for them too
+  const int32_t* stp = t.state + (int64_t)sh * 2 * kTailStateInts + t.parity * kTailStateInts;
+  const auto st4 = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(stp, 16), 0, 0, 0);
+  const int pos_ld = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(t.cur_pos + seq, 4), 0, 0, 0);
+  const int wsa = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.work_start + sh, 8), 0, 0, 0);
+  const int wsb = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.work_start + sh, 8), 4, 0, 0);
+  const int c = i % COLS, il = i / COLS;
+  const int f0 = slice * SL + 4 * c, hc = f0 / DH;     // first float of this column in [GQA*DH], its head
+  // the items' partials: first at the range an even split of the items gives
+  // (every (seq, head) with the same item count, the usual list), issued
+  // with the item range's own load; reloaded when the range differs
+  const int nsh = a.num_sh;
+  const int npe = nsh > 0 ? t.num_items / nsh : 0;
+  int ib = sh * npe, ni = npe;
+  float4 pv[UN];
+  float pm[UN], pl[UN];
+  auto load_partials = [&](int it0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < UN; ++k) {
+      const int it = it0 + k * IL;
+      const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
+      pm[k] = it < ni ? pp[hc] : -INFINITY;
+      pl[k] = pp[GQA + hc];
+      pv[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
+    }
+  };
+  if (dec && npe * nsh == t.num_items) load_partials(il);
 
-  // ---- shared tables ---------------------------------------------------------
-  if (i < NCB) cbs[i] = cbv;
+  const int n_st = min(max(__builtin_amdgcn_readfirstlane((int)st4[0]), 0), NS - 1);   // staged tokens
+  const int ndec = max(__builtin_amdgcn_readfirstlane((int)st4[1]), 0);                 // decode pages flushed so far
+  const int ndrop = max(__builtin_amdgcn_readfirstlane((int)st4[2]), 0);
+  const int pos_new = __builtin_amdgcn_readfirstlane(pos_ld);
+
+  // ---- shared tables; the new token's encode -------------------------------
+  if (i < NJ) ftab[i] = exp2(-(2.0 * i / DH) * a.log2_theta) * 0.15915494309189535;   // inv_freq / 2 pi
+#pragma unroll
+  for (int k = 0; k < NCB / 4 / kTailThreads; ++k) reinterpret_cast<float4*>(cbs)[i + k * kTailThreads] = cbv[k];
+  if (cb_part) reinterpret_cast<float4*>(cbs)[i] = cbv[0];
   if (i < NS * DH / 8) *reinterpret_cast<half8*>(&vs[i / (DH / 8)][8 * (i % (DH / 8))]) = vrow;
   if (i < (NS - 1) * G3) {
     tr[i / G3][i % G3] = sr;
     tc[i / G3][i % G3] = min(max(sc, 0), 7);
   }
   if (i < NS - 1) tp[i] = sp;
-  if (i < DH) kn[i] = kv;
   if (i == 0) tp[NS - 1] = pos_new;
-  __syncthreads();
-  if (wave == NS - 1) {
+  if (wave == 3) {
     // the new token through the tier-3 codebook (_encode_keys_with_codebooks
     // on one token, torch CPU order; N*g*C = 256 < 400 takes ATen's naive
-    // loop: multiply, then add, in order); lane = (group eg, centroid ec)
-    const int eg = lane >> 3, ec = lane & 7;
+    // loop: multiply, then add, in order)
     float r_enc = 0.f;
-    if (eg < G3) {
-      float x[32];
-#pragma unroll
-      for (int k = 0; k < 32; ++k) x[k] = kn[32 * eg + k];
+    if (enc_lane) {
       r_enc = torch_norm(x, 32);
       group_directions<32>(x, __fadd_rn(r_enc, 1e-8f), !t.k_is_fp32, x);    // x becomes dir
-      const float* cr = cbs + (eg * 8 + ec) * 32;
-      float s = 0.f;
+      float sm = 0.f;
 #pragma unroll
-      for (int k = 0; k < 32; ++k) s = __fadd_rn(s, __fmul_rn(x[k], cr[k]));
-      sims[eg][ec] = s;
+      for (int k = 0; k < 32; ++k) sm = __fadd_rn(sm, __fmul_rn(x[k], crow[k]));
+      sims[eg][ec] = sm;
     }
     wave_lds_sync();
-    if (eg < G3 && ec == 0) {
+    if (enc_lane && ec == 0) {
       // first maximum: the ascending scan with '>' (torch.argmax)
       int best = 0;
       float bs = sims[eg][0];
@@ -1184,115 +1228,118 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
       tr[NS - 1][eg] = r_enc;
       tc[NS - 1][eg] = best;
     }
-    wave_lds_sync();
   }
+  __syncthreads();
 
   if (dec) {
     if (blockIdx.x == 0 && i == 0) {                   // malformed-page count: as the merge kernel
       a.status[1] = a.status[0];
       a.status[0] = 0u;
     }
-    // ---- tail logits: wave w scores slot w; lane j = RoPE frequency ---------
+    // ---- tail logits: 16-lane row = slot, lane = FPL RoPE frequencies --------
     {
-      const bool present = wave < n_st || wave == NS - 1;
-      if (present) {
-        const bool act = lane < NJ;
-        const int g1 = j / 32, g2 = (j + NJ) / 32;
-        const float k1 = tr[wave][g1] * cbs[(g1 * 8 + tc[wave][g1]) * 32 + (j & 31)];
-        const float k2 = tr[wave][g2] * cbs[(g2 * 8 + tc[wave][g2]) * 32 + ((j + NJ) & 31)];
-        const float2 z = turn_phasor((double)tp[wave] * fj);
+      const int w = 4 * wave + (lane >> 4);
+      const bool live = w < n_st || w == NS - 1;
+      float part[HPS];
+#pragma unroll
+      for (int hh = 0; hh < HPS; ++hh) part[hh] = 0.f;
+      const int g1 = j0 / 32, g2 = (j0 + NJ) / 32;       // the lane's frequencies stay in one group each
+      const float* c1p = cbs + (g1 * 8 + tc[w][g1]) * 32 + (j0 & 31);
+      const float* c2p = cbs + (g2 * 8 + tc[w][g2]) * 32 + ((j0 + NJ) & 31);
+      const float r1 = tr[w][g1], r2 = tr[w][g2];
+      const double pw = (double)tp[w];
+#pragma unroll
+      for (int f = 0; f < FPL; ++f) {
+        const float k1 = r1 * c1p[f], k2 = r2 * c2p[f];
+        const float2 z = turn_phasor(pw * ftab[j0 + f]);
         // R(pos) k_hat on the pair (j, j + NJ): <q, R(pos) k_hat> = <R(-pos) q, k_hat>
         const float x0 = k1 * z.x - k2 * z.y, x1 = k2 * z.x + k1 * z.y;
-        float part[GQA];
 #pragma unroll
-        for (int hh = 0; hh < GQA; ++hh) part[hh] = act ? qa[hh] * x0 + qb[hh] * x1 : 0.f;
-#pragma unroll
-        for (int hh = 0; hh < GQA; ++hh)
-#pragma unroll
-          for (int m = 32; m >= 1; m >>= 1) part[hh] += shfl_xor(part[hh], m);
-        if (lane == 0)
-#pragma unroll
-          for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = part[hh] * a.scale_log2;
-      } else if (lane == 0) {
-#pragma unroll
-        for (int hh = 0; hh < GQA; ++hh) lg[wave][hh] = -INFINITY;
+        for (int hh = 0; hh < HPS; ++hh) part[hh] += qa[hh][f] * x0 + qb[hh][f] * x1;
       }
+#pragma unroll
+      for (int hh = 0; hh < HPS; ++hh) part[hh] = row_sum16(part[hh]);
+      if (jc == 0)
+#pragma unroll
+        for (int hh = 0; hh < HPS; ++hh) lg[w][hh] = live ? part[hh] * a.scale_log2 : -INFINITY;
     }
-    // ---- the work items' log-sum-exp (partials already in registers) ---------
+    // ---- the work items' log-sum-exp (partials already in registers unless
+    //      the item range differs from the even split) -------------------------
     {
-      float M = -INFINITY, Ls = 0.f;
-      float4 sum = {0.f, 0.f, 0.f, 0.f};
-      for (int it0 = il, r0 = 0; it0 < ni; it0 += IL * UN, ++r0) {
-        if (r0 > 0) {                                  // more than IL * UN items: next round trip
-#pragma unroll
-          for (int k = 0; k < UN; ++k) {
-            const int it = it0 + k * IL;
-            const float* pp = a.partials + (int64_t)(ib + (it < ni ? it : 0)) * PS;
-            pm[k] = it < ni ? pp[hc] : -INFINITY;
-            pl[k] = pp[GQA + hc];
-            pv[k] = *reinterpret_cast<const float4*>(pp + 16 + f0);
-          }
-        }
-        float Mn = M;
-#pragma unroll
-        for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, pm[k]);
-        if (Mn == -INFINITY) continue;
-        const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
-        sum.x *= r; sum.y *= r; sum.z *= r; sum.w *= r;
-        Ls *= r;
-#pragma unroll
-        for (int k = 0; k < UN; ++k) {
-          const float f = (pm[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[k] - Mn);
-          Ls += f * pl[k];
-          sum.x += f * pv[k].x; sum.y += f * pv[k].y; sum.z += f * pv[k].z; sum.w += f * pv[k].w;
-        }
-        M = Mn;
+      const int ib_w = min(max(__builtin_amdgcn_readfirstlane(wsa), 0), t.num_items);
+      const int ie_w = min(max(__builtin_amdgcn_readfirstlane(wsb), ib_w), t.num_items);
+      if (ib_w != ib || ie_w - ib_w != ni || npe * nsh != t.num_items) {
+        ib = ib_w;
+        ni = ie_w - ib_w;
+        load_partials(il);
       }
-      red_v[il][c] = sum;
-      red_m[il][c] = M;
-      red_l[il][c] = Ls;
     }
+    // the tail slots' logits are all in LDS past this barrier; item lane il
+    // starts its state from tail slots il, il + IL, ... (their fp32 weights
+    // and V on this column's 4 floats)
     __syncthreads();
-    // ---- the tail's (max, sum, sum p V) per (head, dim), fp32 ---------------
-    if (i < GQA * DH) {
-      const int hh = i / DH, d = i % DH;
-      float m = -INFINITY;
+    float M = -INFINITY, Ls = 0.f;
+    float4 sum = {0.f, 0.f, 0.f, 0.f};
+    {
+      const int hl = hc - h0, d0 = f0 % DH;
+      constexpr int TPL = (NS + IL - 1) / IL;          // tail slots per item lane
+      float lw[TPL];
 #pragma unroll
-      for (int w = 0; w < NS; ++w) m = fmaxf(m, lg[w][hh]);
-      float l = 0.f, acc = 0.f;
-#pragma unroll
-      for (int w = 0; w < NS; ++w) {
-        const float xw = lg[w][hh];
-        const float p = xw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(xw - m);
-        l += p;
-        acc += p * (float)vs[w][d];
+      for (int k = 0; k < TPL; ++k) {
+        const int w = il + k * IL;
+        lw[k] = w < NS ? lg[w][hl] : -INFINITY;
+        M = fmaxf(M, lw[k]);
       }
-      tacc[i] = acc;
-      if (d == 0) {
-        tml[hh][0] = m;
-        tml[hh][1] = l;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < TPL; ++k) {
+          const int w = il + k * IL;
+          const float p = lw[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(lw[k] - M);
+          const half4 vv = *reinterpret_cast<const half4*>(&vs[w < NS ? w : 0][d0]);
+          Ls += p;
+          sum.x += p * (float)vv[0]; sum.y += p * (float)vv[1]; sum.z += p * (float)vv[2]; sum.w += p * (float)vv[3];
+        }
       }
     }
+    for (int it0 = il, r0 = 0; it0 < ni; it0 += IL * UN, ++r0) {
+      if (r0 > 0) load_partials(it0);                  // more than IL * UN items: next round trip
+      float Mn = M;
+#pragma unroll
+      for (int k = 0; k < UN; ++k) Mn = fmaxf(Mn, pm[k]);
+      if (Mn == -INFINITY) continue;
+      const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+      sum.x *= r; sum.y *= r; sum.z *= r; sum.w *= r;
+      Ls *= r;
+#pragma unroll
+      for (int k = 0; k < UN; ++k) {
+        const float f = (pm[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[k] - Mn);
+        Ls += f * pl[k];
+        sum.x += f * pv[k].x; sum.y += f * pv[k].y; sum.z += f * pv[k].z; sum.w += f * pv[k].w;
+      }
+      M = Mn;
+    }
+    red_v[il][c] = sum;
+    red_m[il][c] = M;
+    red_l[il][c] = Ls;
     __syncthreads();
     if (il == 0) {
-      float Mx = tml[hc][0];
-      for (int k = 0; k < IL; ++k) Mx = fmaxf(Mx, red_m[k][c]);
+      // the log-sum-exp of the item lanes' states (the tail already in them)
+      float mk[IL];
+      float Mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < IL; ++k) {
+        mk[k] = red_m[k][c];
+        Mx = fmaxf(Mx, mk[k]);
+      }
       float4 tot = {0.f, 0.f, 0.f, 0.f};
       float Lt = 0.f;
       if (Mx != -INFINITY) {
+#pragma unroll
         for (int k = 0; k < IL; ++k) {
-          const float mk = red_m[k][c];
-          if (mk == -INFINITY) continue;
-          const float f = __builtin_amdgcn_exp2f(mk - Mx);
+          const float f = mk[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk[k] - Mx);
           const float4 xk = red_v[k][c];
           tot.x += f * xk.x; tot.y += f * xk.y; tot.z += f * xk.z; tot.w += f * xk.w;
           Lt += f * red_l[k][c];
-        }
-        const float mt = tml[hc][0];
-        if (mt != -INFINITY) {
-          const float f = __builtin_amdgcn_exp2f(mt - Mx);
-          tot.x += f * tacc[f0]; tot.y += f * tacc[f0 + 1]; tot.z += f * tacc[f0 + 2]; tot.w += f * tacc[f0 + 3];
-          Lt += f * tml[hc][1];
         }
       }
       const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
@@ -1302,12 +1349,14 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
       *reinterpret_cast<half4*>(a.out + ((int64_t)seq * a.num_kv * GQA + (int64_t)h * GQA) * DH + f0) = o;
     }
   }
-  if (!(t.mode & kTailAppend)) return;
+  if (!(t.mode & kTailAppend) || slice != 0) return;
+  ib = min(max(__builtin_amdgcn_readfirstlane(wsa), 0), t.num_items);
+  const int ie = min(max(__builtin_amdgcn_readfirstlane(wsb), ib), t.num_items);
 
-  // ---- append the new token (_append_decode_kv) ----------------------------
-  // (every staged value was read into LDS before the first barrier; this one
-  // orders the new token's encode, wave NS - 1, before the reads below)
-  __syncthreads();
+  // ---- append the new token (_append_decode_kv), by slice 0 -----------------
+  // (every staged value and the new token's encode are in LDS since the
+  // first barrier)
+  int32_t* nst = t.state + (int64_t)sh * 2 * kTailStateInts + (1 - t.parity) * kTailStateInts;   // next counts
   if (n_st < NS - 1) {
     const int sl = n_st;
     if (i < DH / 8)
@@ -1319,12 +1368,8 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
     }
     if (i == 0) {
       t.stg_pos[(int64_t)sh * NS + sl] = pos_new;
-      t.state[(int64_t)sh * kTailStateInts] = sl + 1;
+      nst[0] = sl + 1; nst[1] = ndec; nst[2] = ndrop; nst[3] = 0;
     }
-    return;
-  }
-  if (ndec >= t.dec_cap) {                             // no decode slot left: the token is dropped
-    if (i == 0) t.state[(int64_t)sh * kTailStateInts + 2] = stp[2] + 1;
     return;
   }
   // ---- the staged 15 tokens and the new one fill a page: flush it
@@ -1334,8 +1379,9 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   constexpr int SLOT = (PB + 15) & ~15;
   const int k = sh * t.dec_cap + ndec;
   const int row = ie > ib ? t.work[4 * (int64_t)ib + 2] : -1;   // sh's next reserved row
-  if (row < 0 || row >= t.num_rows) {                  // no item or a corrupted list: drop
-    if (i == 0) t.state[(int64_t)sh * kTailStateInts + 2] = stp[2] + 1;
+  if (ndec >= t.dec_cap || row < 0 || row >= t.num_rows) {
+    // no decode slot left (or no item / a corrupted list): the token is dropped
+    if (i == 0) { nst[0] = n_st; nst[1] = ndec; nst[2] = ndrop + 1; nst[3] = 0; }
     return;
   }
   if (i < G3) {                                        // r_scale[g] = max_n r[n, g]
@@ -1386,10 +1432,7 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
     dst[1] = hi;
   }
   for (int it = ib + i; it < ie; it += kTailThreads) t.work[4 * (int64_t)it + 2] = row + 1;   // sh's items take the row
-  if (i == 0) {
-    t.state[(int64_t)sh * kTailStateInts] = 0;
-    t.state[(int64_t)sh * kTailStateInts + 1] = ndec + 1;
-  }
+  if (i == 0) { nst[0] = 0; nst[1] = ndec + 1; nst[2] = ndrop; nst[3] = 0; }
 }
 
 // Decode-time pointer table (the layout sphkv_decode_step reads): the
@@ -1501,13 +1544,14 @@ static int launch_decode_tail_t(const DecodeLaunch& L, const TailLaunch& T, hipS
   t.stg_pos = T.stg_pos; t.state = T.state; t.pages = T.pages; t.positions = T.positions;
   t.v_pool = reinterpret_cast<_Float16*>(T.v_pool); t.work = T.work; t.dec_byte0 = T.dec_byte0;
   t.dec_cap = T.dec_cap; t.dec_vpage0 = T.dec_vpage0; t.k_is_fp32 = T.k_is_fp32;
-  t.mode = T.mode; t.num_items = L.num_items; t.num_rows = L.num_rows;
+  t.mode = T.mode; t.num_items = L.num_items; t.num_rows = L.num_rows; t.parity = T.parity & 1;
   const int nsh = L.num_seqs * L.num_kv;
   if ((T.mode & kTailDecode) && L.num_items > 0)
     launch_timed(decode_kernel<DH, GQA>, dim3(L.num_items), dim3(decode_waves<GQA>() * 64), stream, L.work,
                  L.num_items, a);
+  constexpr int NSL = (GQA * DH) / (GQA * DH < 128 ? GQA * DH : 128);
   if (nsh > 0)
-    hipLaunchKernelGGL((decode_tail_kernel<DH, GQA>), dim3(nsh), dim3(kTailThreads), 0, stream, a, t);
+    hipLaunchKernelGGL((decode_tail_kernel<DH, GQA>), dim3(nsh * NSL), dim3(kTailThreads), 0, stream, a, t);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -40,7 +40,7 @@ struct DecodeLaunch {
 constexpr int kTailSlots = 16;
 constexpr int kTailDecode = 1;      // score the tail in the step's softmax, write out
 constexpr int kTailAppend = 2;      // append the new token (flush a full page)
-constexpr int kTailStateInts = 4;   // per (seq, head): staged count, decode pages, dropped tokens, 0
+constexpr int kTailStateInts = 4;   // per (seq, head), twice (step parity): staged count, decode pages, dropped, 0
 inline int tail_page_bytes(int dh) { return 8 + 26 * (dh / 32); }          // tier 3, 16 tokens
 inline int tail_slot_bytes(int dh) { return (tail_page_bytes(dh) + 15) & ~15; }
 
@@ -50,6 +50,7 @@ struct TailLaunch {
   uint8_t* pages; int32_t* positions; uint16_t* v_pool; int32_t* work;
   int64_t dec_byte0; int32_t dec_cap, dec_vpage0;
   int32_t mode;
+  int32_t parity;            // which copy of the tail counts this step reads
 };
 
 struct RaggedLaunch {

@@ -40,17 +40,17 @@ SIGNATURES = {
                                                   I32, I32, I32, P, P, P, I64, I32, I32, F32, F64, P]),
     "sphkv_time_next_decode_kernel": (ctypes.c_int, [P, P]),
     "sphkv_step_plan_create": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P, I32, I32, I32,
-                                              P, P, P, P, P, I64, I32, I32, I32, I32, P, I64, I32, I32, F32, F64,
-                                              P]),
+                                              P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, I64, I32, I32, F32,
+                                              F64, P]),
     "sphkv_step_plan_run": (ctypes.c_int, [P, P, P, I32, P, P, P, I32, P]),
-    "sphkv_step_plan_counts": (ctypes.c_int, [P, P, P]),
+    "sphkv_step_plan_counts": (ctypes.c_int, [P, P, P, P]),
     "sphkv_step_plan_destroy": (None, [P]),
     "sphkv_tail_relayout": (ctypes.c_int, [P, I32, I32, P, P, P, I32, I64, I32, I32, P, P, P, P]),
     "sphkv_decode_step": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P, I32, I32, I32,
-                                         P, P, I32, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, I64,
+                                         P, P, I32, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, P, P, I64,
                                          I32, I32, F32, F64, P]),
     "sphkv_decode_append": (ctypes.c_int, [P, I64, P, I32, P, I64, P, P, I32, P, I32, I32, P, I32, P, P,
-                                           P, P, P, P, P, I64, I32, I32, I32, I32, P]),
+                                           P, P, P, P, P, I64, I32, I32, I32, I32, I32, P]),
     "sphkv_fused_decode_ragged": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
                                                  I32, I32, I32, I32, I32, P, P]),
     "sphkv_encode_append": (ctypes.c_int, [P, P, P, P, P, P, P, P, I32, I64, I32, I32, I32, I32, I32,

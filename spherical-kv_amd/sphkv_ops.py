@@ -7,6 +7,7 @@ wrong device, or a missing library, raise.
 from __future__ import annotations
 
 import math
+import weakref
 from dataclasses import dataclass
 from typing import Dict, Optional, Tuple
 
@@ -469,6 +470,9 @@ def tail_slot_bytes(dh: int) -> int:
     return (fmt.page_nbytes(3, TAIL_SLOTS, dh) + 15) & ~15
 
 
+_TAILS: "weakref.WeakValueDictionary[int, DecodeTail]" = None     # id(pool) -> its attached tail
+
+
 class DecodeTail:
     """Decode-time state of a pool for full reference decode steps
     (_compressed_head_attention_batched + _append_decode_kv,
@@ -496,6 +500,13 @@ class DecodeTail:
             raise ValueError("capacity must be >= 0")
         if pool.codebooks.get(3) is None:
             raise ValueError("decode steps need the tier-3 codebook (decode tokens are tier 3)")
+        global _TAILS
+        if _TAILS is None:
+            _TAILS = weakref.WeakValueDictionary()
+        other = _TAILS.get(id(pool))
+        if other is not None and other.pool is pool:
+            # a second tail would share (or reallocate) the decode-page region
+            raise ValueError("this pool already has a DecodeTail")
         self.pool, self.capacity, self.gqa, self.rope_theta = pool, int(capacity), int(gqa), float(rope_theta)
         self.sm_scale = float(1.0 / math.sqrt(plan.dh) if sm_scale is None else sm_scale)
         self.num_sh = num_sh = plan.num_seqs * plan.num_kv
@@ -517,6 +528,8 @@ class DecodeTail:
             pool.v_pool = grown
         self.pages_bytes = int(pool.pages.numel())
         self.num_vpages = int(pool.v_pool.shape[0])
+        self._pages, self._v_pool = pool.pages, pool.v_pool          # the storage the step plan binds
+        _TAILS[id(pool)] = self
         # decode-time table: prefill rows of sh shifted by sh * capacity, then sh's reserved rows
         self.num_rows = plan.num_rows + nres
         rs = _row_start32(plan.row_start)
@@ -546,15 +559,15 @@ class DecodeTail:
         self.stg_code = torch.zeros((num_sh, TAIL_SLOTS, G3), dtype=torch.int32, device=dev)
         self.stg_v = torch.zeros((num_sh, TAIL_SLOTS, dh), dtype=torch.float16, device=dev)
         self.stg_pos = torch.zeros((num_sh, TAIL_SLOTS), dtype=torch.int32, device=dev)
-        self.state = torch.zeros((num_sh, 4), dtype=torch.int32, device=dev)
+        self.state = torch.zeros((num_sh, 2, 4), dtype=torch.int32, device=dev)
         n = lib.sphkv_decode_paged_workspace_bytes(self.num_items, self.gqa, dh)
         if n < 0:
             raise ValueError("bad gqa / dh for the decode workspace")
         self.workspace = torch.zeros(max(int(n), 4), dtype=torch.uint8, device=dev)
         self._plan = None
-        self._bind(0, 0)
+        self._bind(0, 0, 0)
 
-    def _bind(self, staged: int, flushed: int) -> None:
+    def _bind(self, staged: int, flushed: int, parity: int) -> None:
         import ctypes
         lib = load()
         if self._plan is not None:
@@ -568,7 +581,7 @@ class DecodeTail:
             self.positions.data_ptr(), self.num_rows, pool.v_pool.data_ptr(), self.num_vpages, c1, c2, c3,
             self.work.data_ptr(), self.num_items, self.work_start.data_ptr(), plan.num_seqs, plan.num_kv, self.gqa,
             self.stg_r.data_ptr(), self.stg_code.data_ptr(), self.stg_v.data_ptr(), self.stg_pos.data_ptr(),
-            self.state.data_ptr(), self.dec_byte0, self.dec_vpage0, self.capacity, staged, flushed,
+            self.state.data_ptr(), self.dec_byte0, self.dec_vpage0, self.capacity, staged, flushed, parity,
             self.workspace.data_ptr(), self.workspace.numel(), plan.dh, plan.page_size, self.sm_scale,
             self.rope_theta, ctypes.byref(h))
         check(rc, "sphkv_step_plan_create")
@@ -582,12 +595,13 @@ class DecodeTail:
         except Exception:
             pass
 
-    def counts(self) -> Tuple[int, int]:
-        """(staged tokens, flushed decode pages) per (seq, head)."""
+    def counts(self) -> Tuple[int, int, int]:
+        """(staged tokens, flushed decode pages, step parity) per (seq, head)."""
         import ctypes
-        a, b = ctypes.c_int32(), ctypes.c_int32()
-        check(load().sphkv_step_plan_counts(self._plan, ctypes.byref(a), ctypes.byref(b)), "sphkv_step_plan_counts")
-        return int(a.value), int(b.value)
+        a, b, p = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        check(load().sphkv_step_plan_counts(self._plan, ctypes.byref(a), ctypes.byref(b), ctypes.byref(p)),
+              "sphkv_step_plan_counts")
+        return int(a.value), int(b.value), int(p.value)
 
     @property
     def staged(self) -> int:
@@ -602,7 +616,7 @@ class DecodeTail:
         back to the prefill rows).  Asynchronous, current stream."""
         self.state.zero_()
         self.work.copy_(torch.as_tensor(self._work0), non_blocking=False)
-        self._bind(0, 0)
+        self._bind(0, 0, 0)
 
     def runner(self):
         """The fastest call of a step: fn(q_ptr, k_ptr, k_is_fp32, v_ptr, pos_ptr, out_ptr, mode) with raw
@@ -628,6 +642,8 @@ class DecodeTail:
             raise ValueError("cur_pos must be [num_seqs]")
 
     def _call(self, q, k_new, v_new, cur_pos, out, mode: int) -> None:
+        if self.pool.pages is not self._pages or self.pool.v_pool is not self._v_pool:
+            raise ValueError("the pool's byte pool or V pool was replaced after the DecodeTail was attached")
         rc = self._run(self._plan, _ptr(q), k_new.data_ptr(), 1 if k_new.dtype == torch.float32 else 0,
                        v_new.data_ptr(), cur_pos.data_ptr(), _ptr(out), mode, _stream())
         if rc != 0:
@@ -637,8 +653,10 @@ class DecodeTail:
             check(rc, "sphkv_step_plan_run")
 
     def state_host(self) -> Dict[str, np.ndarray]:
-        """Copies of the tail state (waits for the current stream)."""
-        return {"state": self.state.cpu().numpy(), "stg_r": self.stg_r.cpu().numpy(),
+        """Copies of the tail state (waits for the current stream); "state" is
+        the copy of the counts the next step reads ([num_sh, 4])."""
+        par = self.counts()[2]
+        return {"state": self.state[:, par].cpu().numpy(), "stg_r": self.stg_r.cpu().numpy(),
                 "stg_code": self.stg_code.cpu().numpy(), "stg_v": self.stg_v.cpu().numpy(),
                 "stg_pos": self.stg_pos.cpu().numpy(), "work": self.work.cpu().numpy()}
 

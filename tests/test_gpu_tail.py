@@ -173,3 +173,11 @@ def test_decode_step_capacity_is_enforced(gpu):
         ops.decode_append(pool, tail, _dev(st.k[15], gpu), _dev(st.v[15], gpu), _dev(st.pos[15], gpu))
     torch.cuda.synchronize()
     assert int(tail.state_host()["state"][:, 0].min()) == 15
+
+
+def test_second_tail_on_a_pool_is_refused(gpu):
+    # two tails would share one decode-page region (or reallocate the pool
+    # under the first tail's bound plan)
+    wl, st, pool, cpu, tail, orc = _setup(gpu, config=1, ctx=256, steps=1, capacity=1)
+    with pytest.raises(ValueError, match="already has a DecodeTail"):
+        ops.DecodeTail(pool, wl.gqa, wl.rope_theta, capacity=1)
