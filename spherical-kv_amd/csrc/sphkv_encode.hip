@@ -103,6 +103,20 @@ struct EncodeLds {
 //     every code whose exact score equals the exact maximum passes the test.
 //     No candidate (NaN similarities) falls back to scoring every code.
 constexpr float kCandSlack = 5e-3f;
+// The bound above scales with |c|: it holds, inside the slack, for rows with
+// |c|^2 within kUnitTol of 1.  A staged codebook with any other row (scaled
+// or unnormalised rows: _encode_keys_with_codebooks accepts any codebook,
+// only codebook_loader.py:43-44 normalises) is scored exactly over every
+// code.
+constexpr float kUnitTol = 0.1f;
+
+// Does any staged row (lane < C: its 16 values) leave the unit-row bound?
+__device__ __forceinline__ bool rows_not_unit(const float4 (&row)[4], int lane, int C) {
+  float n2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) n2 += row[i].x * row[i].x + row[i].y * row[i].y + row[i].z * row[i].z + row[i].w * row[i].w;
+  return __builtin_amdgcn_ballot_w64(lane < C && !(fabsf(n2 - 1.f) <= kUnitTol)) != 0;   // NaN: not unit
+}
 
 // Nearest centroid of one (token, group) against the codebook rows cbg[c * GG ..]
 // (wave-uniform, so every centroid coordinate is a scalar operand): the fmaf
@@ -247,6 +261,7 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
         for (int i = 0; i < 4; ++i)
           crow[i] = lane < C0 ? *reinterpret_cast<const float4*>(cbg + lane * 16 + 4 * i) : float4{0.f, 0.f, 0.f, 0.f};
       }
+      bool exact_all = rows_not_unit(crow, lane, C0);
       // do all g = 16 pages of the workgroup use (tid0, h0)?
       bool same = true;
 #pragma unroll
@@ -340,7 +355,8 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
       auto score = [&](uint32_t lo, uint32_t hi, int C) {
         uint64_t mk = (uint64_t)lo | ((uint64_t)hi << 32);
         if (C < 64) mk &= (1ull << C) - 1;
-        if (mk == 0) mk = C == 64 ? ~0ull : ((1ull << C) - 1);      // NaN similarities: score every code
+        if (mk == 0 || exact_all) mk = C == 64 ? ~0ull : ((1ull << C) - 1);   // NaN similarities or
+                                                                                // non-unit rows: every code
         const bool naive = ord_l * 16 * C < 400;                     // torch's own small-bmm loop
         const bool m1 = !naive && ord_l == 1;                        // MKL's M = 1 kernel
         float best_sim = 0.f;
@@ -386,11 +402,15 @@ __global__ __launch_bounds__(kEncWaves * 64) void encode_pages_kernel(EncodeArgs
           if (tid != st_tid || h != st_h) {
             wave_lds_sync();
             const float* cbg = a.cb[tid] + ((int64_t)h * (DH / 16) + gi) * C * 16;
+            float4 row[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              row[i] = lane < C ? *reinterpret_cast<const float4*>(cbg + lane * 16 + 4 * i) : float4{0.f, 0.f, 0.f, 0.f};
             if (lane < C) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<float4*>(&cbs[lane][4 * i]) = *reinterpret_cast<const float4*>(cbg + lane * 16 + 4 * i);
+              for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&cbs[lane][4 * i]) = row[i];
             }
+            exact_all = rows_not_unit(row, lane, C);
             st_tid = tid;
             st_h = h;
             wave_lds_sync();

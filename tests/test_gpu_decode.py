@@ -426,3 +426,40 @@ def test_decode_malformed_rows_are_skipped_and_counted(gpu):
     assert err <= TOL and torch.isfinite(out).all()
     ops.decode_paged(pool, q, wl.gqa, wl.rope_theta, workspace=ws)
     assert ops.decode_status(pool, ws, wl.gqa) == 0
+
+
+@pytest.mark.parametrize("config,heads", [(2, None), (5, 2)])
+def test_decode_peaked_softmax_with_sink(gpu, config, heads):
+    # One dense sink token (position 0) 25 log2 units above a long, quiet
+    # tail, with one work item per (seq, head): at config 5 every wave then
+    # walks ~680 pages whose weights sit 2^-25 below the running maximum
+    # (the sink's); the tail still carries 2^17 * 2^-25 of the mass.  The
+    # output must match the fp64 oracle within the north-star tolerance.
+    from gpu_helpers import check_sampled_heads
+    wl = synth.make_decode_workload(config, num_seqs_override=1 if config == 5 else None)
+    D = fmt.DENSE_TIER_ID
+    q = wl.q[0].astype(np.float64)
+    for h in range(wl.num_kv):
+        K = wl.K[0][h].astype(np.float32)
+        K[1:] *= 0.02                                          # a quiet tail
+        qs = q[h * wl.gqa:(h + 1) * wl.gqa]
+        u = qs.sum(axis=0)
+        u /= np.linalg.norm(u)
+        gap = (qs @ u) / np.sqrt(wl.dh)                        # natural-log logit per unit of sink norm
+        K[0] = (25.0 * np.log(2.0) / gap.min()) * u           # every q head >= 25 log2 units above
+        wl.K[0][h] = K.astype(np.float16)
+        wl.tier_of[h][0] = D
+    wl.plan = fmt.plan_pages(wl.tier_of, None, 1, wl.num_kv, wl.dh, 16, rng=np.random.default_rng(7))
+    log(f"peaked softmax config{config}: rows={wl.plan.num_rows}, one item per head")
+    pool, _, _ = ops.build_pool_gpu(wl, gpu, rows_per_item=1 << 22)
+    assert pool.num_items == wl.num_kv
+    out = ops.decode_paged(pool, torch.as_tensor(wl.q, device=gpu), wl.gqa, wl.rope_theta, check=True)
+    torch.cuda.synchronize()
+    if heads is None:
+        cpu = oracle.build_pool(wl)
+        want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+        err = max_err(out.float().cpu().numpy(), want)
+        log(f"  all heads: max abs err {err:.3e}")
+        assert err <= TOL
+    else:
+        check_sampled_heads(wl, pool, out, heads, seed=55, tol=TOL)

@@ -142,3 +142,48 @@ def test_encode_near_ties_and_degenerate_groups(gpu):
     assert (c[comp] == cpu["codes"][comp]).all(), f"{int((c[comp] != cpu['codes'][comp]).sum())} codes differ"
     assert (r[comp].view(np.uint32) == cpu["r"][comp].view(np.uint32)).all()
     assert (pool.pages.cpu().numpy() == cpu["pages"]).all()
+
+
+@pytest.mark.parametrize("kind", ["scaled", "raw", "near_unit"])
+def test_encode_non_unit_codebooks_bit_exact(gpu, kind):
+    # _encode_keys_with_codebooks (spherical_kv_pipeline.py:1130-1144) takes
+    # any codebook; only codebook_loader.py:43-44 normalises the rows.  Rows
+    # scaled by 0.5..3, raw N(0,1) rows, and rows 1% off unit length (inside
+    # the pre-ranking bound) must all give the oracle's codes, radii and pages.
+    rng = np.random.default_rng({"scaled": 31, "raw": 32, "near_unit": 33}[kind])
+    dh, H, L = 128, 2, 200
+    tier_of = [rng.choice(np.array([1, 2, 3], np.int32), size=L) for _ in range(H)]
+    cbs = synth.make_codebooks(rng, H, dh, [1, 2, 3])
+    for tid, cb in cbs.items():
+        if kind == "scaled":
+            cb *= rng.uniform(0.5, 3.0, size=cb.shape[:-1] + (1,)).astype(np.float32)
+        elif kind == "raw":
+            cb[:] = rng.standard_normal(cb.shape).astype(np.float32)
+        else:
+            cb *= np.float32(1.01)
+    # keys on near-ties of the scaled rows: c_a + c_b and c_a + 1e-3 c_b, plus plain ones
+    K = np.zeros((H, L, dh), np.float32)
+    for h in range(H):
+        for t in range(L):
+            cb = cbs[int(tier_of[h][t])][h]
+            G, C, g = cb.shape
+            for j in range(G):
+                a, b = rng.choice(C, size=2, replace=False)
+                m = (t + j) % 3
+                v = cb[j, a] + cb[j, b] if m == 0 else (cb[j, a] + np.float32(1e-3) * cb[j, b] if m == 1
+                                                         else rng.standard_normal(g).astype(np.float32))
+                K[h, t, j * g:(j + 1) * g] = v
+    V = [rng.standard_normal((H, L, dh)).astype(np.float16)]
+    plan = fmt.plan_pages(tier_of, None, 1, H, dh, 16, rng=rng, num_vpages=None)
+    wl = synth.Workload(name=f"nonunit_{kind}", dh=dh, num_kv=H, gqa=1, num_seqs=1, lengths=[L], rope_theta=5e5,
+                        codebooks=cbs, K=[K.astype(np.float16)], V=V, q=np.zeros((1, H, dh), np.float16),
+                        tier_of=tier_of, plan=plan)
+    log(f"encode non-unit codebooks ({kind}) rows={plan.num_rows}")
+    pool, r_out, c_out = ops.build_pool_gpu(wl, gpu, with_codes=True)
+    torch.cuda.synchronize()
+    cpu = oracle.build_pool(wl, with_codes=True)
+    r, c = r_out.cpu().numpy(), c_out.cpu().numpy()
+    comp = wl.plan.tier != fmt.DENSE_TIER_ID
+    assert (c[comp] == cpu["codes"][comp]).all(), f"{int((c[comp] != cpu['codes'][comp]).sum())} codes differ"
+    assert (r[comp].view(np.uint32) == cpu["r"][comp].view(np.uint32)).all()
+    assert (pool.pages.cpu().numpy() == cpu["pages"]).all()
