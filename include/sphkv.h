@@ -152,7 +152,7 @@ int sphkv_decode_paged(const uint8_t* pages, int64_t pages_bytes, const int32_t*
  * live in a device array of the library (SPHKV_NOALLOC_SCRATCH_BYTES per GPU,
  * held until the process ends); the call allocates nothing and returns
  * SPHKV_EINVAL when sphkv_decode_paged_workspace_bytes(num_items, gqa, dh)
- * exceeds that size (8 MiB: 3,970 work items at gqa 4 / dh 128, 2,016 at
+ * exceeds that size (8 MiB: 3,971 work items at gqa 4 / dh 128, 2,016 at
  * gqa 8).  All calls on one GPU share that GPU's array: calls that overlap
  * on one GPU (several streams or threads) race.  Results equal
  * sphkv_decode_paged's on the same inputs.  Malformed pages are skipped as
@@ -172,8 +172,8 @@ int sphkv_decode_paged_noalloc(const uint8_t* pages, int64_t pages_bytes, const 
 /*
  * Malformed input.  The decode never reads outside the buffers it is given;
  * a pointer-table row that does not address the pools, a page whose tier id
- * is not 1, 2, 3 or 0xFF, a count above page_size, a dense page whose K rows
- * are not 16-byte aligned inside its theta section, or a compressed page
+ * is not 1, 2, 3 or 0xFF, a count above page_size, a non-empty dense page
+ * whose K rows are not 16-byte aligned inside its theta section, or a compressed page
  * whose sections leave the byte pool (or the 512 bytes from its page's 16-byte
  * line) contributes no token, and is counted in the workspace's status word.
  *

@@ -233,8 +233,9 @@ __device__ __forceinline__ int page_check(const DecodeArgs& a, const PageRows& r
     thr = sec_ok ? t0 : 0;
     rdr = sec_ok ? r0 : 0;
   } else if (dense) {
+    // an empty dense page (count 0, rad_off == th_off) is well formed
     const uint32_t kend = (uint32_t)r.th_off + (uint32_t)(n * DH * 2);
-    const bool dense_ok = t.dbase != kOOB && kend <= (uint32_t)r.rad_off && kend <= (uint32_t)a.pages32;
+    const bool dense_ok = n == 0 || (t.dbase != kOOB && kend <= (uint32_t)r.rad_off && kend <= (uint32_t)a.pages32);
     bad = bad || !dense_ok;
     n = dense_ok ? n : 0;
   }

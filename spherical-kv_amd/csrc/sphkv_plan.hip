@@ -4,11 +4,18 @@
 // without a host round trip per (layer, head, tier).
 //
 // The plan equals sphkv_format.plan_pages with logical placement: for each
-// (sequence, kv head) the rows of its pages, tiers in order of first
-// appearance (the reference's dict insertion order), token indices ascending
-// within a tier, chunks of 16; pages placed back to back in row order at
-// 16-byte aligned offsets (a dense fp16 page so that its payload after the
-// 8-byte header is 16-byte aligned).
+// (sequence, kv head) the rows of its pages, tiers in order of their smallest
+// token index, token indices ascending within a tier, chunks of 16; pages
+// placed back to back in row order at 16-byte aligned offsets (a dense fp16
+// page so that its payload after the 8-byte header is 16-byte aligned).
+//
+// The reference orders a head's tiers by first appearance in allocate()'s
+// retained list, sinks + recents + the rest (allocation.py:207-217; dict
+// insertion order, spherical_kv_pipeline.py:1156-1162).  Smallest index
+// gives the same order when every sink and recent token carries token 0's
+// tier, as with the protected tier at SINK_TOKENS=4, RECENT_WINDOW=256
+// (config.py:14-15); a caller whose recents carry another tier than its
+// sinks gets index order.
 //
 // Kernels (a (sequence, head)'s tokens are cut into chunks of kPlanChunk):
 //   plan_count_kernel  per (sequence, head, chunk): tokens and first index

@@ -395,7 +395,9 @@ def test_decode_malformed_rows_past_the_first_page_table(gpu):
 def test_decode_malformed_rows_are_skipped_and_counted(gpu):
     # five malformed rows of different kinds: each contributes no token, the
     # checked entry reports all five, the output equals the oracle over the
-    # other rows, and a clean decode on the same workspace reports zero again
+    # other rows, and a clean decode on the same workspace reports zero again.
+    # An empty dense page (count 0, radius offset = theta offset) is well
+    # formed: no token, not counted
     wl = synth.make_decode_workload(2, ctx_override=3000)
     pool, cpu = pool_from_oracle(wl, gpu)
     plan = wl.plan
@@ -403,14 +405,17 @@ def test_decode_malformed_rows_are_skipped_and_counted(gpu):
     dense = [p for p in range(rs[0], rs[1]) if plan.tier[p] == fmt.DENSE_TIER_ID]
     comp = [p for p in range(rs[2], rs[3]) if plan.tier[p] == 1]
     r_off, r_vs, r_tier, r_dense, r_sec = int(rs[1]) + 3, int(rs[4]) + 1, int(rs[5]) + 2, dense[1], comp[4]
+    r_empty = dense[2]
     pt = plan.ptable.copy()
     vs = plan.vslot.copy()
     pt[r_off, 0] = -16                                 # page offset outside the pool
     vs[r_vs] = plan.num_vpages + 5                     # V slot outside the V pool
     pt[r_dense, 1] += 2                                # dense K rows not 16-byte aligned
     pt[r_sec, 2] += 600                                # radius section beyond the 512-byte window
+    pt[r_empty, 2] = pt[r_empty, 1]                    # empty dense page: no K rows
     pages = pool.pages.clone()
     pages[int(plan.ptable[r_tier, 0])] = 7             # unknown tier id
+    pages[int(plan.ptable[r_empty, 0]) + 1] = 0        # its count byte
     bad = ops.PagedPool(**{**pool.__dict__, "ptable": torch.as_tensor(pt, device=gpu),
                            "vslot": torch.as_tensor(vs, device=gpu), "pages": pages})
     q = torch.as_tensor(wl.q, device=gpu)
@@ -419,8 +424,8 @@ def test_decode_malformed_rows_are_skipped_and_counted(gpu):
     assert ops.decode_status(bad, ws, wl.gqa) == 5
     with pytest.raises(Exception, match="5 malformed"):
         ops.decode_paged(bad, q, wl.gqa, wl.rope_theta, workspace=ws, check=True)
-    want = oracle.decode_mode_b(cpu, _drop_rows(plan, [r_off, r_vs, r_tier, r_dense, r_sec]), wl.codebooks,
-                                wl.q, wl.gqa, wl.rope_theta)
+    want = oracle.decode_mode_b(cpu, _drop_rows(plan, [r_off, r_vs, r_tier, r_dense, r_sec, r_empty]),
+                                wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
     err = max_err(out.float().cpu().numpy(), want)
     log(f"  malformed rows skipped: max abs err {err:.3e} against the oracle without them")
     assert err <= TOL and torch.isfinite(out).all()

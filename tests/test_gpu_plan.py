@@ -49,9 +49,9 @@ def _row_base(lengths, num_kv):
     return np.asarray(base, np.int64)
 
 
-def _check(dp, tier_of, lengths, num_kv, base=None, positions_of=None):
+def _check(dp, tier_of, lengths, num_kv, base=None, positions_of=None, sink=0, recent=0):
     plan = dp.to_host()
-    groups = paging.group_pages(paging.retained_tokens(tier_of, len(lengths), num_kv))
+    groups = paging.group_pages(paging.retained_tokens(tier_of, len(lengths), num_kv, sink=sink, recent=recent))
     paging.check_plan(plan, groups, positions_of=positions_of)
     # placement invariants
     ops.validate_plan(plan)
@@ -150,3 +150,28 @@ def test_device_plan_many_ranges_and_many_chunks(gpu):
     dp = ops.plan_pages_gpu(t, lens, 1, 64)
     log(f"140000 tokens: rows {dp.rows} pool bytes {dp.pages_bytes}")
     _check(dp, tier_of, lengths, 1)
+
+
+def test_device_plan_follows_allocate_order_at_reference_defaults(gpu):
+    # the reference orders a head's tiers by first appearance in allocate()'s
+    # sinks + recents + rest list (SINK_TOKENS=4, RECENT_WINDOW=256,
+    # config.py:14-15); the device planner by smallest token index.  With
+    # the sinks and recents at the protected tier (token 0 is a sink) the
+    # two orders agree: checked against the list order itself, on heads
+    # shorter than, equal to and longer than sink + recent tokens
+    rng = np.random.default_rng(12)
+    num_kv, dh = 4, 128
+    lengths = [3, 260, 261, 700, 2500]
+    tier_of = []
+    for L in lengths:
+        for h in range(num_kv):
+            t = rng.choice(np.array([0, 1, 2, 3]), size=L, p=[.2, .3, .3, .2]).astype(np.int32)
+            prot = [fmt.DENSE_TIER_ID, 3][h % 2]                   # the protected tier of this head
+            t[:4] = prot
+            t[max(0, L - 256):] = prot
+            tier_of.append(t)
+    t, lens, _ = _device_inputs(tier_of, lengths, num_kv, gpu)
+    base = _row_base(lengths, num_kv)
+    dp = ops.plan_pages_gpu(t, lens, num_kv, dh, row_base=torch.from_numpy(base).to(gpu))
+    log(f"sink 4 / recent 256: rows {dp.rows} pool bytes {dp.pages_bytes}")
+    _check(dp, tier_of, lengths, num_kv, base, sink=4, recent=256)

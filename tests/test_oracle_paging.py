@@ -125,3 +125,25 @@ def test_check_plan_rejects_a_wrong_tier_order():
     swapped = sorted(ret, key=lambda r: r.tier != 1)     # same tokens, tier 1 now appears first
     with pytest.raises(AssertionError, match="tier 2 != 1"):
         paging.check_plan(plan, paging.group_pages(swapped))
+
+
+def test_host_planner_index_order_is_allocate_order_at_reference_defaults():
+    # the planners order tiers by smallest token index; allocate() returns
+    # sinks + recents + rest (SINK_TOKENS=4, RECENT_WINDOW=256).  They agree
+    # when sinks and recents carry token 0's (protected) tier, and differ
+    # when the recents carry a tier that first appears later in index order
+    rng = np.random.default_rng(12)
+    lengths, num_kv = [3, 260, 261, 700], 2
+    tier_of = []
+    for L in lengths:
+        for h in range(num_kv):
+            t = rng.choice(np.array([0, 1, 2, 3]), size=L, p=[.2, .3, .3, .2]).astype(np.int32)
+            t[:4] = t[max(0, L - 256):] = [D, 3][h]
+            tier_of.append(t)
+    plan = fmt.plan_pages(tier_of, None, len(lengths), num_kv, 128)
+    paging.check_plan(plan, paging.group_pages(paging.retained_tokens(tier_of, len(lengths), num_kv, 4, 256)))
+    t = np.full(300, 1, np.int32)
+    t[:4], t[100], t[-256:] = D, 2, 3                    # index order D, 1, 2, 3; list order D, 3, 1, 2
+    plan = fmt.plan_pages([t], None, 1, 1, 128)
+    with pytest.raises(AssertionError):
+        paging.check_plan(plan, paging.group_pages(paging.retained_tokens([t], 1, 1, 4, 256)))
