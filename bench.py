@@ -369,18 +369,33 @@ def bench_modea(args, dev):
 def bench_ragged(args, dev):
     """fused_decode_ragged (logits only, the reference's tiered call,
     spherical_kv_pipeline.py:1860-1875): one step = one call per compressed
-    tier over config 2's pages of that tier, all kv heads.  Algorithmic bytes
-    per call: the tier's pages, positions and logits plus the cos / sin rows
-    (first halves) of the distinct positions.  CPU baseline: the oracle's fp64
-    restatement on a bounded sample of pages, scaled by page count."""
+    tier over config 2's pages of that tier, all kv heads, with RoPE tables
+    built as the reference builds them (a default transformers rotary
+    embedding, :1597-1608; fp32 angles).  The tables are fitted on the first
+    call (untimed; its cost is reported) and the timed calls form the phases
+    in the kernel; --no-rope-fit reads the tables' rows instead.  Algorithmic
+    bytes per call: the tier's pointer-table rows, head ids, pages, positions
+    and logits, plus (table path only) the cos / sin rows (first halves) of the
+    distinct positions.  CPU baseline: the oracle's fp64 restatement on a
+    bounded sample of pages, scaled by page count."""
     import fused_decode
     import oracle
     log("[bench] building config2 workload for fused_decode_ragged")
     wl = synth.make_decode_workload(2)
     pool, _, _ = ops.build_pool_gpu(wl, dev)
     plan = wl.plan
-    cos_h, sin_h = fmt.rope_tables(max(wl.lengths) + 16, wl.dh, wl.rope_theta)
-    cos_t, sin_t = torch.as_tensor(cos_h, device=dev), torch.as_tensor(sin_h, device=dev)
+    max_pos = max(wl.lengths) + 64
+    if args.rope_tables == "hf":
+        cos_t, sin_t = synth.hf_rope_tables(max_pos, wl.dh, wl.rope_theta, dev)
+    else:
+        cos_t, sin_t = (torch.as_tensor(x, device=dev) for x in fmt.rope_tables(max_pos, wl.dh, wl.rope_theta))
+    cos_h, sin_h = cos_t.cpu().numpy(), sin_t.cpu().numpy()
+    fused_decode.use_rope_fit = not args.no_rope_fit
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model = fused_decode.rope_fit_info(cos_t, sin_t)[0] if fused_decode.use_rope_fit else 0
+    fit_ms = (time.perf_counter() - t0) * 1e3
+    log(f"[bench] RoPE tables ({args.rope_tables}): fit model {model} in {fit_ms:.2f} ms (once per table)")
     q_h = wl.q[0].astype(np.float32)
     q = torch.as_tensor(q_h, device=dev)
     calls, host, nbytes, npages = [], [], 0, 0
@@ -397,7 +412,8 @@ def bench_ragged(args, dev):
         host.append((rows, heads, pos, cb, G, g, b))
         n_tok = int((pos >= 0).sum())
         nbytes += (int(sum(fmt.page_nbytes(tid, int(n), wl.dh) for n in plan.count[rows])) + 4 * pos.size
-                   + 4 * wl.gqa * pos.size + 2 * 4 * (wl.dh // 2) * int(np.unique(pos[pos >= 0]).size))
+                   + 4 * wl.gqa * pos.size + 16 * rows.size
+                   + (0 if model else 2 * 4 * (wl.dh // 2) * int(np.unique(pos[pos >= 0]).size)))
         npages += rows.size
         log(f"[bench] tier {tid}: {rows.size} pages, {n_tok} tokens")
 
@@ -411,13 +427,16 @@ def bench_ragged(args, dev):
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
+    h0 = time.perf_counter()
     for i in range(args.steps):
         step(i)
+    host_us = (time.perf_counter() - h0) / args.steps * 1e6
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
     gbps = nbytes / (ms * 1e-3) / 1e9
-    log(f"[bench] fused_decode_ragged {ms * 1e3:.2f} us per step (tiers 1 + 2)  {gbps:.1f} GB/s")
+    log(f"[bench] fused_decode_ragged {ms * 1e3:.2f} us per step (tiers 1 + 2)  {gbps:.1f} GB/s; "
+        f"host {host_us:.2f} us per step to enqueue")
     cpu = None
     if not args.no_cpu_baseline:
         pages_h = pool.pages.cpu().numpy()
@@ -438,7 +457,9 @@ def bench_ragged(args, dev):
         "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "u8 codes, fp32 tables and math", "data": "synthetic (config 2 spec of BASELINE.json)",
         "config": {"workload": "config2 tier-1 and tier-2 pages (16 tokens), 8 kv heads, grp 4, dh 128",
-                   "pages": int(npages), "algorithmic_bytes_per_step": int(nbytes)},
+                   "pages": int(npages), "algorithmic_bytes_per_step": int(nbytes),
+                   "rope_tables": args.rope_tables, "rope_model": int(model), "rope_fit_once_ms": round(fit_ms, 2),
+                   "host_us_per_step": round(host_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": RAGGED_TRAFFIC_BYTES, "kernel": "ragged_pipe_kernel",
                      "kernel_us": round(ms * 1e3, 3)},
@@ -680,6 +701,9 @@ def main():
                          "the append; the headline); pages: the page-resident decode alone; modea: LayerPool "
                          "decode; prefill: device page plan + fused encode; ragged: fused_decode_ragged")
     ap.add_argument("--page-size", type=int, default=16, help="Mode-A page size (16..128, multiple of 16)")
+    ap.add_argument("--rope-tables", default="hf", choices=["hf", "exact"],
+                    help="ragged: RoPE tables of the HF construction (fp32 angles) or of exact angles")
+    ap.add_argument("--no-rope-fit", action="store_true", help="ragged: read the RoPE tables' rows every call")
     ap.add_argument("--calibrate", action="store_true",
                     help="after timing, run plain device copies of COPY_BYTES (torch copy_), the "
                          "reference kernel of known traffic for FETCH_SIZE / WRITE_SIZE counters")

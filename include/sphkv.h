@@ -371,6 +371,43 @@ int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const i
                               int32_t page_size, float* logits_out, void* stream);
 
 /*
+ * RoPE tables checked once, phases formed in the kernel.  No reference
+ * counterpart: the reference's callers pass the same cos / sin tables to
+ * every call (spherical_kv_pipeline.py:1102-1125, built once by
+ * _ensure_rope_tables :1591-1610 from the model's rotary embedding), and
+ * reading a row of each per token is the ragged kernel's largest read.
+ *
+ * sphkv_rope_table_fit: fits the tables [max_pos, dh] (HF layout: the second
+ * half of a row repeats the first) to a rotation per pair j and checks every
+ * entry on the device; waits for `stream`.  *model:
+ *   0  no fit: some entry is off both models by more than 2^-20, or a row's
+ *      halves differ (the tables are read as given)
+ *   1  cos / sin of exact angles 2 pi pos f_j (f_j fitted, fp64)
+ *   2  cos / sin of fp32 angles fl32(pos * inv_j) (inv_j fitted, fp32): the
+ *      HF construction, fp32 inv_freq times the fp32 position
+ * (model 1 is preferred when both hold).  fit: device memory of
+ * SPHKV_ROPE_FIT_BYTES, written with the frequencies; max_dev (host float[2],
+ * may be NULL): the largest deviation of models 1 and 2.  The fit describes
+ * the tables' contents at the time of the call: fit again after they change.
+ *
+ * sphkv_fused_decode_ragged_fitted: sphkv_fused_decode_ragged with the tables'
+ * fit: rope_model 1 or 2 (the model returned) forms each token's phases from
+ * it instead of reading the table rows (results within about 1e-6 of the
+ * table path's per logit unit); 0 reads the tables (rope_fit may be NULL).
+ * A fit of another model, dh or max_pos makes every logit NaN.
+ */
+#define SPHKV_ROPE_FIT_BYTES 1024
+int sphkv_rope_table_fit(const float* cos_tbl, const float* sin_tbl, int32_t max_pos, int32_t dh, void* fit,
+                         int32_t* model, float* max_dev, void* stream);
+int sphkv_fused_decode_ragged_fitted(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                                     const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
+                                     const float* cos_tbl, const float* sin_tbl, int32_t max_pos,
+                                     const float* q, int32_t grp, int32_t num_kv, const float* codebooks,
+                                     int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
+                                     int32_t page_size, const void* rope_fit, int32_t rope_model,
+                                     float* logits_out, void* stream);
+
+/*
  * ---- Mode-A (LayerPool) path -------------------------------------------
  * Unpacked pools as sphkv_lut.py:71-80 builds them:
  *   theta_codes, radius_codes  uint8 [num_pages, page_size, G_max]

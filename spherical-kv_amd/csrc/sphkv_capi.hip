@@ -1,6 +1,7 @@
 // extern "C" boundary of libsphkv.so (declarations: include/sphkv.h).
 // Host code only: argument validation, error reporting, kernel dispatch.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -497,27 +498,151 @@ int sphkv_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_ro
                                                    (hipStream_t)stream), fn);
 }
 
+static int ragged_call(const char* fn, const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                       const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
+                       const float* cos_tbl, const float* sin_tbl, int32_t max_pos,
+                       const float* q, int32_t grp, int32_t num_kv, const float* codebooks,
+                       int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
+                       int32_t page_size, const void* rope_fit, int32_t rope_model, float* logits_out,
+                       void* stream) {
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (group_size <= 0 || groups * group_size != dh || (group_size % 8) != 0)
+    return fail(SPHKV_EINVAL, "%s: groups*group_size must equal dh, group_size %% 8 == 0", fn);
+  if (b_theta < 1 || b_theta > 8) return fail(SPHKV_EINVAL, "%s: b_theta must be 1..8", fn);
+  if (page_size < 1 || page_size > 128)
+    return fail(SPHKV_EINVAL, "%s: page_size must be 1..128 (got %d)", fn, page_size);
+  if (num_pages < 0 || grp <= 0 || num_kv <= 0 || max_pos <= 0) return fail(SPHKV_EINVAL, "%s: bad size", fn);
+  if (rope_model < sphkv::kRopeNone || rope_model > sphkv::kRopeFp32 || (rope_model != sphkv::kRopeNone && !rope_fit))
+    return fail(SPHKV_EINVAL, "%s: rope_model must be 0, 1 or 2 (1 and 2 with a fit)", fn);
+  if (num_pages == 0) return ok();
+  if (!pages || !ptable || !head_ids || !positions || !cos_tbl || !sin_tbl || !q || !codebooks || !logits_out)
+    return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  sphkv::RaggedLaunch L{pages, pages_bytes, ptable, head_ids, positions, num_pages, cos_tbl, sin_tbl,
+                        max_pos, q, grp, num_kv, codebooks, dh, groups, group_size, b_theta,
+                        page_size, logits_out,
+                        rope_model != sphkv::kRopeNone ? static_cast<const sphkv::RopeFit*>(rope_fit) : nullptr,
+                        rope_model};
+  return launch_status(sphkv::launch_ragged(L, (hipStream_t)stream), fn);
+}
+
 int sphkv_fused_decode_ragged(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
                               const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
                               const float* cos_tbl, const float* sin_tbl, int32_t max_pos,
                               const float* q, int32_t grp, int32_t num_kv, const float* codebooks,
                               int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
                               int32_t page_size, float* logits_out, void* stream) {
-  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: dh must be 64 or 128 (got %d)", dh);
-  if (group_size <= 0 || groups * group_size != dh || (group_size % 8) != 0)
-    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: groups*group_size must equal dh, group_size %% 8 == 0");
-  if (b_theta < 1 || b_theta > 8) return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: b_theta must be 1..8");
-  if (page_size < 1 || page_size > 128)
-    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: page_size must be 1..128 (got %d)", page_size);
-  if (num_pages < 0 || grp <= 0 || num_kv <= 0 || max_pos <= 0)
-    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: bad size");
-  if (num_pages == 0) return ok();
-  if (!pages || !ptable || !head_ids || !positions || !cos_tbl || !sin_tbl || !q || !codebooks || !logits_out)
-    return fail(SPHKV_EINVAL, "sphkv_fused_decode_ragged: null pointer argument");
-  sphkv::RaggedLaunch L{pages, pages_bytes, ptable, head_ids, positions, num_pages, cos_tbl, sin_tbl,
-                        max_pos, q, grp, num_kv, codebooks, dh, groups, group_size, b_theta,
-                        page_size, logits_out};
-  return launch_status(sphkv::launch_ragged(L, (hipStream_t)stream), "sphkv_fused_decode_ragged");
+  return ragged_call("sphkv_fused_decode_ragged", pages, pages_bytes, ptable, head_ids, positions, num_pages,
+                     cos_tbl, sin_tbl, max_pos, q, grp, num_kv, codebooks, dh, groups, group_size, b_theta,
+                     page_size, nullptr, sphkv::kRopeNone, logits_out, stream);
+}
+
+int sphkv_fused_decode_ragged_fitted(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                                     const int32_t* head_ids, const int32_t* positions, int32_t num_pages,
+                                     const float* cos_tbl, const float* sin_tbl, int32_t max_pos,
+                                     const float* q, int32_t grp, int32_t num_kv, const float* codebooks,
+                                     int32_t dh, int32_t groups, int32_t group_size, int32_t b_theta,
+                                     int32_t page_size, const void* rope_fit, int32_t rope_model,
+                                     float* logits_out, void* stream) {
+  return ragged_call("sphkv_fused_decode_ragged_fitted", pages, pages_bytes, ptable, head_ids, positions,
+                     num_pages, cos_tbl, sin_tbl, max_pos, q, grp, num_kv, codebooks, dh, groups, group_size,
+                     b_theta, page_size, rope_fit, rope_model, logits_out, stream);
+}
+
+int sphkv_rope_table_fit(const float* cos_tbl, const float* sin_tbl, int32_t max_pos, int32_t dh, void* fit,
+                         int32_t* model, float* max_dev, void* stream) {
+  const char* fn = "sphkv_rope_table_fit";
+  if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
+  if (max_pos < 1 || max_pos > (1 << 24))
+    return fail(SPHKV_EINVAL, "%s: max_pos must be 1..2^24 (got %d)", fn, max_pos);
+  if (!cos_tbl || !sin_tbl || !fit || !model) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  const hipStream_t s = (hipStream_t)stream;
+  const int half = dh / 2;
+  constexpr double kTwoPi = 6.283185307179586;
+  sphkv::RopeFit h;
+  memset(&h, 0, sizeof(h));
+  h.model = sphkv::kRopeNone;
+  h.dh = dh;
+  h.max_pos = max_pos;
+  // rows 1, 2, 4, ... and the last: each pair's frequency is read from row
+  // 1 (atan2, turns) and refined on each later row, whose angle is unwrapped
+  // by the previous estimate (an estimate good to e turns per token predicts
+  // row 2r to 2 r e turns, far inside the half turn the unwrap needs)
+  int rows[40];
+  int nr = 0;
+  for (int64_t r = 1; r < max_pos; r *= 2) rows[nr++] = (int)r;
+  if (nr > 0 && rows[nr - 1] != max_pos - 1) rows[nr++] = max_pos - 1;
+  float* hc = nullptr;
+  if (nr > 0) {
+    hc = new (std::nothrow) float[2 * (size_t)nr * dh];
+    if (!hc) return fail(SPHKV_EINVAL, "%s: host allocation failed", fn);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < nr && e == hipSuccess; ++i) {
+      e = hipMemcpyAsync(hc + (size_t)i * dh, cos_tbl + (int64_t)rows[i] * dh, dh * 4, hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(hc + (size_t)(nr + i) * dh, sin_tbl + (int64_t)rows[i] * dh, dh * 4,
+                           hipMemcpyDeviceToHost, s);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      delete[] hc;
+      return fail(SPHKV_ELAUNCH, "%s: reading the tables failed: %s", fn, hipGetErrorString(e));
+    }
+    for (int j = 0; j < half; ++j) {
+      const float* c = hc;
+      const float* sn = hc + (size_t)nr * dh;
+      double f = atan2((double)sn[j], (double)c[j]) / kTwoPi;
+      for (int i = 1; i < nr; ++i) {
+        const double t = atan2((double)sn[(size_t)i * dh + j], (double)c[(size_t)i * dh + j]) / kTwoPi;
+        f = (t + nearbyint(rows[i] * f - t)) / rows[i];
+      }
+      h.f[j] = f;
+      // the fp32 inverse frequency: of the floats within 4 ulps of 2 pi f,
+      // the one whose fp32 angles best reproduce the ladder rows
+      float cand = (float)(f * kTwoPi);
+      for (int k = 0; k < 4; ++k) cand = nextafterf(cand, -INFINITY);
+      float best = cand;
+      double best_dev = INFINITY;
+      for (int k = 0; k < 9; ++k, cand = nextafterf(cand, INFINITY)) {
+        double dev = 0.0;
+        for (int i = 0; i < nr; ++i) {
+          const float a = (float)rows[i] * cand;
+          dev = fmax(dev, fmax(fabs((double)c[(size_t)i * dh + j] - cos((double)a)),
+                               fabs((double)sn[(size_t)i * dh + j] - sin((double)a))));
+        }
+        if (dev < best_dev) {
+          best_dev = dev;
+          best = cand;
+        }
+      }
+      h.inv32[j] = best;
+    }
+    delete[] hc;
+  }
+  // every entry against both models (on the device), then the choice
+  sphkv::RopeFit* d = static_cast<sphkv::RopeFit*>(fit);
+  sphkv::RopeFit back;
+  hipError_t e = hipMemcpyAsync(d, &h, sizeof(h), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && sphkv::launch_rope_check(cos_tbl, sin_tbl, max_pos, dh, d, s) != 0) e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(&back, d, 32, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(SPHKV_ELAUNCH, "%s: the table check failed: %s", fn, hipGetErrorString(e));
+  float dev[2];
+  memcpy(&dev[0], &back.dev_bits[0], 4);
+  memcpy(&dev[1], &back.dev_bits[1], 4);
+  int32_t m = sphkv::kRopeNone;
+  if (nr > 0 && back.half_mismatch == 0) {
+    if (dev[0] <= sphkv::kRopeFitTol) m = sphkv::kRopeExact;
+    else if (dev[1] <= sphkv::kRopeFitTol) m = sphkv::kRopeFp32;
+  }
+  e = hipMemcpyAsync(&d->model, &m, 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(SPHKV_ELAUNCH, "%s: writing the fit failed: %s", fn, hipGetErrorString(e));
+  *model = m;
+  if (max_dev) {
+    max_dev[0] = dev[0];
+    max_dev[1] = dev[1];
+  }
+  return ok();
 }
 
 }  // extern "C"

@@ -397,6 +397,8 @@ __device__ __forceinline__ int xcd_item(int b, int nb) {
   return (b & 7) * (full >> 3) + (b >> 3);
 }
 
+constexpr double kInvTwoPi = 0.15915494309189535;      // 1 / (2 pi), rounded to fp64
+
 // e^{i 2 pi x} with x a phase in turns (fp32 hardware sine/cosine take turns).
 __device__ __forceinline__ float2 turn_phasor(double x) {
   const float ph = (float)__builtin_amdgcn_fract(x);
@@ -529,7 +531,7 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // workgroup has a multiple of NJ threads, so the delta-table entries
   // (d, j) = i, i = threadIdx.x + k * kT, of a thread all have its own j: the
   // table is built from registers while the first loads are in flight.
-  const double f_lane = exp2(-(2.0 * (lane % NJ) / DH) * a.log2_theta) * 0.15915494309189535;  // / (2 pi)
+  const double f_lane = exp2(-(2.0 * (lane % NJ) / DH) * a.log2_theta) * kInvTwoPi;  // / (2 pi)
   static_assert((kWaves * 64) % NJ == 0, "delta-table rows need whole frequency runs per thread");
   if (wave == 0 && lane < NJ) ftab[lane] = f_lane;       // the far pages' phasors read it
   for (int i = threadIdx.x; i < kDelta * NJ; i += kT) {
@@ -1194,7 +1196,7 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   const int pos_new = __builtin_amdgcn_readfirstlane(pos_ld);
 
   // ---- shared tables; the new token's encode -------------------------------
-  if (i < NJ) ftab[i] = exp2(-(2.0 * i / DH) * a.log2_theta) * 0.15915494309189535;   // inv_freq / 2 pi
+  if (i < NJ) ftab[i] = exp2(-(2.0 * i / DH) * a.log2_theta) * kInvTwoPi;   // inv_freq / 2 pi
 #pragma unroll
   for (int k = 0; k < NCB / 4 / kTailThreads; ++k) reinterpret_cast<float4*>(cbs)[i + k * kTailThreads] = cbv[k];
   if (cb_part) reinterpret_cast<float4*>(cbs)[i] = cbv[0];
@@ -1799,6 +1801,15 @@ __global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
 // is computed (vector loads only: scalar loads share a wait counter with the
 // LDS reads and return out of order, so a wait for LDS data would wait for
 // them too).  The arithmetic per chunk is ragged_fast_kernel's.
+//
+// RM (a RopeFit model): kRopeNone reads each token's cos / sin rows from the
+// caller's tables (16 rows of 2 x DH/2 floats per chunk, the kernel's largest
+// read); kRopeExact and kRopeFp32 form the same phasors in the kernel from
+// the fitted frequencies (every table entry within kRopeFitTol of them,
+// checked once per table by sphkv_rope_table_fit): the lane's pairs j turn by
+// 2 pi pos f[j] (exact angle) or by the fp32 angle fl32(pos * inv32[j])
+// reduced in fp64, on the hardware sine / cosine (turns).
+constexpr int kStage4 = 8;   // float4 per thread of a 32 KB LDS stage (256 threads)
 struct RagRow {          // round trip 1 of one chunk
   uint32_t w0, w1, w2;   // pointer-table row (page_off, th_off, rad_off)
   int hk, hb, pos;       // head of the chunk's page, head of the iteration's first chunk, slot position
@@ -1809,79 +1820,129 @@ struct RagPage {         // round trip 2 of one chunk, with its row's fields
   int rc[2];
   int page_off, th_off, rad_off, hk, hb, pos, p, c16;
 };
+// LDS rows of the pipelined kernel are padded by 4 floats, so that the 16
+// codebook rows (random codes) or the 4 q heads one read touches start in
+// different banks
+template <int GS> __host__ __device__ constexpr int rag_cb_stride() { return GS + 4; }
+template <int DH> __host__ __device__ constexpr int rag_q_stride() { return DH + 4; }
 
-template <int DH, int GS, int NHS>
+// Offsets are 32-bit: the launcher takes this kernel only for byte pools
+// below 2 GiB and fewer than 2^31 slots; a pointer-table row with a negative
+// offset reads nothing and contributes no token.
+template <int DH, int GS, int NHS, int RM>
 __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   constexpr int NPL = DH / 8, NM = NPL / 4;
   constexpr int G = DH / GS;
+  constexpr int QS = rag_q_stride<DH>(), CS = rag_cb_stride<GS>();
+  constexpr int SLOTS = 4 * NHS;                       // q rows per head in LDS (zeros past grp)
   extern __shared__ float rag_smem[];
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int t = lane & 15, u = lane >> 4;
   const int cpp = a.page_size / 16;
-  const int64_t nch = (int64_t)a.num_pages * cpp;
+  const int cpp_sh = (cpp & (cpp - 1)) == 0 ? __builtin_ctz(cpp) : -1;
+  const int nch = a.num_pages * cpp;
   // Work split for L2 locality.  Chunks come grouped by head, each head's in
   // ascending position, and every head covers about the same positions, so
   // [0, nch) is cut into S = NX * K equal segments (K per XCD, K ~ heads)
   // and XCD x (workgroups b with b mod NX = x; the dispatcher deals
   // workgroups to the 8 XCDs in turn) takes segments x, x + NX, ...: about
   // the same 1/NX of the positions of every head, so its L2 holds 1/NX of
-  // the cos / sin rows.  Its segments, concatenated, are cut into GPX equal
-  // runs, one per workgroup.  Any order of pages is still covered exactly
-  // once.  Lane k < K holds segment k's list range and chunk offset; a list
-  // position maps to a chunk by a ballot over that table.
+  // the cos / sin rows (table path) and a workgroup's run mostly stays in
+  // one head (one codebook stage).  Its segments, concatenated, are cut into
+  // GPX equal runs, one per workgroup.  Any order of pages is still covered
+  // exactly once.  Lane k < K holds segment k's list range and chunk offset;
+  // a list position maps to a chunk by a ballot over that table.
   const int NX = (gridDim.x % 8 == 0 && gridDim.x >= 64) ? 8 : 1;
   const int K = NX == 8 ? min(max(a.num_kv, 1), 8) : 1;
   const int S = NX * K, xcd = blockIdx.x % NX, GPX = gridDim.x / NX, wj = blockIdx.x / NX;
-  int64_t seg_end = 0, seg_base = 0;                   // lane k < K: list end and chunk - list offset of segment k
+  int seg_end = 0, seg_base = 0;                       // lane k < K: list end and chunk - list offset of segment k
   {
-    const int64_t sg = xcd + (int64_t)NX * lane;
-    const int64_t b0 = lane < K ? sg * nch / S : 0, b1 = lane < K ? (sg + 1) * nch / S : 0;
-    int64_t len = b1 - b0, incl = len;
+    const int sg = xcd + NX * lane;
+    const int b0 = lane < K ? (int)((int64_t)sg * nch / S) : 0;
+    const int b1 = lane < K ? (int)((int64_t)(sg + 1) * nch / S) : 0;
+    const int len = b1 - b0;
+    int incl = len;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      const int64_t o = __shfl_up(incl, d, 64);
+      const int o = __shfl_up(incl, d, 64);
       if (lane >= d) incl += o;
     }
     seg_end = incl;
     seg_base = b0 - (incl - len);
   }
-  const int64_t Lx = __shfl(seg_end, K - 1, 64);
-  const int64_t q0 = wj * Lx / GPX, q1 = (wj + 1) * Lx / GPX;
-  const int64_t it0 = 0, it1 = (q1 - q0 + 3) / 4;
+  const int Lx = __builtin_amdgcn_readlane(seg_end, K - 1);
+  const int q0 = (int)((int64_t)wj * Lx / GPX), q1 = (int)((int64_t)(wj + 1) * Lx / GPX);
+  const int it1 = (q1 - q0 + 3) / 4;
   if (it1 == 0) return;                                // whole workgroup
-  auto chunk_of = [&](int64_t q) {                     // list position (< Lx) -> chunk index
+  auto chunk_of = [&](int q) {                         // list position (< Lx) -> chunk index
     const uint64_t m = __builtin_amdgcn_ballot_w64(lane < K && seg_end > q);
     const int k = m ? (int)__builtin_ctzll(m) : 0;
-    const int64_t base = ((int64_t)__builtin_amdgcn_readlane((int)(seg_base >> 32), k) << 32) |
-                         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)seg_base, k);
-    return q + base;
+    return q + __builtin_amdgcn_readlane(seg_base, k);
   };
   const int b = a.b_theta, C = 1 << b;
-  const int nq = a.num_kv * a.grp;
-  float* q_s = rag_smem;                               // [num_kv * grp][DH]
-  float* cb_s = rag_smem + nq * DH;                    // [G][C][GS] of the staged head
+  float* q_s = rag_smem;                               // [num_kv][SLOTS][QS]
+  float* cb_s = rag_smem + a.num_kv * SLOTS * QS;      // [G * C][CS] of the staged head
+  const uint32_t pb = (uint32_t)a.pages_bytes;         // < 2^31
   const rsrc_t rs = make_rsrc(a.pages, a.pages_bytes);
   const rsrc_t rt = make_rsrc(a.ptable, (int64_t)a.num_pages * 12);
   const rsrc_t rh = make_rsrc(a.head_ids, (int64_t)a.num_pages * 4);
   const rsrc_t rp = make_rsrc(a.positions, (int64_t)a.num_pages * a.page_size * 4);
   const rsrc_t rcb = make_rsrc(a.codebooks, (int64_t)a.num_kv * G * C * GS * 4);
-  const int64_t pb = a.pages_bytes > 0x7FFFFFFF ? 0x7FFFFFFF : a.pages_bytes;
-  const int tail4 = (int)(pb & ~(int64_t)3);
+  const uint32_t tail4 = pb & ~3u;
   uint32_t tailw = 0;
 #pragma unroll
   for (int i = 0; i < 3; ++i)
-    tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? tail4 + i : kOOB, 0, 0) << (8 * i);
-  for (int i = threadIdx.x; i < nq * DH / 4; i += 256)
-    reinterpret_cast<float4*>(q_s)[i] = reinterpret_cast<const float4*>(a.q)[i];
+    tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? (int)(tail4 + i) : kOOB, 0, 0)
+             << (8 * i);
+  // q of every head into LDS (rows of slots past grp are zeros; at most 32
+  // KB, 8 float4 per thread): every load issued before the first write
+  {
+    constexpr int R4 = DH / 4;
+    const int n4 = a.num_kv * SLOTS * R4;
+    const rsrc_t rq = make_rsrc(a.q, (int64_t)a.num_kv * a.grp * DH * 4);
+    float4 v[kStage4];
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + 256 * k, row = i / R4, h = row / SLOTS, sl = row % SLOTS;
+      const int src = (i < n4 && sl < a.grp) ? 16 * ((h * a.grp + sl) * R4 + i % R4) : kOOB;
+      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, src, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n4) *reinterpret_cast<float4*>(q_s + (i / R4) * QS + 4 * (i % R4)) = v[k];
+    }
+  }
   const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
+  // the fitted frequencies of the lane's pairs d0 .. d0 + NPL - 1; a fit of
+  // another model or shape makes every logit NaN
+  double fr[RM == kRopeExact ? NPL : 1];
+  float iv[RM == kRopeFp32 ? NPL : 1];
+  bool fit_ok = true;
+  if constexpr (RM != kRopeNone) {
+    fit_ok = a.rope->model == RM && a.rope->dh == DH && a.rope->max_pos == a.max_pos;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      if constexpr (RM == kRopeExact) fr[i] = a.rope->f[d0 + i];
+      else iv[i] = a.rope->inv32[d0 + i];
+    }
+  }
 
-  auto row_of = [&](int64_t it) {                      // issue round trip 1 of this wave's chunk of iteration it
+  auto row_of = [&](int it) {                          // issue round trip 1 of this wave's chunk of iteration it
     RagRow r;
-    const int64_t q = q0 + 4 * it + wave;
+    const int q = q0 + 4 * it + wave;
     const bool act = it < it1 && q < q1;
-    const int64_t ch = act ? chunk_of(q) : 0, ch0 = it < it1 ? chunk_of(q0 + 4 * it) : 0;
-    const int p = (int)(ch / cpp), c16 = (int)(ch % cpp);
-    const int p0 = (int)(ch0 / cpp);
+    const int ch = act ? chunk_of(q) : 0, ch0 = it < it1 ? chunk_of(q0 + 4 * it) : 0;
+    int p, c16, p0;
+    if (cpp_sh >= 0) {
+      p = ch >> cpp_sh;
+      c16 = ch & (cpp - 1);
+      p0 = ch0 >> cpp_sh;
+    } else {
+      p = (int)((uint32_t)ch / (uint32_t)cpp);
+      c16 = ch - p * cpp;
+      p0 = (int)((uint32_t)ch0 / (uint32_t)cpp);
+    }
     r.p = p;
     r.c16 = c16;
     // unconditional loads (absent ones read zeros): a branch around a load
@@ -1893,11 +1954,6 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     r.pos = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, act ? 4 * (p * a.page_size + 16 * c16 + t) : kOOB, 0, 0);
     return r;
   };
-  auto in_pool = [&](int64_t o) { return (o >= 0 && o < pb) ? (int)o : kOOB; };
-  auto dword_at = [&](int64_t o4) {
-    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
-    return w | (o4 == tail4 ? tailw : 0u);             // the partial dword itself reads as zero
-  };
   auto page_of = [&](const RagRow& r, int ts, float4 (&cc)[NM], float4 (&ss)[NM]) {   // issue round trip 2
     RagPage g;
     g.page_off = (int32_t)__builtin_amdgcn_readfirstlane(r.w0);
@@ -1908,65 +1964,74 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     g.pos = r.pos;
     g.p = r.p;
     g.c16 = r.c16;
-    const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
-    g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(page_off + 1), 0, 0);
+    const bool row_ok = (g.page_off | g.th_off | g.rad_off) >= 0;
+    const uint32_t po = g.page_off, tho = g.th_off, ro = g.rad_off;
+    auto in_pool = [&](uint32_t o) { return row_ok && o < pb ? (int)o : kOOB; };
+    auto dword_at = [&](uint32_t o4) {
+      const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
+      return w | (row_ok && o4 == tail4 ? tailw : 0u);  // the partial dword itself reads as zero
+    };
+    g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(po + 1), 0, 0);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int64_t cbit = th_off * 8 + (int64_t)(ts * G + (k ? gj : gi)) * b;
-      const int64_t o4 = (cbit >> 5) * 4;
+      const int gg = k ? gj : gi;
+      const uint32_t x = 8u * (tho & 3u) + (uint32_t)((ts * G + gg) * b);   // bit offset from tho & ~3
+      const uint32_t o4 = (tho & ~3u) + 4u * (x >> 5);
       g.cw[k][0] = dword_at(o4);
       g.cw[k][1] = dword_at(o4 + 4);
-      g.rc[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(rad_off + ts * G + (k ? gj : gi)), 0, 0);
-      const int64_t so = page_off + kHeaderBytes + 4 * (k ? gj : gi);
-      const int64_t s4 = so >= 0 ? (so >> 2) * 4 : -4;
+      g.rc[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(ro + (uint32_t)(ts * G + gg)), 0, 0);
+      const uint32_t s4 = (po + kHeaderBytes + 4 * gg) & ~3u;
       g.sw[k][0] = dword_at(s4);
       g.sw[k][1] = dword_at(s4 + 4);
     }
-    const int pos = (r.pos >= 0 && r.pos < a.max_pos) ? r.pos : 0;
-    const float* cs = a.cos_tbl + (int64_t)pos * DH + d0;
-    const float* sn = a.sin_tbl + (int64_t)pos * DH + d0;
+    if constexpr (RM == kRopeNone) {
+      const int pos = (r.pos >= 0 && r.pos < a.max_pos) ? r.pos : 0;
+      const float* cs = a.cos_tbl + (int64_t)pos * DH + d0;
+      const float* sn = a.sin_tbl + (int64_t)pos * DH + d0;
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      cc[m] = *reinterpret_cast<const float4*>(cs + 4 * m);
-      ss[m] = *reinterpret_cast<const float4*>(sn + 4 * m);
+      for (int m = 0; m < NM; ++m) {
+        cc[m] = *reinterpret_cast<const float4*>(cs + 4 * m);
+        ss[m] = *reinterpret_cast<const float4*>(sn + 4 * m);
+      }
     }
     return g;
   };
   const int64_t total_slots = (int64_t)a.num_pages * a.page_size;
   const float inv = 1.0f / __builtin_sqrtf((float)DH);
   int staged = -1;
-  auto compute = [&](auto cb_lds_f, int64_t it, const RagPage& g, const float4 (&cc)[NM], const float4 (&ss)[NM])
+  auto compute = [&](auto cb_lds_f, const RagPage& g, const float4 (&cc)[NM], const float4 (&ss)[NM])
                      __attribute__((always_inline)) {
     constexpr bool CB_LDS = decltype(cb_lds_f)::value;
     const int p = g.p, ts = 16 * g.c16 + t;
-    const int64_t page_off = g.page_off, th_off = g.th_off, rad_off = g.rad_off;
+    const bool row_ok = (g.page_off | g.th_off | g.rad_off) >= 0;
+    const uint32_t po = g.page_off, tho = g.th_off, ro = g.rad_off;
     const int hk = g.hk;
-    const bool hdr_ok = page_off >= 0 && page_off + 2 <= a.pages_bytes;
-    int n = hdr_ok ? min((int)g.cnt, a.page_size) : 0;
-    if (page_off + kHeaderBytes + 4 * G > a.pages_bytes || th_off < 0 || rad_off < 0 ||
-        th_off + ((int64_t)n * G * b + 7) / 8 > a.pages_bytes || rad_off + (int64_t)n * G > a.pages_bytes)
+    int n = row_ok && po + 2 <= pb ? min((int)g.cnt, a.page_size) : 0;
+    if (po + kHeaderBytes + 4 * G > pb || tho + (uint32_t)((n * G * b + 7) >> 3) > pb || ro + (uint32_t)(n * G) > pb)
       n = 0;
     const bool head_ok = hk >= 0 && hk < a.num_kv;
     const bool valid = ts < n && g.pos >= 0 && g.pos < a.max_pos && head_ok;
     const int hq = head_ok ? hk : 0;
+    const int ppos = (g.pos >= 0 && g.pos < a.max_pos) ? g.pos : 0;
     int code[2];
     float rad[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int64_t cbit = th_off * 8 + (int64_t)(ts * G + (k ? gj : gi)) * b;
-      code[k] = (int)(__builtin_amdgcn_alignbit(g.cw[k][1], g.cw[k][0], (uint32_t)(cbit & 31)) & (uint32_t)(C - 1));
-      const int64_t so = page_off + kHeaderBytes + 4 * (k ? gj : gi);
-      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_alignbyte(g.sw[k][1], g.sw[k][0], (uint32_t)(so & 3)));
+      const int gg = k ? gj : gi;
+      const uint32_t x = 8u * (tho & 3u) + (uint32_t)((ts * G + gg) * b);
+      code[k] = (int)(__builtin_amdgcn_alignbit(g.cw[k][1], g.cw[k][0], x & 31u) & (uint32_t)(C - 1));
+      const uint32_t so = po + kHeaderBytes + 4 * gg;
+      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_alignbyte(g.sw[k][1], g.sw[k][0], so & 3u));
       rad[k] = (float)g.rc[k] * sc * (1.0f / 127.0f);
     }
-    const int r1 = (gi * C + code[0]) * GS + off, r2 = (gj * C + code[1]) * GS + off;
+    // codebook rows of the two codes: padded rows in LDS, or the global table
+    const int r1 = (gi * C + code[0]) * (CB_LDS ? CS : GS) + off, r2 = (gj * C + code[1]) * (CB_LDS ? CS : GS) + off;
     const int hbase = hq * G * C * GS;                   // floats; the codebook stays below 2^29 floats
     floatx4 acc[NHS];
 #pragma unroll
     for (int hs = 0; hs < NHS; ++hs) acc[hs] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      // the staged head's rows from LDS, another head's with buffer loads
       float4 cv1, cv2;
       if constexpr (CB_LDS) {
         cv1 = *reinterpret_cast<const float4*>(cb_s + r1 + 4 * m);
@@ -1977,16 +2042,26 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
       }
       const float k1[4] = {rad[0] * cv1.x, rad[0] * cv1.y, rad[0] * cv1.z, rad[0] * cv1.w};
       const float k2[4] = {rad[1] * cv2.x, rad[1] * cv2.y, rad[1] * cv2.z, rad[1] * cv2.w};
-      const float co[4] = {cc[m].x, cc[m].y, cc[m].z, cc[m].w}, si[4] = {ss[m].x, ss[m].y, ss[m].z, ss[m].w};
-      float4 q0[NHS], q1[NHS];
+      float co[4], si[4];
+      if constexpr (RM == kRopeNone) {
+        co[0] = cc[m].x; co[1] = cc[m].y; co[2] = cc[m].z; co[3] = cc[m].w;
+        si[0] = ss[m].x; si[1] = ss[m].y; si[2] = ss[m].z; si[3] = ss[m].w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double x = RM == kRopeExact ? (double)ppos * fr[4 * m + e]
+                                            : (double)((float)ppos * iv[4 * m + e]) * kInvTwoPi;
+          const float2 z = turn_phasor(x);
+          co[e] = z.x;
+          si[e] = z.y;
+        }
+      }
+      float4 q0v[NHS], q1v[NHS];
 #pragma unroll
       for (int hs = 0; hs < NHS; ++hs) {
-        const int slot = 4 * hs + (t & 3);
-        const bool q_ok = slot < a.grp;
-        const int qo = (hq * a.grp + (q_ok ? slot : 0)) * DH + d0 + 4 * m;
-        q0[hs] = *reinterpret_cast<const float4*>(q_s + qo);
-        q1[hs] = *reinterpret_cast<const float4*>(q_s + qo + DH / 2);
-        if (!q_ok) { q0[hs] = float4{0.f, 0.f, 0.f, 0.f}; q1[hs] = q0[hs]; }
+        const int qo = (hq * SLOTS + 4 * hs + (t & 3)) * QS + d0 + 4 * m;
+        q0v[hs] = *reinterpret_cast<const float4*>(q_s + qo);
+        q1v[hs] = *reinterpret_cast<const float4*>(q_s + qo + DH / 2);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -1994,8 +2069,8 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
         const float x1 = k2[e] * co[e] + k1[e] * si[e];
 #pragma unroll
         for (int hs = 0; hs < NHS; ++hs) {
-          const float qa = e == 0 ? q0[hs].x : e == 1 ? q0[hs].y : e == 2 ? q0[hs].z : q0[hs].w;
-          const float qb = e == 0 ? q1[hs].x : e == 1 ? q1[hs].y : e == 2 ? q1[hs].z : q1[hs].w;
+          const float qa = e == 0 ? q0v[hs].x : e == 1 ? q0v[hs].y : e == 2 ? q0v[hs].z : q0v[hs].w;
+          const float qb = e == 0 ? q1v[hs].x : e == 1 ? q1v[hs].y : e == 2 ? q1v[hs].z : q1v[hs].w;
           acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa, x0, acc[hs], 0, 0, 0);
           acc[hs] = __builtin_amdgcn_mfma_f32_4x4x1f32(qb, x1, acc[hs], 0, 0, 0);
         }
@@ -2011,16 +2086,29 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
       const float v = x + y;
       const int i = 4 * hs + u;
       if (i < a.grp)
-        a.logits_out[(int64_t)i * total_slots + (int64_t)p * a.page_size + ts] = valid ? v * inv : -INFINITY;
+        a.logits_out[(int64_t)i * total_slots + p * a.page_size + ts] =
+            !fit_ok ? __builtin_nanf("") : valid ? v * inv : -INFINITY;
     }
   };
   // the codebook of head hb into LDS when it is not the staged one (a
   // workgroup-uniform decision: hb is the head of the iteration's first chunk)
   auto stage = [&](int hb) {
     if (hb == staged || hb < 0 || hb >= a.num_kv || C > 64) return;
+    // at most 32 KB: every load issued before the barrier and the writes
+    constexpr int R4 = GS / 4;
+    const int n4 = G * C * R4, base = hb * n4;
+    float4 v[kStage4];
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, i < n4 ? 16 * (base + i) : kOOB, 0, 0));
+    }
     __syncthreads();                                   // every wave is done with the previous codebook
-    const float4* src = reinterpret_cast<const float4*>(a.codebooks + (int64_t)hb * G * C * GS);
-    for (int i = threadIdx.x; i < G * C * GS / 4; i += 256) reinterpret_cast<float4*>(cb_s)[i] = src[i];
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n4) *reinterpret_cast<float4*>(cb_s + (i / R4) * CS + 4 * (i % R4)) = v[k];
+    }
     __syncthreads();
     staged = hb;
   };
@@ -2028,47 +2116,76 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   // pipeline: rows two iterations ahead, page bytes and tables one ahead;
   // rows and pages each in two register sets used alternately (the loop is
   // unrolled by two, so no register a load is still filling is copied)
-  RagRow ra = row_of(it0), rb = row_of(it0 + 1);
+  RagRow ra = row_of(0), rb = row_of(1);
   float4 cca[NM], ssa[NM], ccb[NM], ssb[NM];
   RagPage ga = page_of(ra, 16 * ra.c16 + t, cca, ssa), gb;
   __syncthreads();                                     // q staged
-  for (int64_t it = it0; it < it1; it += 2) {
+  for (int it = 0; it < it1; it += 2) {
     gb = page_of(rb, 16 * rb.c16 + t, ccb, ssb);       // waits for rows it + 1 (and so for pages it)
     ra = row_of(it + 2);
     stage(ga.hb);
     if (q0 + 4 * it + wave < q1) {
-      if (ga.hk == staged) compute(Flag<true>(), it, ga, cca, ssa);
-      else compute(Flag<false>(), it, ga, cca, ssa);
+      if (ga.hk == staged) compute(Flag<true>(), ga, cca, ssa);
+      else compute(Flag<false>(), ga, cca, ssa);
     }
     if (it + 1 >= it1) break;
     ga = page_of(ra, 16 * ra.c16 + t, cca, ssa);
     rb = row_of(it + 3);
     stage(gb.hb);
     if (q0 + 4 * (it + 1) + wave < q1) {
-      if (gb.hk == staged) compute(Flag<true>(), it + 1, gb, ccb, ssb);
-      else compute(Flag<false>(), it + 1, gb, ccb, ssb);
+      if (gb.hk == staged) compute(Flag<true>(), gb, ccb, ssb);
+      else compute(Flag<false>(), gb, ccb, ssb);
     }
   }
 }
 
+// LDS bytes of ragged_pipe_kernel: padded q rows of every head (4 or 8 slots
+// per head) and the padded codebook of one head.
+inline int64_t ragged_pipe_lds(const RaggedLaunch& L) {
+  const int64_t slots = L.grp > 4 ? 8 : 4;
+  return 4 * (L.num_kv * slots * (L.dh + 4) + (int64_t)(L.dh / L.group_size) * (1 << L.b_theta) * (L.group_size + 4));
+}
+
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
   if (L.num_pages <= 0) return 0;
+  // the fast forms take 32-bit offsets: byte pools below 2 GiB, slots below 2^29
   const bool fast = L.page_size % 16 == 0 && (L.group_size == 16 || L.group_size == 32) && L.grp <= 8 &&
-                    L.groups * L.group_size == L.dh;
-  const int64_t q_bytes = (int64_t)L.num_kv * L.grp * L.dh * 4;
+                    L.groups * L.group_size == L.dh && L.pages_bytes <= 0x7FFFFFFFLL &&
+                    (int64_t)L.num_pages * L.page_size * 4 <= 0x7FFFFF00LL;
+  const int64_t q_stage = (int64_t)L.num_kv * (L.grp > 4 ? 8 : 4) * L.dh * 4;
   const int64_t cb_bytes = (int64_t)L.dh * (1 << L.b_theta) * 4;
-  if (fast && L.b_theta <= 6 && q_bytes <= 32768 && cb_bytes <= 32768 &&
-      (int64_t)L.num_pages * L.page_size * 4 <= 0x7FFFFF00LL) {
+  if (fast && L.b_theta <= 6 && q_stage <= 32768 && cb_bytes <= 32768 && ragged_pipe_lds(L) <= 65536) {
     const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
     const int64_t iters = (chunks + 3) / 4;
-    const dim3 grid((unsigned)(iters < 512 ? iters : 512));
-    const size_t lds = (size_t)(q_bytes + cb_bytes);
+    const size_t lds = (size_t)ragged_pipe_lds(L);
+    const int rm = L.rope ? L.rope_model : kRopeNone;
+    // one resident round of workgroups: as many per CU as registers and LDS
+    // allow (2 or 3), 256 CUs
+    auto launch = [&](const void* fn, void (*k)(RaggedLaunch)) {
+      struct Occ { const void* fn; size_t lds; int per_cu; };
+      thread_local Occ cache[8] = {};
+      thread_local int next = 0;
+      int per_cu = 0;
+      for (const Occ& o : cache)
+        if (o.fn == fn && o.lds == lds) per_cu = o.per_cu;
+      if (per_cu == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) per_cu = 2;
+        per_cu = per_cu < 1 ? 1 : per_cu > 3 ? 3 : per_cu;
+        cache[next] = Occ{fn, lds, per_cu};
+        next = (next + 1) % 8;
+      }
+      const int64_t cap = 256LL * per_cu;
+      hipLaunchKernelGGL(k, dim3((unsigned)(iters < cap ? iters : cap)), dim3(256), lds, stream, L);
+    };
+#define SPHKV_RAGGED_RM(D, S, N, R) \
+    if (L.dh == D && L.group_size == S && (L.grp > 4) == (N == 2) && rm == R) \
+      launch(reinterpret_cast<const void*>(&ragged_pipe_kernel<D, S, N, R>), &ragged_pipe_kernel<D, S, N, R>);
 #define SPHKV_RAGGED(D, S, N) \
-    if (L.dh == D && L.group_size == S && (L.grp > 4) == (N == 2)) \
-      hipLaunchKernelGGL((ragged_pipe_kernel<D, S, N>), grid, dim3(256), lds, stream, L);
+    SPHKV_RAGGED_RM(D, S, N, kRopeNone) SPHKV_RAGGED_RM(D, S, N, kRopeExact) SPHKV_RAGGED_RM(D, S, N, kRopeFp32)
     SPHKV_RAGGED(128, 16, 1) SPHKV_RAGGED(128, 16, 2) SPHKV_RAGGED(128, 32, 1) SPHKV_RAGGED(128, 32, 2)
     SPHKV_RAGGED(64, 16, 1) SPHKV_RAGGED(64, 16, 2) SPHKV_RAGGED(64, 32, 1) SPHKV_RAGGED(64, 32, 2)
 #undef SPHKV_RAGGED
+#undef SPHKV_RAGGED_RM
   } else if (fast) {
     const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
     const dim3 grid((unsigned)((chunks + 3) / 4));
@@ -2084,6 +2201,57 @@ int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
     else
       hipLaunchKernelGGL(ragged_logits_kernel<64>, dim3((L.num_pages + 3) / 4), dim3(256), 0, stream, L);
   }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Every entry of HF-layout cos / sin tables [max_pos, dh] against both
+// models of fit (its f and inv32 set): the largest deviation of each model
+// over the first-half entries (evaluated with fp64 sine / cosine), and the
+// entries whose second half is not a copy of the first.  Results are added
+// to fit's counters with vector atomics, one per wave.
+__global__ __launch_bounds__(256) void rope_check_kernel(const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                                         int dh, RopeFit* fit) {
+  const int half = dh / 2;
+  const int64_t total = (int64_t)max_pos * half;
+  double da = 0.0, db = 0.0;
+  int mism = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int p = (int)(i / half), j = (int)(i % half);
+    const float* cr = cos_tbl + (int64_t)p * dh;
+    const float* sr = sin_tbl + (int64_t)p * dh;
+    const float c0 = cr[j], c1 = cr[j + half], s0 = sr[j], s1 = sr[j + half];
+    mism += (__float_as_uint(c0) != __float_as_uint(c1)) || (__float_as_uint(s0) != __float_as_uint(s1));
+    double t = (double)p * fit->f[j];
+    t -= floor(t);
+    double sa, ca, sb, cb;
+    sincospi(2.0 * t, &sa, &ca);
+    const float a32 = (float)p * fit->inv32[j];
+    sincos((double)a32, &sb, &cb);
+    const double ea = fmax(fabs((double)c0 - ca), fabs((double)s0 - sa));
+    const double eb = fmax(fabs((double)c0 - cb), fabs((double)s0 - sb));
+    da = ea <= da ? da : ea;        // NaN entries make the deviation NaN (kept: not <=)
+    db = eb <= db ? db : eb;
+  }
+  float fa = da <= 1e30 ? (float)da : INFINITY, fb = db <= 1e30 ? (float)db : INFINITY;
+  for (int m = 32; m >= 1; m >>= 1) {
+    fa = fmaxf(fa, shfl_xor(fa, m));
+    fb = fmaxf(fb, shfl_xor(fb, m));
+    mism += __shfl_xor(mism, m, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&fit->dev_bits[0], __float_as_uint(fa));
+    atomicMax(&fit->dev_bits[1], __float_as_uint(fb));
+    if (mism) atomicAdd(&fit->half_mismatch, mism);
+  }
+}
+
+int launch_rope_check(const float* cos_tbl, const float* sin_tbl, int32_t max_pos, int32_t dh, RopeFit* fit,
+                      hipStream_t stream) {
+  const int64_t total = (int64_t)max_pos * (dh / 2);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0)
+    hipLaunchKernelGGL(rope_check_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream,
+                       cos_tbl, sin_tbl, max_pos, dh, fit);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -53,12 +53,33 @@ struct TailLaunch {
   int32_t parity;            // which copy of the tail counts this step reads
 };
 
+// A RoPE fitted to a caller's HF-layout cos / sin tables [max_pos, dh]
+// (sphkv_rope_table_fit), in device memory.  Pair j (dims j, j + dh/2) turns
+// by either model:
+//   kRopeExact  cos / sin of the exact angle 2 pi pos f[j]  (f in turns per token)
+//   kRopeFp32   cos / sin of the fp32 angle fl32(pos * inv32[j])  (the HF
+//               construction: fp32 inv_freq times the fp32 position)
+// model is the one every table entry follows within kRopeFitTol (kRopeNone:
+// neither; the tables are read as given).
+constexpr int kRopeNone = 0, kRopeExact = 1, kRopeFp32 = 2;
+constexpr float kRopeFitTol = 0x1p-20f;
+struct RopeFit {
+  int32_t model, dh, max_pos, half_mismatch;   // half_mismatch: entries whose second half differs from the first
+  uint32_t dev_bits[2];                        // max |table - model| of kRopeExact, kRopeFp32 (fp32 bits)
+  int32_t pad[2];
+  double f[64];
+  float inv32[64];
+};
+static_assert(sizeof(RopeFit) <= 1024, "SPHKV_ROPE_FIT_BYTES");
+
 struct RaggedLaunch {
   const uint8_t* pages; int64_t pages_bytes; const int32_t* ptable; const int32_t* head_ids;
   const int32_t* positions; int32_t num_pages; const float* cos_tbl; const float* sin_tbl;
   int32_t max_pos; const float* q; int32_t grp; int32_t num_kv; const float* codebooks;
   int32_t dh; int32_t groups; int32_t group_size; int32_t b_theta; int32_t page_size;
   float* logits_out;
+  const RopeFit* rope;       // NULL, or the tables' fit (phases formed in the kernel)
+  int32_t rope_model;        // kRopeNone when rope is NULL
 };
 
 // Mode-A (LayerPool) path
@@ -154,6 +175,10 @@ int launch_tail_relayout(const int32_t* row_start, int32_t num_sh, int32_t num_r
                          int32_t dec_vpage0, int32_t dh, int32_t* ptable_d, int32_t* vslot_d,
                          int32_t* positions_d, hipStream_t stream);
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream);
+// check every table entry against both models of *fit (f / inv32 set); adds
+// to fit's half_mismatch and dev_bits (which start at zero)
+int launch_rope_check(const float* cos_tbl, const float* sin_tbl, int32_t max_pos, int32_t dh, RopeFit* fit,
+                      hipStream_t stream);
 
 // fp32 elements of one work item's partial: 16 (m, l, padding) + gqa * dh
 inline int64_t partial_floats(int gqa, int dh) { return 16 + (int64_t)gqa * dh; }

@@ -15,7 +15,9 @@ contiguous tensors of the reference's dtype.
 """
 from __future__ import annotations
 
+import ctypes
 import math
+import weakref
 
 import torch
 
@@ -37,6 +39,62 @@ def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
     return t.contiguous()
 
 
+ROPE_FIT_BYTES = 1024            # SPHKV_ROPE_FIT_BYTES
+# Fitted RoPE tables (sphkv_rope_table_fit), one entry per (cos, sin) tensor
+# pair, valid while both tensors are alive at the same storage and version
+# (torch bumps a tensor's version on every in-place change through it or its
+# views; a write that bypasses torch, such as a raw kernel, is not seen).
+_FITS: dict = {}
+_FIT_LIMIT = 16
+use_rope_fit = True             # False: every call reads the tables' rows
+fit_calls = 0                   # table fits run so far
+
+
+class _RopeFit:
+    __slots__ = ("cos", "sin", "sig", "buf", "model", "dev")
+
+
+def _fit_signature(cos_src, sin_src, dh):
+    return (cos_src._version, sin_src._version, cos_src.data_ptr(), sin_src.data_ptr(), tuple(cos_src.shape),
+            cos_src.dtype, sin_src.dtype, cos_src.device, int(dh))
+
+
+def _rope_fit(cos_src, sin_src, cos32, sin32, dh) -> _RopeFit:
+    """The fit of the caller's tables, from the cache or fitted now (one
+    device pass over the tables and a wait)."""
+    global fit_calls
+    key = (id(cos_src), id(sin_src))
+    sig = _fit_signature(cos_src, sin_src, dh)
+    e = _FITS.get(key)
+    if e is not None and e.cos() is cos_src and e.sin() is sin_src and e.sig == sig:
+        return e
+    buf = torch.empty(ROPE_FIT_BYTES, dtype=torch.uint8, device=cos32.device)
+    model = ctypes.c_int32(0)
+    dev = (ctypes.c_float * 2)()
+    rc = _lib.sphkv_rope_table_fit(cos32.data_ptr(), sin32.data_ptr(), int(cos32.shape[0]), int(dh),
+                                   buf.data_ptr(), ctypes.byref(model), dev, _stream())
+    check(rc, "sphkv_rope_table_fit")
+    fit_calls += 1
+    e = _RopeFit()
+    e.cos, e.sin, e.sig, e.buf, e.model, e.dev = (weakref.ref(cos_src), weakref.ref(sin_src), sig, buf,
+                                                  int(model.value), (float(dev[0]), float(dev[1])))
+    for k in [k for k, v in _FITS.items() if v.cos() is None or v.sin() is None]:
+        del _FITS[k]
+    while len(_FITS) >= _FIT_LIMIT:
+        del _FITS[next(iter(_FITS))]
+    _FITS[key] = e
+    return e
+
+
+def rope_fit_info(cos_tbl, sin_tbl):
+    """(model, deviation of the exact-angle model, deviation of the fp32-angle
+    model) of the tables' fit: model 0 = the tables are read as given, 1 =
+    exact angles, 2 = fp32 angles (the HF construction)."""
+    c, s = _dev(cos_tbl, "cos_tbl", torch.float32), _dev(sin_tbl, "sin_tbl", torch.float32)
+    e = _rope_fit(cos_tbl, sin_tbl, c, s, int(c.shape[1]))
+    return e.model, e.dev[0], e.dev[1]
+
+
 def fused_decode_ragged(pages, ptable, head_ids, positions, cos_tbl, sin_tbl, q, grp, num_kv,
                         codebooks, dh, groups, group_size, b_theta, page_size):
     """Logits of every (q head, page slot) of one tier's packed pages.
@@ -48,7 +106,14 @@ def fused_decode_ragged(pages, ptable, head_ids, positions, cos_tbl, sin_tbl, q,
     Returns fp32 [grp, P * page_size]: row i, slot p*page_size+s is q head
     head_ids[p]*grp + i against slot s of page p, scaled by 1/sqrt(dh);
     pad slots are -inf.
+
+    The first call with a (cos, sin) pair fits them to a RoPE rotation and
+    checks every entry (sphkv_rope_table_fit); while they stay unchanged,
+    later calls form the phases in the kernel from the fit (each entry is
+    within 2^-20 of it) instead of reading a table row per token.  Tables
+    that fit neither model are read as given.
     """
+    cos_src, sin_src = cos_tbl, sin_tbl
     pages = _dev(pages, "pages", torch.uint8)
     ptable = _dev(ptable, "ptable", torch.int32)
     head_ids = _dev(head_ids, "head_ids", torch.int32)
@@ -70,11 +135,16 @@ def fused_decode_ragged(pages, ptable, head_ids, positions, cos_tbl, sin_tbl, q,
     if tuple(codebooks.shape) != (num_kv * groups, C, group_size):
         raise ValueError(f"codebooks must be [{num_kv * groups}, {C}, {group_size}]")
     out = torch.empty((int(grp), P * int(page_size)), dtype=torch.float32, device=pages.device)
-    rc = _lib.sphkv_fused_decode_ragged(
+    fit_ptr, model = None, 0
+    if use_rope_fit and P > 0:
+        fit = _rope_fit(cos_src, sin_src, cos_tbl, sin_tbl, dh)
+        if fit.model:
+            fit_ptr, model = fit.buf.data_ptr(), fit.model
+    rc = _lib.sphkv_fused_decode_ragged_fitted(
         pages.data_ptr(), pages.numel(), ptable.data_ptr(), head_ids.data_ptr(), positions.data_ptr(), P,
         cos_tbl.data_ptr(), sin_tbl.data_ptr(), cos_tbl.shape[0], q.data_ptr(), int(grp), int(num_kv),
         codebooks.data_ptr(), int(dh), int(groups), int(group_size), int(b_theta), int(page_size),
-        out.data_ptr(), _stream())
+        fit_ptr, model, out.data_ptr(), _stream())
     check(rc, "fused_decode_ragged")
     return out
 

@@ -53,6 +53,9 @@ SIGNATURES = {
                                            P, P, P, P, P, I64, I32, I32, I32, I32, I32, P]),
     "sphkv_fused_decode_ragged": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
                                                  I32, I32, I32, I32, I32, P, P]),
+    "sphkv_fused_decode_ragged_fitted": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
+                                                        I32, I32, I32, I32, I32, P, I32, P, P]),
+    "sphkv_rope_table_fit": (ctypes.c_int, [P, P, I32, I32, P, P, P, P]),
     "sphkv_encode_append": (ctypes.c_int, [P, P, P, P, P, P, P, P, I32, I64, I32, I32, I32, I32, I32,
                                            I32, I32, I32, P]),
     "sphkv_decode_modea": (ctypes.c_int, [P, P, P, P, P, P, P, P, I64, P, P, P, P, P, I32, I32, I32, I32,

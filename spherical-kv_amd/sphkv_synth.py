@@ -115,6 +115,18 @@ class Workload:
         return out.astype(np.int64)
 
 
+def hf_rope_tables(max_pos: int, dh: int, theta: float, device):
+    """cos / sin tables [max_pos, dh] fp32 as a default-RoPE transformers
+    rotary embedding builds them for spherical_kv_pipeline.py:1597-1608:
+    inv_freq = 1 / theta ** (arange(0, dh, 2) / dh) in fp32 (torch's pow),
+    angles fl32(inv_freq * pos), the halves concatenated, cos / sin in fp32."""
+    import torch
+    inv = 1.0 / (theta ** (torch.arange(0, dh, 2, dtype=torch.int64, device=device).float() / dh))
+    ang = torch.arange(max_pos, device=device, dtype=torch.float32)[:, None] * inv.float()[None, :]
+    ang = torch.cat([ang, ang], dim=1)
+    return ang.cos().contiguous(), ang.sin().contiguous()
+
+
 def make_codebooks(rng, num_kv: int, dh: int, tier_ids) -> Dict[int, np.ndarray]:
     cbs = {}
     for tid in tier_ids:

@@ -143,6 +143,30 @@ def test_ragged_argument_errors():
     args[16] = 9                                   # b_theta
     assert lib.sphkv_fused_decode_ragged(*args) == -1
     assert "b_theta" in lib.sphkv_last_error().decode()
+    # the fitted entry: same checks, and the rope model with its fit
+    args[16] = 6
+    fa = args[:18] + [None, 3] + args[18:]
+    assert lib.sphkv_fused_decode_ragged_fitted(*fa) == -1
+    assert "rope_model must be 0, 1 or 2" in lib.sphkv_last_error().decode()
+    fa[19] = 1                                     # model 1 without a fit
+    assert lib.sphkv_fused_decode_ragged_fitted(*fa) == -1
+    assert "rope_model" in lib.sphkv_last_error().decode()
+    fa[19] = 0
+    assert lib.sphkv_fused_decode_ragged_fitted(*fa) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+
+
+def test_rope_table_fit_argument_errors():
+    import ctypes
+    lib = sphkv_lib.load()
+    m = ctypes.c_int32(7)
+    assert lib.sphkv_rope_table_fit(None, None, 100, 96, None, ctypes.byref(m), None, None) == -1
+    assert "dh must be 64 or 128" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_rope_table_fit(None, None, 0, 128, None, ctypes.byref(m), None, None) == -1
+    assert "max_pos" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_rope_table_fit(None, None, 100, 128, None, ctypes.byref(m), None, None) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    assert m.value == 7                            # untouched on error
 
 
 def _modea_args(**kw):
