@@ -1809,7 +1809,8 @@ __global__ __launch_bounds__(256) void ragged_fast_kernel(RaggedLaunch a) {
 // checked once per table by sphkv_rope_table_fit): the lane's pairs j turn by
 // 2 pi pos f[j] (exact angle) or by the fp32 angle fl32(pos * inv32[j])
 // reduced in fp64, on the hardware sine / cosine (turns).
-constexpr int kStage4 = 8;   // float4 per thread of a 32 KB LDS stage (256 threads)
+constexpr int kRagWaves = 4, kRagThreads = 64 * kRagWaves;     // waves of a pipelined-kernel workgroup
+constexpr int kStage4 = (2048 + kRagThreads - 1) / kRagThreads;  // float4 per thread of a 32 KB LDS stage
 struct RagRow {          // round trip 1 of one chunk
   uint32_t w0, w1, w2;   // pointer-table row (page_off, th_off, rad_off)
   int hk, hb, pos;       // head of the chunk's page, head of the iteration's first chunk, slot position
@@ -1820,21 +1821,26 @@ struct RagPage {         // round trip 2 of one chunk, with its row's fields
   int rc[2];
   int page_off, th_off, rad_off, hk, hb, pos, p, c16;
 };
-// LDS rows of the pipelined kernel are padded by 4 floats, so that the 16
-// codebook rows (random codes) or the 4 q heads one read touches start in
-// different banks
-template <int GS> __host__ __device__ constexpr int rag_cb_stride() { return GS + 4; }
+// LDS of the pipelined kernel: the staged head's q rows (padded by 4 floats,
+// so that the 4 rows one read touches start in different banks) and its
+// codebook, whose float4 slots are XOR-swizzled by the row (a read of 16
+// random codes then spreads over 16 bank groups instead of 4).
 template <int DH> __host__ __device__ constexpr int rag_q_stride() { return DH + 4; }
+template <int GS>
+__device__ __forceinline__ int rag_cb_index(int row, int slot4) {   // float index of float4 slot4 of a row
+  constexpr int R4 = GS / 4, SH = R4 == 4 ? 2 : 1;                  // 16 bank groups of 64 banks
+  return row * GS + 4 * (slot4 ^ ((row >> SH) & (R4 - 1)));
+}
 
 // Offsets are 32-bit: the launcher takes this kernel only for byte pools
 // below 2 GiB and fewer than 2^31 slots; a pointer-table row with a negative
 // offset reads nothing and contributes no token.
 template <int DH, int GS, int NHS, int RM>
-__global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
+__global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a) {
   constexpr int NPL = DH / 8, NM = NPL / 4;
   constexpr int G = DH / GS;
-  constexpr int QS = rag_q_stride<DH>(), CS = rag_cb_stride<GS>();
-  constexpr int SLOTS = 4 * NHS;                       // q rows per head in LDS (zeros past grp)
+  constexpr int QS = rag_q_stride<DH>();
+  constexpr int SLOTS = 4 * NHS;                       // q rows of a head in LDS (zeros past grp)
   extern __shared__ float rag_smem[];
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int t = lane & 15, u = lane >> 4;
@@ -1857,13 +1863,15 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   const int S = NX * K, xcd = blockIdx.x % NX, GPX = gridDim.x / NX, wj = blockIdx.x / NX;
   int seg_end = 0, seg_base = 0;                       // lane k < K: list end and chunk - list offset of segment k
   {
-    const int sg = xcd + NX * lane;
-    const int b0 = lane < K ? (int)((int64_t)sg * nch / S) : 0;
-    const int b1 = lane < K ? (int)((int64_t)(sg + 1) * nch / S) : 0;
+    // 32-bit products: sg < 64 and nch < 2^25
+    const uint32_t sg = xcd + NX * lane;
+    const int b0 = lane < K ? (int)(sg * (uint32_t)nch / (uint32_t)S) : 0;
+    const int b1 = lane < K ? (int)((sg + 1) * (uint32_t)nch / (uint32_t)S) : 0;
     const int len = b1 - b0;
     int incl = len;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
+    for (int d = 1; d < 8; d <<= 1) {                  // K <= 8 lanes
+
       const int o = __shfl_up(incl, d, 64);
       if (lane >= d) incl += o;
     }
@@ -1871,8 +1879,9 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     seg_base = b0 - (incl - len);
   }
   const int Lx = __builtin_amdgcn_readlane(seg_end, K - 1);
-  const int q0 = (int)((int64_t)wj * Lx / GPX), q1 = (int)((int64_t)(wj + 1) * Lx / GPX);
-  const int it1 = (q1 - q0 + 3) / 4;
+  const int q0 = (int)((uint32_t)wj * (uint32_t)Lx / (uint32_t)GPX);      // wj < 128, Lx < 2^25
+  const int q1 = (int)((uint32_t)(wj + 1) * (uint32_t)Lx / (uint32_t)GPX);
+  const int it1 = (q1 - q0 + kRagWaves - 1) / kRagWaves;
   if (it1 == 0) return;                                // whole workgroup
   auto chunk_of = [&](int q) {                         // list position (< Lx) -> chunk index
     const uint64_t m = __builtin_amdgcn_ballot_w64(lane < K && seg_end > q);
@@ -1880,8 +1889,8 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     return q + __builtin_amdgcn_readlane(seg_base, k);
   };
   const int b = a.b_theta, C = 1 << b;
-  float* q_s = rag_smem;                               // [num_kv][SLOTS][QS]
-  float* cb_s = rag_smem + a.num_kv * SLOTS * QS;      // [G * C][CS] of the staged head
+  float* q_s = rag_smem;                               // [SLOTS][QS] of the staged head
+  float* cb_s = rag_smem + SLOTS * QS;                 // [G * C][GS] (swizzled) of the staged head
   const uint32_t pb = (uint32_t)a.pages_bytes;         // < 2^31
   const rsrc_t rs = make_rsrc(a.pages, a.pages_bytes);
   const rsrc_t rt = make_rsrc(a.ptable, (int64_t)a.num_pages * 12);
@@ -1894,25 +1903,7 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   for (int i = 0; i < 3; ++i)
     tailw |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, tail4 + i < pb ? (int)(tail4 + i) : kOOB, 0, 0)
              << (8 * i);
-  // q of every head into LDS (rows of slots past grp are zeros; at most 32
-  // KB, 8 float4 per thread): every load issued before the first write
-  {
-    constexpr int R4 = DH / 4;
-    const int n4 = a.num_kv * SLOTS * R4;
-    const rsrc_t rq = make_rsrc(a.q, (int64_t)a.num_kv * a.grp * DH * 4);
-    float4 v[kStage4];
-#pragma unroll
-    for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + 256 * k, row = i / R4, h = row / SLOTS, sl = row % SLOTS;
-      const int src = (i < n4 && sl < a.grp) ? 16 * ((h * a.grp + sl) * R4 + i % R4) : kOOB;
-      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, src, 0, 0));
-    }
-#pragma unroll
-    for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n4) *reinterpret_cast<float4*>(q_s + (i / R4) * QS + 4 * (i % R4)) = v[k];
-    }
-  }
+  const rsrc_t rq = make_rsrc(a.q, (int64_t)a.num_kv * a.grp * DH * 4);
   const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
   // the fitted frequencies of the lane's pairs d0 .. d0 + NPL - 1; a fit of
   // another model or shape makes every logit NaN
@@ -1930,9 +1921,9 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
 
   auto row_of = [&](int it) {                          // issue round trip 1 of this wave's chunk of iteration it
     RagRow r;
-    const int q = q0 + 4 * it + wave;
+    const int q = q0 + kRagWaves * it + wave;
     const bool act = it < it1 && q < q1;
-    const int ch = act ? chunk_of(q) : 0, ch0 = it < it1 ? chunk_of(q0 + 4 * it) : 0;
+    const int ch = act ? chunk_of(q) : 0, ch0 = it < it1 ? chunk_of(q0 + kRagWaves * it) : 0;
     int p, c16, p0;
     if (cpp_sh >= 0) {
       p = ch >> cpp_sh;
@@ -2024,8 +2015,8 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
       const float sc = __builtin_bit_cast(float, __builtin_amdgcn_alignbyte(g.sw[k][1], g.sw[k][0], so & 3u));
       rad[k] = (float)g.rc[k] * sc * (1.0f / 127.0f);
     }
-    // codebook rows of the two codes: padded rows in LDS, or the global table
-    const int r1 = (gi * C + code[0]) * (CB_LDS ? CS : GS) + off, r2 = (gj * C + code[1]) * (CB_LDS ? CS : GS) + off;
+    // codebook rows of the two codes: swizzled rows in LDS, or the global table
+    const int r1 = gi * C + code[0], r2 = gj * C + code[1];
     const int hbase = hq * G * C * GS;                   // floats; the codebook stays below 2^29 floats
     floatx4 acc[NHS];
 #pragma unroll
@@ -2034,11 +2025,13 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     for (int m = 0; m < NM; ++m) {
       float4 cv1, cv2;
       if constexpr (CB_LDS) {
-        cv1 = *reinterpret_cast<const float4*>(cb_s + r1 + 4 * m);
-        cv2 = *reinterpret_cast<const float4*>(cb_s + r2 + 4 * m);
+        cv1 = *reinterpret_cast<const float4*>(cb_s + rag_cb_index<GS>(r1, off / 4 + m));
+        cv2 = *reinterpret_cast<const float4*>(cb_s + rag_cb_index<GS>(r2, off / 4 + m));
       } else {
-        cv1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r1 + 4 * m), 0, 0));
-        cv2 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r2 + 4 * m), 0, 0));
+        cv1 = __builtin_bit_cast(float4,
+                                 __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r1 * GS + off + 4 * m), 0, 0));
+        cv2 = __builtin_bit_cast(float4,
+                                 __builtin_amdgcn_raw_buffer_load_b128(rcb, 4 * (hbase + r2 * GS + off + 4 * m), 0, 0));
       }
       const float k1[4] = {rad[0] * cv1.x, rad[0] * cv1.y, rad[0] * cv1.z, rad[0] * cv1.w};
       const float k2[4] = {rad[1] * cv2.x, rad[1] * cv2.y, rad[1] * cv2.z, rad[1] * cv2.w};
@@ -2056,12 +2049,21 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
           si[e] = z.y;
         }
       }
+      // q of the lane's head slot: the staged head's rows in LDS, another
+      // head's from the global q (slots past grp read zeros)
       float4 q0v[NHS], q1v[NHS];
 #pragma unroll
       for (int hs = 0; hs < NHS; ++hs) {
-        const int qo = (hq * SLOTS + 4 * hs + (t & 3)) * QS + d0 + 4 * m;
-        q0v[hs] = *reinterpret_cast<const float4*>(q_s + qo);
-        q1v[hs] = *reinterpret_cast<const float4*>(q_s + qo + DH / 2);
+        const int slot = 4 * hs + (t & 3);
+        if constexpr (CB_LDS) {
+          const int qo = slot * QS + d0 + 4 * m;
+          q0v[hs] = *reinterpret_cast<const float4*>(q_s + qo);
+          q1v[hs] = *reinterpret_cast<const float4*>(q_s + qo + DH / 2);
+        } else {
+          const int qo = slot < a.grp ? 4 * ((hq * a.grp + slot) * DH + d0 + 4 * m) : kOOB;
+          q0v[hs] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0));
+          q1v[hs] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo == kOOB ? kOOB : qo + 2 * DH, 0, 0));
+        }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -2092,39 +2094,61 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
   };
   // the codebook of head hb into LDS when it is not the staged one (a
   // workgroup-uniform decision: hb is the head of the iteration's first chunk)
+  // the codebook (at most 32 KB) and the q rows (SLOTS x DH, at most 4 KB)
+  // of head hb: every load issued before the barrier and the writes
+  constexpr int CR4 = GS / 4, QR4 = DH / 4;
+  const int cn4 = G * C * CR4;
+  constexpr int QK = (SLOTS * QR4 + kRagThreads - 1) / kRagThreads;
+  struct StageRegs { float4 cb[kStage4], q[QK]; };
+  auto stage_load = [&](int hb, StageRegs& v) {
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + kRagThreads * k;
+      v.cb[k] = __builtin_bit_cast(float4,
+                                   __builtin_amdgcn_raw_buffer_load_b128(rcb, i < cn4 ? 16 * (hb * cn4 + i) : kOOB, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < QK; ++k) {
+      const int i = threadIdx.x + kRagThreads * k, sl = i / QR4;
+      const int src = (i < SLOTS * QR4 && sl < a.grp) ? 16 * ((hb * a.grp + sl) * QR4 + i % QR4) : kOOB;
+      v.q[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, src, 0, 0));
+    }
+  };
+  auto stage_store = [&](const StageRegs& v) {
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = threadIdx.x + kRagThreads * k;
+      if (i < cn4) *reinterpret_cast<float4*>(cb_s + rag_cb_index<GS>(i / CR4, i % CR4)) = v.cb[k];
+    }
+#pragma unroll
+    for (int k = 0; k < QK; ++k) {
+      const int i = threadIdx.x + kRagThreads * k;
+      if (i < SLOTS * QR4) *reinterpret_cast<float4*>(q_s + (i / QR4) * QS + 4 * (i % QR4)) = v.q[k];
+    }
+  };
+  auto stageable = [&](int hb) { return hb != staged && hb >= 0 && hb < a.num_kv && C <= 64; };
   auto stage = [&](int hb) {
-    if (hb == staged || hb < 0 || hb >= a.num_kv || C > 64) return;
-    // at most 32 KB: every load issued before the barrier and the writes
-    constexpr int R4 = GS / 4;
-    const int n4 = G * C * R4, base = hb * n4;
-    float4 v[kStage4];
-#pragma unroll
-    for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rcb, i < n4 ? 16 * (base + i) : kOOB, 0, 0));
-    }
-    __syncthreads();                                   // every wave is done with the previous codebook
-#pragma unroll
-    for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n4) *reinterpret_cast<float4*>(cb_s + (i / R4) * CS + 4 * (i % R4)) = v[k];
-    }
+    if (!stageable(hb)) return;
+    StageRegs v;
+    stage_load(hb, v);
+    __syncthreads();                                   // every wave is done with the previous head
+    stage_store(v);
     __syncthreads();
     staged = hb;
   };
 
-  // pipeline: rows two iterations ahead, page bytes and tables one ahead;
-  // rows and pages each in two register sets used alternately (the loop is
-  // unrolled by two, so no register a load is still filling is copied)
+  // pipeline: rows two iterations ahead, page bytes (and, on the table
+  // path, table rows) one ahead, in two register sets used alternately (the
+  // loop is unrolled by two, so no register a load is still filling is
+  // copied)
   RagRow ra = row_of(0), rb = row_of(1);
   float4 cca[NM], ssa[NM], ccb[NM], ssb[NM];
   RagPage ga = page_of(ra, 16 * ra.c16 + t, cca, ssa), gb;
-  __syncthreads();                                     // q staged
   for (int it = 0; it < it1; it += 2) {
     gb = page_of(rb, 16 * rb.c16 + t, ccb, ssb);       // waits for rows it + 1 (and so for pages it)
     ra = row_of(it + 2);
     stage(ga.hb);
-    if (q0 + 4 * it + wave < q1) {
+    if (q0 + kRagWaves * it + wave < q1) {
       if (ga.hk == staged) compute(Flag<true>(), ga, cca, ssa);
       else compute(Flag<false>(), ga, cca, ssa);
     }
@@ -2132,18 +2156,18 @@ __global__ __launch_bounds__(256) void ragged_pipe_kernel(RaggedLaunch a) {
     ga = page_of(ra, 16 * ra.c16 + t, cca, ssa);
     rb = row_of(it + 3);
     stage(gb.hb);
-    if (q0 + 4 * (it + 1) + wave < q1) {
+    if (q0 + kRagWaves * (it + 1) + wave < q1) {
       if (gb.hk == staged) compute(Flag<true>(), gb, ccb, ssb);
       else compute(Flag<false>(), gb, ccb, ssb);
     }
   }
 }
 
-// LDS bytes of ragged_pipe_kernel: padded q rows of every head (4 or 8 slots
-// per head) and the padded codebook of one head.
+// LDS bytes of ragged_pipe_kernel: the padded q rows (4 or 8 slots) and the
+// codebook of one head.
 inline int64_t ragged_pipe_lds(const RaggedLaunch& L) {
   const int64_t slots = L.grp > 4 ? 8 : 4;
-  return 4 * (L.num_kv * slots * (L.dh + 4) + (int64_t)(L.dh / L.group_size) * (1 << L.b_theta) * (L.group_size + 4));
+  return 4 * (slots * (L.dh + 4) + (int64_t)L.dh * (1 << L.b_theta));
 }
 
 int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
@@ -2152,15 +2176,14 @@ int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
   const bool fast = L.page_size % 16 == 0 && (L.group_size == 16 || L.group_size == 32) && L.grp <= 8 &&
                     L.groups * L.group_size == L.dh && L.pages_bytes <= 0x7FFFFFFFLL &&
                     (int64_t)L.num_pages * L.page_size * 4 <= 0x7FFFFF00LL;
-  const int64_t q_stage = (int64_t)L.num_kv * (L.grp > 4 ? 8 : 4) * L.dh * 4;
   const int64_t cb_bytes = (int64_t)L.dh * (1 << L.b_theta) * 4;
-  if (fast && L.b_theta <= 6 && q_stage <= 32768 && cb_bytes <= 32768 && ragged_pipe_lds(L) <= 65536) {
+  if (fast && L.b_theta <= 6 && cb_bytes <= 32768 && (int64_t)L.num_kv * L.grp * L.dh * 4 <= 0x7FFFFFFFLL) {
     const int64_t chunks = (int64_t)L.num_pages * (L.page_size / 16);
-    const int64_t iters = (chunks + 3) / 4;
+    const int64_t iters = (chunks + kRagWaves - 1) / kRagWaves;
     const size_t lds = (size_t)ragged_pipe_lds(L);
     const int rm = L.rope ? L.rope_model : kRopeNone;
     // one resident round of workgroups: as many per CU as registers and LDS
-    // allow (2 or 3), 256 CUs
+    // allow, 256 CUs
     auto launch = [&](const void* fn, void (*k)(RaggedLaunch)) {
       struct Occ { const void* fn; size_t lds; int per_cu; };
       thread_local Occ cache[8] = {};
@@ -2169,13 +2192,13 @@ int launch_ragged(const RaggedLaunch& L, hipStream_t stream) {
       for (const Occ& o : cache)
         if (o.fn == fn && o.lds == lds) per_cu = o.per_cu;
       if (per_cu == 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) per_cu = 2;
-        per_cu = per_cu < 1 ? 1 : per_cu > 3 ? 3 : per_cu;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kRagThreads, lds) != hipSuccess) per_cu = 1;
+        per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;
         cache[next] = Occ{fn, lds, per_cu};
         next = (next + 1) % 8;
       }
       const int64_t cap = 256LL * per_cu;
-      hipLaunchKernelGGL(k, dim3((unsigned)(iters < cap ? iters : cap)), dim3(256), lds, stream, L);
+      hipLaunchKernelGGL(k, dim3((unsigned)(iters < cap ? iters : cap)), dim3(kRagThreads), lds, stream, L);
     };
 #define SPHKV_RAGGED_RM(D, S, N, R) \
     if (L.dh == D && L.group_size == S && (L.grp > 4) == (N == 2) && rm == R) \
