@@ -610,10 +610,19 @@ def bench_step(args, dev):
     stg_tok = 4 * G3 + 4 * G3 + 2 * dh + 4                                 # radii, codes, V, position
     new_tok = 2 * dh * 2                                                   # k_new, v_new
 
-    def step_bytes(p):
-        j = done[p]
+    def step_bytes(j):
+        """(decode kernel, whole step) algorithmic bytes of a pool's step
+        after j appending steps on it."""
         kern = base + num_sh * (j // 16) * dec_page
         return kern, kern + num_sh * ((j % 16) * stg_tok + new_tok)
+
+    def steps_bytes(n, which):
+        """Bytes of the next n steps (pool i mod R, each appending)."""
+        sim, tot = list(done), 0
+        for i in range(n):
+            tot += step_bytes(sim[i % R])[which]
+            sim[i % R] += 1
+        return tot
 
     log(f"[bench] rows={wl.plan.num_rows} items={tails[0].num_items} pools={R} decode-page capacity={cap}")
     # untimed settle without appending (the contexts do not grow)
@@ -621,19 +630,21 @@ def bench_step(args, dev):
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    tot_bytes = 0
+    tot_bytes = steps_bytes(args.steps, 1)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    h0 = time.perf_counter()
     for i in range(args.steps):
-        tot_bytes += step_bytes(i % R)[1]
         step(i)
+    host_us = (time.perf_counter() - h0) / args.steps * 1e6
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     us = ms * 1e3
     nbytes = tot_bytes / args.steps
     gbps = nbytes / (ms * 1e-3) / 1e9
-    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s); "
+        f"host {host_us:.2f} us per step to enqueue")
 
     # the dominant kernel: the decode kernel of K more steps, each launch
     # timed by its own kernel-only timestamps (hipExtLaunchKernel events)
@@ -642,9 +653,8 @@ def bench_step(args, dev):
         e0.record()
         e1.record()
     torch.cuda.synchronize()
-    kb = 0
+    kb = steps_bytes(args.steps, 0)
     for i in range(args.steps):
-        kb += step_bytes(i % R)[0]
         ops.time_next_decode_kernel(*evs[i])
         step(i)
     torch.cuda.synchronize()
@@ -670,6 +680,7 @@ def bench_step(args, dev):
                                f"full decode step: page context + staged tokens + new token, then the append",
                    "num_seqs": wl.num_seqs, "ctx": max(wl.lengths), "pages": wl.plan.num_rows,
                    "rotated_pools": R, "algorithmic_bytes_per_step": round(nbytes),
+                   "call": "DecodeTail.runner() (sphkv_step_plan_run)", "host_us_per_step": round(host_us, 2),
                    "kernels_per_step": ["decode_kernel", "decode_tail_kernel"]},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
@@ -747,21 +758,35 @@ def main():
     ws = torch.zeros(max(pool0.workspace_bytes(wl.gqa), 4), dtype=torch.uint8, device=dev)
     nbytes = fmt.decode_bytes(wl.plan)
     log(f"[bench] rows={wl.plan.num_rows} items={pool0.num_items} algorithmic bytes/step={nbytes}")
+    # the bound call (one ctypes call of four arguments per step)
+    runs = [ops.DecodeRunner(p, wl.gqa, wl.rope_theta, workspace=ws).raw() for p in pools]
+    qp, op, R = q.data_ptr(), out.data_ptr(), len(pools)
 
-    settle(lambda i: ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws))
+    settle(lambda i: runs[i % R](qp, op))
     for i in range(args.warmup):
-        ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
+        runs[i % R](qp, op)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    h0 = time.perf_counter()
     for i in range(args.steps):
-        ops.decode_paged(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
+        runs[i % R](qp, op)
+    host_us = (time.perf_counter() - h0) / args.steps * 1e6
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     us = ms * 1e3
     gbps = nbytes / (ms * 1e-3) / 1e9
-    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s)")
+    log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s); "
+        f"host {host_us:.2f} us per call to enqueue")
+    # host cost of the checked Python call, for comparison (enqueue only)
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    for i in range(args.steps):
+        ops.decode_paged(pools[i % R], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
+    py_host_us = (time.perf_counter() - h0) / args.steps * 1e6
+    torch.cuda.synchronize()
+    log(f"[bench] decode_paged (checked Python call): host {py_host_us:.2f} us per call to enqueue")
 
     # the dominant kernel alone: the same steps' first phase (partials), timed
     # with HIP events on the stream it runs on
@@ -802,7 +827,9 @@ def main():
         "config": {"workload": f"config{args.config}: {wl.num_q} q / {wl.num_kv} kv heads, dh {wl.dh}, "
                                f"{wl.num_seqs} seq x {max(wl.lengths)} ctx, 16-token pages, tier mix of BASELINE",
                    "num_seqs": wl.num_seqs, "ctx": max(wl.lengths), "pages": wl.plan.num_rows,
-                   "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes},
+                   "rotated_pools": len(pools), "algorithmic_bytes_per_step": nbytes,
+                   "call": "DecodeRunner.raw() (sphkv_decode_plan_run)", "host_us_per_call": round(host_us, 2),
+                   "host_us_per_call_decode_paged": round(py_host_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": measured_traffic(args.config, args.layout),

@@ -227,6 +227,29 @@ int sphkv_decode_merge_partials(const void* workspace, int64_t workspace_bytes, 
                                 int32_t gqa, int32_t dh, uint16_t* out, void* stream);
 
 /*
+ * A bound paged decode, no reference counterpart: every argument of
+ * sphkv_decode_paged but q, out and the stream, checked once at creation;
+ * each sphkv_decode_plan_run then launches the decode (partials and merge)
+ * with no further argument checks.  For serving loops whose per-call host
+ * cost matters (the reference's decode is one Python call per layer,
+ * spherical_kv_pipeline.py:2057).  The plan holds the pointers it was given:
+ * the buffers must outlive it and keep their sizes.  A plan may be run from
+ * several threads; runs that share its workspace must not overlap on the
+ * device (use one stream, or one plan per stream).
+ */
+typedef struct sphkv_decode_plan sphkv_decode_plan;
+int sphkv_decode_plan_create(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                             const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                             const uint16_t* v_pool, int64_t num_vpages,
+                             const float* cb1, const float* cb2, const float* cb3,
+                             const int32_t* work, int32_t num_items, const int32_t* work_start,
+                             int32_t num_seqs, int32_t num_kv, int32_t gqa, void* workspace,
+                             int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
+                             double rope_theta, sphkv_decode_plan** plan_out);
+int sphkv_decode_plan_run(const sphkv_decode_plan* plan, const uint16_t* q, uint16_t* out, void* stream);
+void sphkv_decode_plan_destroy(sphkv_decode_plan* plan);
+
+/*
  * Measurement hook, no reference counterpart: the next launch of the paged
  * decode kernel on the calling thread (by sphkv_decode_paged, _checked,
  * _partials, _noalloc or sphkv_decode_step) records its own start and stop

@@ -116,13 +116,13 @@ int64_t sphkv_decode_paged_workspace_bytes(int32_t num_items, int32_t gqa, int32
 
 namespace {
 
-int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_bytes,
-                const int32_t* ptable, const int32_t* vslot, const int32_t* positions, int32_t num_rows,
-                const uint16_t* v_pool, int64_t num_vpages, const float* cb1, const float* cb2,
-                const float* cb3, const int32_t* work, int32_t num_items, const int32_t* work_start,
-                int32_t num_seqs, int32_t num_kv, int32_t gqa, const uint16_t* q, uint16_t* out,
-                void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size,
-                float sm_scale, double rope_theta, void* stream) {
+// argument checks of the paged decode (SPHKV_OK: launchable, or nothing to do for num_seqs == 0)
+int decode_checks(const char* fn, int phases, const uint8_t* pages, int64_t pages_bytes,
+                  const int32_t* ptable, const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                  const uint16_t* v_pool, int64_t num_vpages, const int32_t* work, int32_t num_items,
+                  const int32_t* work_start, int32_t num_seqs, int32_t num_kv, int32_t gqa, const uint16_t* q,
+                  uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size,
+                  double rope_theta) {
   if (!dh_ok(dh)) return fail(SPHKV_EINVAL, "%s: dh must be 64 or 128 (got %d)", fn, dh);
   if (!gqa_ok(gqa)) return fail(SPHKV_EINVAL, "%s: gqa must be 1, 2, 4 or 8 (got %d)", fn, gqa);
   if (page_size != 16) return fail(SPHKV_EINVAL, "%s: page_size must be 16 (got %d)", fn, page_size);
@@ -153,6 +153,20 @@ int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_
   if ((phases & sphkv::kPhasePartials) &&
       (!q || !work || !pages || !ptable || !vslot || !positions || !v_pool))
     return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
+  return SPHKV_OK;
+}
+
+int decode_call(const char* fn, int phases, const uint8_t* pages, int64_t pages_bytes,
+                const int32_t* ptable, const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                const uint16_t* v_pool, int64_t num_vpages, const float* cb1, const float* cb2,
+                const float* cb3, const int32_t* work, int32_t num_items, const int32_t* work_start,
+                int32_t num_seqs, int32_t num_kv, int32_t gqa, const uint16_t* q, uint16_t* out,
+                void* workspace, int64_t workspace_bytes, int32_t dh, int32_t page_size,
+                float sm_scale, double rope_theta, void* stream) {
+  const int rc = decode_checks(fn, phases, pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool,
+                               num_vpages, work, num_items, work_start, num_seqs, num_kv, gqa, q, out, workspace,
+                               workspace_bytes, dh, page_size, rope_theta);
+  if (rc != SPHKV_OK || num_seqs == 0) return rc == SPHKV_OK ? ok() : rc;
   sphkv::DecodeLaunch L{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
                         cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, q, out,
                         static_cast<float*>(workspace), dh, sm_scale, rope_theta};
@@ -371,7 +385,12 @@ int sphkv_decode_append(uint8_t* pages, int64_t pages_bytes, int32_t* positions,
 // A bound decode step: every static argument of sphkv_decode_step, validated
 // once, and the host's mirror of the tail counts (every (seq, head) stages
 // one token per appending step).
+// Plans carry a tag, cleared when they are destroyed: a run on a destroyed
+// plan whose memory still holds the cleared tag fails instead of launching.
+constexpr uint32_t kStepPlanTag = 0x53504C31u, kDecodePlanTag = 0x44504C31u, kDeadPlanTag = 0u;
+
 struct sphkv_step_plan {
+  uint32_t tag;
   sphkv::DecodeLaunch L;
   sphkv::TailLaunch T;
   int64_t workspace_bytes;
@@ -417,6 +436,7 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
     return fail(SPHKV_EINVAL, "%s: staged must be 0..15 and flushed 0..dec_cap", fn);
   auto* p = new (std::nothrow) sphkv_step_plan;
   if (!p) return fail(SPHKV_EINVAL, "%s: out of host memory", fn);
+  p->tag = kStepPlanTag;
   p->L = sphkv::DecodeLaunch{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
                              cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, nullptr, nullptr,
                              static_cast<float*>(workspace), dh, sm_scale, rope_theta};
@@ -433,7 +453,7 @@ int sphkv_step_plan_create(uint8_t* pages, int64_t pages_bytes, const int32_t* p
 int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_new, int32_t k_is_fp32,
                         const uint16_t* v_new, const int32_t* cur_pos, uint16_t* out, int32_t mode, void* stream) {
   const char* fn = "sphkv_step_plan_run";
-  if (!plan) return fail(SPHKV_EINVAL, "%s: null plan", fn);
+  if (!plan || plan->tag != kStepPlanTag) return fail(SPHKV_EINVAL, "%s: null or destroyed plan", fn);
   if (mode < 1 || mode > 3) return fail(SPHKV_EINVAL, "%s: mode must be 1 (decode), 2 (append) or 3 (both)", fn);
   const bool dec = mode & sphkv::kTailDecode, app = mode & sphkv::kTailAppend;
   if (!k_new || !v_new || !cur_pos || (dec && (!q || !out))) return fail(SPHKV_EINVAL, "%s: null pointer argument", fn);
@@ -462,14 +482,72 @@ int sphkv_step_plan_run(sphkv_step_plan* plan, const uint16_t* q, const void* k_
 }
 
 int sphkv_step_plan_counts(const sphkv_step_plan* plan, int32_t* staged, int32_t* flushed, int32_t* step_parity) {
-  if (!plan || !staged || !flushed || !step_parity) return fail(SPHKV_EINVAL, "sphkv_step_plan_counts: null argument");
+  if (!plan || plan->tag != kStepPlanTag || !staged || !flushed || !step_parity)
+    return fail(SPHKV_EINVAL, "sphkv_step_plan_counts: null argument or destroyed plan");
   *staged = plan->staged;
   *flushed = plan->flushed;
   *step_parity = plan->parity;
   return ok();
 }
 
-void sphkv_step_plan_destroy(sphkv_step_plan* plan) { delete plan; }
+void sphkv_step_plan_destroy(sphkv_step_plan* plan) {
+  if (!plan) return;
+  *reinterpret_cast<volatile uint32_t*>(&plan->tag) = kDeadPlanTag;
+  delete plan;
+}
+
+}  // extern "C"
+
+struct sphkv_decode_plan {
+  uint32_t tag;
+  sphkv::DecodeLaunch L;
+};
+
+extern "C" {
+
+int sphkv_decode_plan_create(const uint8_t* pages, int64_t pages_bytes, const int32_t* ptable,
+                             const int32_t* vslot, const int32_t* positions, int32_t num_rows,
+                             const uint16_t* v_pool, int64_t num_vpages,
+                             const float* cb1, const float* cb2, const float* cb3,
+                             const int32_t* work, int32_t num_items, const int32_t* work_start,
+                             int32_t num_seqs, int32_t num_kv, int32_t gqa, void* workspace,
+                             int64_t workspace_bytes, int32_t dh, int32_t page_size, float sm_scale,
+                             double rope_theta, sphkv_decode_plan** plan_out) {
+  const char* fn = "sphkv_decode_plan_create";
+  if (!plan_out) return fail(SPHKV_EINVAL, "%s: null plan_out", fn);
+  *plan_out = nullptr;
+  // q and out come with each run: a stand-in address lets the checks run
+  static uint16_t probe[1] = {0};
+  int rc = decode_checks(fn, sphkv::kPhasePartials | sphkv::kPhaseMerge, pages, pages_bytes, ptable, vslot,
+                         positions, num_rows, v_pool, num_vpages, work, num_items, work_start, num_seqs, num_kv,
+                         gqa, probe, probe, workspace, workspace_bytes, dh, page_size, rope_theta);
+  if (rc != SPHKV_OK) return rc;
+  if (num_seqs <= 0) return fail(SPHKV_EINVAL, "%s: num_seqs must be > 0", fn);
+  auto* p = new (std::nothrow) sphkv_decode_plan;
+  if (!p) return fail(SPHKV_EINVAL, "%s: out of host memory", fn);
+  p->tag = kDecodePlanTag;
+  p->L = sphkv::DecodeLaunch{pages, pages_bytes, ptable, vslot, positions, num_rows, v_pool, num_vpages,
+                             cb1, cb2, cb3, work, num_items, work_start, num_seqs, num_kv, gqa, nullptr, nullptr,
+                             static_cast<float*>(workspace), dh, sm_scale, rope_theta};
+  *plan_out = p;
+  return ok();
+}
+
+int sphkv_decode_plan_run(const sphkv_decode_plan* plan, const uint16_t* q, uint16_t* out, void* stream) {
+  if (!plan || plan->tag != kDecodePlanTag || !q || !out)
+    return fail(SPHKV_EINVAL, "sphkv_decode_plan_run: null argument or destroyed plan");
+  sphkv::DecodeLaunch L = plan->L;
+  L.q = q;
+  L.out = out;
+  return launch_status(sphkv::launch_decode(L, sphkv::kPhasePartials | sphkv::kPhaseMerge, (hipStream_t)stream),
+                       "sphkv_decode_plan_run");
+}
+
+void sphkv_decode_plan_destroy(sphkv_decode_plan* plan) {
+  if (!plan) return;
+  *reinterpret_cast<volatile uint32_t*>(&plan->tag) = kDeadPlanTag;
+  delete plan;
+}
 
 int sphkv_time_next_decode_kernel(void* start_event, void* stop_event) {
   if ((start_event == nullptr) != (stop_event == nullptr))

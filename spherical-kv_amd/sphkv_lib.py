@@ -56,6 +56,10 @@ SIGNATURES = {
     "sphkv_fused_decode_ragged_fitted": (ctypes.c_int, [P, I64, P, P, P, I32, P, P, I32, P, I32, I32, P,
                                                         I32, I32, I32, I32, I32, P, I32, P, P]),
     "sphkv_rope_table_fit": (ctypes.c_int, [P, P, I32, I32, P, P, P, P]),
+    "sphkv_decode_plan_create": (ctypes.c_int, [P, I64, P, P, P, I32, P, I64, P, P, P, P, I32, P, I32, I32, I32,
+                                                P, I64, I32, I32, F32, F64, P]),
+    "sphkv_decode_plan_run": (ctypes.c_int, [P, P, P, P]),
+    "sphkv_decode_plan_destroy": (None, [P]),
     "sphkv_encode_append": (ctypes.c_int, [P, P, P, P, P, P, P, P, I32, I64, I32, I32, I32, I32, I32,
                                            I32, I32, I32, P]),
     "sphkv_decode_modea": (ctypes.c_int, [P, P, P, P, P, P, P, P, I64, P, P, P, P, P, I32, I32, I32, I32,

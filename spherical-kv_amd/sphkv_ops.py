@@ -413,6 +413,69 @@ def decode_paged(pool: PagedPool, q: torch.Tensor, gqa: int, rope_theta: float,
     return out
 
 
+class DecodeRunner:
+    """decode_paged bound to one pool (sphkv_decode_plan): the pool's
+    pointers, gqa, RoPE base, scale and workspace are checked once here, and
+    each call is one ctypes call of four arguments.  Holds the pool and the
+    workspace; calls that share the workspace must not overlap on the device.
+
+    runner(q, out) checks q and out like decode_paged and returns out;
+    runner.raw() returns fn(q_ptr, out_ptr) over raw device addresses, bound
+    to the stream current when raw() is called (no checks: the serving-loop
+    form)."""
+
+    def __init__(self, pool: PagedPool, gqa: int, rope_theta: float, sm_scale: Optional[float] = None,
+                 workspace: Optional[torch.Tensor] = None):
+        import ctypes
+        plan = pool.plan
+        self.pool, self.gqa, self.rope_theta = pool, int(gqa), float(rope_theta)
+        self.workspace = _decode_workspace(pool, gqa, workspace)
+        self.sm_scale = float(1.0 / math.sqrt(plan.dh) if sm_scale is None else sm_scale)
+        self._plan = None
+        lib = load()
+        c1, c2, c3 = pool.cb_ptrs()
+        h = ctypes.c_void_p()
+        rc = lib.sphkv_decode_plan_create(
+            pool.pages.data_ptr(), plan.pages_bytes, pool.ptable.data_ptr(), pool.vslot.data_ptr(),
+            pool.positions.data_ptr(), plan.num_rows, pool.v_pool.data_ptr(), plan.num_vpages, c1, c2, c3,
+            pool.work.data_ptr(), pool.num_items, pool.work_start.data_ptr(), plan.num_seqs, plan.num_kv,
+            self.gqa, self.workspace.data_ptr(), self.workspace.numel(), plan.dh, plan.page_size, self.sm_scale,
+            self.rope_theta, ctypes.byref(h))
+        check(rc, "sphkv_decode_plan_create")
+        self._plan = h.value
+        self._run = lib.sphkv_decode_plan_run
+        self._pages, self._v_pool = pool.pages, pool.v_pool
+
+    def __call__(self, q: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.pool.pages is not self._pages or self.pool.v_pool is not self._v_pool:
+            raise ValueError("the pool's byte pool or V pool was replaced after the runner was bound")
+        _check_q(self.pool, q, self.gqa)
+        if out is None:
+            out = torch.empty_like(q)
+        _need(out, torch.float16, "out", self.pool.device)
+        if out.shape != q.shape:
+            raise ValueError("out must match q")
+        check(self._run(self._plan, q.data_ptr(), out.data_ptr(), _stream()), "sphkv_decode_plan_run")
+        return out
+
+    def raw(self):
+        run, stream, owner = self._run, _stream(), self
+
+        def fn(q_ptr: int, out_ptr: int) -> None:
+            # the closure holds the runner: its plan lives as long as fn
+            rc = run(owner._plan, q_ptr, out_ptr, stream)
+            if rc:
+                check(rc, "sphkv_decode_plan_run")
+        return fn
+
+    def __del__(self):
+        try:
+            if self._plan is not None:
+                load().sphkv_decode_plan_destroy(self._plan)
+        except Exception:
+            pass
+
+
 def decode_status(pool: PagedPool, workspace: torch.Tensor, gqa: int) -> int:
     """Malformed rows / pages skipped by the last merged decode on this
     workspace (waits for the current stream)."""
@@ -621,11 +684,12 @@ class DecodeTail:
     def runner(self):
         """The fastest call of a step: fn(q_ptr, k_ptr, k_is_fp32, v_ptr, pos_ptr, out_ptr, mode) with raw
         device addresses (mode 1 decode, 2 append, 3 both) on the current stream; one ctypes call."""
-        run, plan = self._run, self._plan
-        stream = _stream()
+        run, stream, owner = self._run, _stream(), self
 
         def fn(q, k, k32, v, pos, out, mode):
-            check(run(plan, q, k, k32, v, pos, out, mode, stream), "sphkv_step_plan_run")
+            # the closure holds the tail, and reads its current plan (reset()
+            # binds a new one)
+            check(run(owner._plan, q, k, k32, v, pos, out, mode, stream), "sphkv_step_plan_run")
         return fn
 
     def _step_inputs(self, k_new: torch.Tensor, v_new: torch.Tensor, cur_pos: torch.Tensor):

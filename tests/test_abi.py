@@ -252,3 +252,55 @@ def test_noalloc_refuses_work_beyond_its_scratch():
     args = _decode_args(num_seqs=0)
     del args[19:21]
     assert lib.sphkv_decode_paged_noalloc(*args) == 0
+
+
+def test_decode_plan_argument_errors():
+    import ctypes
+    lib = sphkv_lib.load()
+    h = ctypes.c_void_p(123)
+    # (pages, bytes, ptable, vslot, positions, rows, v_pool, vpages, cb1..3, work, items, work_start,
+    #  seqs, kv, gqa, workspace, ws_bytes, dh, page_size, sm_scale, theta, plan_out)
+    args = [None, 0, None, None, None, 0, None, 0, None, None, None, None, 8, None, 1, 8, 4, None, 1 << 20,
+            96, 16, 0.1, 500000.0, ctypes.byref(h)]
+    assert lib.sphkv_decode_plan_create(*args) == -1
+    assert "dh must be 64 or 128" in lib.sphkv_last_error().decode()
+    assert h.value is None                         # no plan on error
+    args[19] = 128
+    args[14] = 0                                   # no sequence: nothing a plan could run
+    assert lib.sphkv_decode_plan_create(*args) == -1
+    args[14] = 1
+    assert lib.sphkv_decode_plan_create(*args) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    args[-1] = None
+    assert lib.sphkv_decode_plan_create(*args) == -1
+    assert "plan_out" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_decode_plan_run(None, None, None, None) == -1
+    lib.sphkv_decode_plan_destroy(None)            # a no-op
+
+
+def test_decode_runner_closure_keeps_its_plan_alive(monkeypatch):
+    # the raw() form of a bound decode holds its runner, so the C plan cannot
+    # be destroyed while the closure exists (a runner built and dropped in one
+    # expression, DecodeRunner(...).raw(), must stay usable); built here with
+    # stand-in addresses: plan creation checks arguments and touches no memory
+    import ctypes
+    import gc
+    import weakref
+    import sphkv_ops as ops
+    lib = sphkv_lib.load()
+    h = ctypes.c_void_p()
+    fake = 1 << 20                                    # non-null stand-in address, never dereferenced
+    rc = lib.sphkv_decode_plan_create(fake, 1024, fake, fake, fake, 8, fake, 8, fake, None, None, fake, 8, fake,
+                                      1, 8, 4, fake, 1 << 20, 128, 16, 0.1, 500000.0, ctypes.byref(h))
+    assert rc == 0 and h.value
+    monkeypatch.setattr(ops, "_stream", lambda: 0)    # (no device here: the default stream's handle)
+    r = object.__new__(ops.DecodeRunner)
+    r._plan, r._run = h.value, lib.sphkv_decode_plan_run
+    alive = weakref.ref(r)
+    fn = r.raw()
+    del r
+    gc.collect()
+    assert alive() is not None                        # held by fn
+    del fn
+    gc.collect()
+    assert alive() is None                            # and released with it (its plan destroyed)

@@ -468,3 +468,35 @@ def test_decode_peaked_softmax_with_sink(gpu, config, heads):
         assert err <= TOL
     else:
         check_sampled_heads(wl, pool, out, heads, seed=55, tol=TOL)
+
+
+@pytest.mark.parametrize("config,ctx", [(2, 4096), (1, None)])
+def test_decode_runner_equals_decode_paged(gpu, config, ctx):
+    # the bound call (sphkv_decode_plan) launches the same kernels as
+    # decode_paged: bit-identical output, in both of its forms, over two
+    # calls with different q
+    wl = synth.make_decode_workload(config, ctx_override=ctx)
+    pool, cpu = pool_from_oracle(wl, gpu)
+    run = ops.DecodeRunner(pool, wl.gqa, wl.rope_theta)
+    fn = run.raw()
+    rng = np.random.default_rng(30)
+    for k in range(2):
+        qh = wl.q if k == 0 else (rng.standard_normal(wl.q.shape) * 0.5).astype(np.float16)
+        q = torch.as_tensor(qh, device=gpu)
+        a = ops.decode_paged(pool, q, wl.gqa, wl.rope_theta)
+        b = run(q)
+        c = torch.empty_like(q)
+        fn(q.data_ptr(), c.data_ptr())
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(a, c)
+    want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, qh, wl.gqa, wl.rope_theta)
+    assert max_err(c.float().cpu().numpy(), want) <= TOL
+    # regression: a runner dropped right after raw() (the closure keeps it and
+    # its plan alive)
+    import gc
+    fn2 = ops.DecodeRunner(pool, wl.gqa, wl.rope_theta).raw()
+    gc.collect()
+    d = torch.empty_like(q)
+    fn2(q.data_ptr(), d.data_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(a, d)
