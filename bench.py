@@ -2,13 +2,19 @@
 
 `python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]`
 
-A step is one decode over the whole paged context of one layer (all kv heads)
-for the workload named in BASELINE.json's metric: config 2, Llama-3.1-8B
-attention shape (32 q / 8 kv heads, dh 128), 32K context, 60/30/10 tier mix,
-randomly permuted page table.  Inputs are resident in HBM before timing; the
+A step is one full reference decode step of one layer (all kv heads) for the
+workload named in BASELINE.json's metric: config 2, Llama-3.1-8B attention
+shape (32 q / 8 kv heads, dh 128), 32K context, 60/30/10 tier mix, randomly
+permuted page table: attention over the page-resident context, the tokens
+staged since the last decode page and the step's new token in one softmax,
+then the new token's append (tier-3 encode, staging, a page flush every 16
+steps) -- decode_kernel + decode_tail_kernel through the bound step call
+(DecodeTail.runner()).  Inputs are resident in HBM before timing; the
 Infinity Cache (256 MB) is defeated by rotating through ROTATE independent
 copies of the KV pool (each ~80 MB).  Timing uses HIP events on the stream the
-kernels run on (torch's current stream), around exactly K steps.
+kernels run on (torch's current stream), around exactly K steps; the
+roofline object's kernel time is decode_kernel's own start / stop timestamps
+(hipExtLaunchKernel) over K more steps, the duration rocprofv3 reports.
 
 Before the W counted warmup steps, every path runs an untimed settle phase
 of the same step for at least SETTLE_S seconds: on a fresh process the GPU's
@@ -22,8 +28,9 @@ attention shape with unpacked uint8 pools (fused_decode.sphkv_decode);
 `--path prefill` measures prefill paging of the same layer on the GPU (device
 page plan + fused encode / bitpack / V placement); `--path ragged` measures
 fused_decode_ragged (logits only) over the same layer's tier-1 and tier-2
-pages.  The default line is the
-angle-domain (Mode-B) decode above.
+pages, with the caller's RoPE tables fitted once; `--path pages` measures the
+page-resident decode alone (decode_kernel + decode_merge_kernel through the
+bound DecodeRunner).  The default line is the full decode step above.
 """
 from __future__ import annotations
 
@@ -71,6 +78,17 @@ def settle(step_fn):
         torch.cuda.synchronize()
 
 
+def calibrate_copies(dev):
+    """Four plain device copies of COPY_BYTES (torch copy_): the reference of
+    known traffic for the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration: 4 device copies of {COPY_BYTES} bytes")
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -86,7 +104,7 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
 # with `bench.py --calibrate` under rocprofv3 --pmc (summary and commands in
 # profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
-TRAFFIC_BYTES = {(2, "default"): 86461801}
+TRAFFIC_BYTES = {(2, "default"): 86506939}
 
 # encode_pages_kernel at config 3, from rocprofv3 --pmc on MI355X
 # (profiles/encode_config3_counters.txt): VALU instructions per launch (MFMA
@@ -100,7 +118,7 @@ ENCODE_TRAFFIC_BYTES = {3: 55598602}
 # tiers' ragged_pipe_kernel launches; profiles/ragged_config2_hbm_traffic.txt),
 # FETCH_SIZE * 2 + WRITE_SIZE as above.
 MODEA_TRAFFIC_BYTES = {16: 80479122}
-RAGGED_TRAFFIC_BYTES = 47988605
+RAGGED_TRAFFIC_BYTES = {"fit": 13703189, "table": 47988605}   # phases in the kernel / table rows read
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
@@ -437,6 +455,8 @@ def bench_ragged(args, dev):
     gbps = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] fused_decode_ragged {ms * 1e3:.2f} us per step (tiers 1 + 2)  {gbps:.1f} GB/s; "
         f"host {host_us:.2f} us per step to enqueue")
+    if args.calibrate:
+        calibrate_copies(dev)
     cpu = None
     if not args.no_cpu_baseline:
         pages_h = pool.pages.cpu().numpy()
@@ -461,8 +481,12 @@ def bench_ragged(args, dev):
                    "rope_tables": args.rope_tables, "rope_model": int(model), "rope_fit_once_ms": round(fit_ms, 2),
                    "host_us_per_step": round(host_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": RAGGED_TRAFFIC_BYTES, "kernel": "ragged_pipe_kernel",
-                     "kernel_us": round(ms * 1e3, 3)},
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": RAGGED_TRAFFIC_BYTES["fit" if model else "table"], "kernel": "ragged_pipe_kernel",
+                     "kernel_us": round(ms * 1e3, 3),
+                     "frac_of": "both tiers' launches back to back (HIP events around the step); algorithmic bytes",
+                     "traffic_of": "both launches, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
+                                   "(profiles/ragged_config2_hbm_traffic.txt)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -662,6 +686,8 @@ def bench_step(args, dev):
     kbytes = kb / args.steps
     kern_gbps = kbytes / (kern_ms * 1e-3) / 1e9
     log(f"[bench] decode_kernel {kern_ms * 1e3:.2f} us (kernel-only timestamps)  {kern_gbps:.1f} GB/s")
+    if args.calibrate:
+        calibrate_copies(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -686,11 +712,15 @@ def bench_step(args, dev):
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": measured_traffic(args.config, args.layout),
                      "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
-                     "kernel_timing": "kernel-only start/stop timestamps of each launch (hipExtLaunchKernel), "
-                                      "the duration rocprofv3's kernel trace reports",
-                     "numerator": "algorithmic bytes of the kernel's launch (pages, dense K, V, positions, "
-                                  "pointer-table rows)",
-                     "step_frac": round(gbps / PEAK_HBM_GBPS, 4)},
+                     "frac_of": "decode_kernel alone (the step's dominant kernel), kernel-only start / stop "
+                                "timestamps of each launch (hipExtLaunchKernel); algorithmic bytes of its launch "
+                                "(pages, dense K, V, positions, pointer-table rows)",
+                     "traffic_of": "decode_kernel launch, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
+                                   "(profiles/decode_config2_hbm_traffic.txt)",
+                     "whole_step_achieved": round(gbps, 1),
+                     "whole_step_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "whole_step_of": "the headline value: both kernels, HIP events around the steps; algorithmic "
+                                      "bytes incl. the staged tokens and the new token"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -788,28 +818,26 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] decode_paged (checked Python call): host {py_host_us:.2f} us per call to enqueue")
 
-    # the dominant kernel alone: the same steps' first phase (partials), timed
-    # with HIP events on the stream it runs on
+    # the dominant kernel alone: K decode_kernel launches back to back (the
+    # partials phase only), HIP events around them on the stream they run on
+    # (the launch gap included).  Kernel-only timestamps of a launch that
+    # follows the merge kernel start while that kernel still runs here, so
+    # they are not used on this path.
     for i in range(args.warmup):
-        ops.decode_paged_partials(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, ws)
+        ops.decode_paged_partials(pools[i % R], q, wl.gqa, wl.rope_theta, ws)
     torch.cuda.synchronize()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     k0.record()
     for i in range(args.steps):
-        ops.decode_paged_partials(pools[i % len(pools)], q, wl.gqa, wl.rope_theta, ws)
+        ops.decode_paged_partials(pools[i % R], q, wl.gqa, wl.rope_theta, ws)
     k1.record()
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / args.steps
     kern_gbps = nbytes / (kern_ms * 1e-3) / 1e9
-    log(f"[bench] decode_kernel alone {kern_ms * 1e3:.2f} us  {kern_gbps:.1f} GB/s")
+    log(f"[bench] decode_kernel {kern_ms * 1e3:.2f} us (back-to-back launches)  {kern_gbps:.1f} GB/s")
 
     if args.calibrate:
-        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration: 4 device copies of {COPY_BYTES} bytes")
+        calibrate_copies(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -834,7 +862,13 @@ def main():
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": measured_traffic(args.config, args.layout),
                      "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
-                     "step_frac": round(gbps / PEAK_HBM_GBPS, 4)},
+                     "frac_of": "decode_kernel alone, HIP events around back-to-back launches (launch gap "
+                                "included); algorithmic bytes of its launch",
+                     "traffic_of": "decode_kernel launch, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
+                                   "(profiles/decode_config2_hbm_traffic.txt)",
+                     "whole_step_achieved": round(gbps, 1),
+                     "whole_step_frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "whole_step_of": "the value: decode_kernel + decode_merge_kernel, HIP events around the steps"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
