@@ -21,7 +21,7 @@ from gpu_helpers import check_sampled_heads, log
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("config,heads", [(4, 6), (5, 3)])
+@pytest.mark.parametrize("config,heads", [(4, 16), (5, 6)])
 def test_full_size_decode_matches_oracle_on_sampled_heads(gpu, config, heads):
     log(f"full-size config {config}: drawing K/V on the device and planning")
     wl = synth.make_decode_workload(config, kv_device=gpu)
