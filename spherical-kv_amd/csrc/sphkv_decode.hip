@@ -1905,18 +1905,20 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
              << (8 * i);
   const rsrc_t rq = make_rsrc(a.q, (int64_t)a.num_kv * a.grp * DH * 4);
   const int d0 = NPL * u, gi = d0 / GS, off = d0 % GS, gj = gi + G / 2;
-  // the fitted frequencies of the lane's pairs d0 .. d0 + NPL - 1; a fit of
-  // another model or shape makes every logit NaN
-  double fr[RM == kRopeExact ? NPL : 1];
-  float iv[RM == kRopeFp32 ? NPL : 1];
+  // the fitted frequencies in LDS (a lane reads its pairs' four at a time:
+  // 16 registers fewer than holding them); a fit of another model or shape
+  // makes every logit NaN.  The return above is workgroup-uniform, so every
+  // thread reaches the barrier.
+  __shared__ double fr_s[RM == kRopeExact ? DH / 2 : 1];
+  __shared__ float iv_s[RM == kRopeFp32 ? DH / 2 : 1];
   bool fit_ok = true;
   if constexpr (RM != kRopeNone) {
     fit_ok = a.rope->model == RM && a.rope->dh == DH && a.rope->max_pos == a.max_pos;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      if constexpr (RM == kRopeExact) fr[i] = a.rope->f[d0 + i];
-      else iv[i] = a.rope->inv32[d0 + i];
+    if (threadIdx.x < DH / 2) {
+      if constexpr (RM == kRopeExact) fr_s[threadIdx.x] = a.rope->f[threadIdx.x];
+      else iv_s[threadIdx.x] = a.rope->inv32[threadIdx.x];
     }
+    __syncthreads();
   }
 
   auto row_of = [&](int it) {                          // issue round trip 1 of this wave's chunk of iteration it
@@ -2040,10 +2042,19 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
         co[0] = cc[m].x; co[1] = cc[m].y; co[2] = cc[m].z; co[3] = cc[m].w;
         si[0] = ss[m].x; si[1] = ss[m].y; si[2] = ss[m].z; si[3] = ss[m].w;
       } else {
+        float ivm[4];
+        double frm[4];
+        if constexpr (RM == kRopeFp32) {
+          const float4 w = *reinterpret_cast<const float4*>(iv_s + d0 + 4 * m);
+          ivm[0] = w.x; ivm[1] = w.y; ivm[2] = w.z; ivm[3] = w.w;
+        } else {
+          const double2 w0 = *reinterpret_cast<const double2*>(fr_s + d0 + 4 * m);
+          const double2 w1 = *reinterpret_cast<const double2*>(fr_s + d0 + 4 * m + 2);
+          frm[0] = w0.x; frm[1] = w0.y; frm[2] = w1.x; frm[3] = w1.y;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const double x = RM == kRopeExact ? (double)ppos * fr[4 * m + e]
-                                            : (double)((float)ppos * iv[4 * m + e]) * kInvTwoPi;
+          const double x = RM == kRopeExact ? (double)ppos * frm[e] : (double)((float)ppos * ivm[e]) * kInvTwoPi;
           const float2 z = turn_phasor(x);
           co[e] = z.x;
           si[e] = z.y;
@@ -2100,29 +2111,37 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
   const int cn4 = G * C * CR4;
   constexpr int QK = (SLOTS * QR4 + kRagThreads - 1) / kRagThreads;
   struct StageRegs { float4 cb[kStage4], q[QK]; };
+  // The stage's addresses and predicates are formed at each stage (an opaque
+  // copy of the thread index keeps the compiler from computing them once in
+  // the prologue and holding them, with their predicates, in registers for
+  // the whole kernel: a stage is rare, the registers are not).
   auto stage_load = [&](int hb, StageRegs& v) {
+    int tx = threadIdx.x;
+    asm volatile("" : "+v"(tx));
 #pragma unroll
     for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + kRagThreads * k;
+      const int i = tx + kRagThreads * k;
       v.cb[k] = __builtin_bit_cast(float4,
                                    __builtin_amdgcn_raw_buffer_load_b128(rcb, i < cn4 ? 16 * (hb * cn4 + i) : kOOB, 0, 0));
     }
 #pragma unroll
     for (int k = 0; k < QK; ++k) {
-      const int i = threadIdx.x + kRagThreads * k, sl = i / QR4;
+      const int i = tx + kRagThreads * k, sl = i / QR4;
       const int src = (i < SLOTS * QR4 && sl < a.grp) ? 16 * ((hb * a.grp + sl) * QR4 + i % QR4) : kOOB;
       v.q[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, src, 0, 0));
     }
   };
   auto stage_store = [&](const StageRegs& v) {
+    int tx = threadIdx.x;
+    asm volatile("" : "+v"(tx));
 #pragma unroll
     for (int k = 0; k < kStage4; ++k) {
-      const int i = threadIdx.x + kRagThreads * k;
+      const int i = tx + kRagThreads * k;
       if (i < cn4) *reinterpret_cast<float4*>(cb_s + rag_cb_index<GS>(i / CR4, i % CR4)) = v.cb[k];
     }
 #pragma unroll
     for (int k = 0; k < QK; ++k) {
-      const int i = threadIdx.x + kRagThreads * k;
+      const int i = tx + kRagThreads * k;
       if (i < SLOTS * QR4) *reinterpret_cast<float4*>(q_s + (i / QR4) * QS + 4 * (i % QR4)) = v.q[k];
     }
   };
