@@ -1959,12 +1959,16 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
     g.c16 = r.c16;
     const bool row_ok = (g.page_off | g.th_off | g.rad_off) >= 0;
     const uint32_t po = g.page_off, tho = g.th_off, ro = g.rad_off;
-    auto in_pool = [&](uint32_t o) { return row_ok && o < pb ? (int)o : kOOB; };
+    // the page's reads go through a resource of the pool's size (of none for
+    // a bad row), so an offset past the pool reads zero by the buffer range
+    // check alone, with no per-load select (the offsets, below 2^31 plus a
+    // few KB, do not wrap)
+    const rsrc_t rsp = make_rsrc(a.pages, row_ok ? (int64_t)pb : 0);
     auto dword_at = [&](uint32_t o4) {
-      const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rs, in_pool(o4), 0, 0);
+      const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(rsp, (int)o4, 0, 0);
       return w | (row_ok && o4 == tail4 ? tailw : 0u);  // the partial dword itself reads as zero
     };
-    g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(po + 1), 0, 0);
+    g.cnt = __builtin_amdgcn_raw_buffer_load_b8(rsp, (int)(po + 1), 0, 0);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int gg = k ? gj : gi;
@@ -1972,7 +1976,7 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
       const uint32_t o4 = (tho & ~3u) + 4u * (x >> 5);
       g.cw[k][0] = dword_at(o4);
       g.cw[k][1] = dword_at(o4 + 4);
-      g.rc[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rs, in_pool(ro + (uint32_t)(ts * G + gg)), 0, 0);
+      g.rc[k] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rsp, (int)(ro + (uint32_t)(ts * G + gg)), 0, 0);
       const uint32_t s4 = (po + kHeaderBytes + 4 * gg) & ~3u;
       g.sw[k][0] = dword_at(s4);
       g.sw[k][1] = dword_at(s4 + 4);

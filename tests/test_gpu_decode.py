@@ -242,21 +242,12 @@ def test_ragged_logits_matches_oracle(gpu, ctx):
         assert max_err(got[fin], want[fin]) < 2e-4
 
 
-@pytest.mark.parametrize("tid,page_size,dh,grp,num_kv", [
-    (1, 128, 128, 4, 2), (3, 128, 128, 4, 2), (3, 16, 128, 4, 2), (2, 128, 64, 4, 2), (1, 16, 128, 8, 2),
-    (3, 32, 64, 6, 2), (2, 48, 128, 1, 2), (1, 16, 64, 3, 2), (1, 24, 128, 4, 2), (2, 128, 128, 9, 2),
-    (1, 16, 128, 8, 9), (2, 32, 64, 5, 11)])
-def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, grp, num_kv):
-    # the reference's call shape: PAGE_SIZE = 128 pages (config.py:4,
-    # spherical_kv_pipeline.py:1109-1125) and tier-3 decode pages (:1900-1910);
-    # pages laid out back to back as _build_per_head_pages does (:1198-1213).
-    # page_size 24 and grp 9 take the general kernel; 9 heads x grp 8 at dh
-    # 128 (q 36 KB, over the LDS budget) the one-chunk-per-wave form; the rest
-    # the pipeline (11 heads: codebooks restaged at each head change).
-    import fused_decode
+def _reference_layout_case(tid, page_size, dh, grp, num_kv, L=300):
+    """Pages of num_kv heads laid out back to back as _build_per_head_pages
+    does (spherical_kv_pipeline.py:1198-1213), one masked token in each head's
+    first page; returns the fused_decode_ragged inputs as numpy arrays."""
     from oracle import paging
     rng = np.random.default_rng(700 + tid + page_size + dh + grp + num_kv)
-    L = 300
     g, b = fmt.TIER_GEOMETRY[tid]
     G = dh // g
     cbs = synth.make_codebooks(rng, num_kv, dh, [tid])[tid]
@@ -279,23 +270,78 @@ def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, gr
             heads.append(h)
         ptab.append(rows)
         base += sum(x.size for x in buf[len(buf) - len(counts):])
-    pages = np.concatenate(buf)
-    ptable = np.concatenate(ptab).astype(np.int32)
-    heads = np.asarray(heads, np.int32)
-    pos = np.concatenate(pos).astype(np.int32)
     cos_t, sin_t = fmt.rope_tables(4100, dh, 500000.0)
-    q = rng.standard_normal((num_kv * grp, dh)).astype(np.float32)
-    cb = cbs.reshape(num_kv * G, 2 ** b, g)
-    log(f"ragged tier {tid}, page_size {page_size}, dh {dh}, grp {grp}: {ptable.shape[0]} pages")
+    return dict(pages=np.concatenate(buf), ptable=np.concatenate(ptab).astype(np.int32),
+                heads=np.asarray(heads, np.int32), pos=np.concatenate(pos).astype(np.int32), cos_t=cos_t,
+                sin_t=sin_t, q=rng.standard_normal((num_kv * grp, dh)).astype(np.float32),
+                cb=cbs.reshape(num_kv * G, 2 ** b, g), G=G, g=g, b=b)
+
+
+def _ragged_gpu(c, gpu, grp, num_kv, dh, page_size):
+    import fused_decode
     got = fused_decode.fused_decode_ragged(
-        torch.as_tensor(pages, device=gpu), torch.as_tensor(ptable, device=gpu), torch.as_tensor(heads, device=gpu),
-        torch.as_tensor(pos, device=gpu), torch.as_tensor(cos_t, device=gpu), torch.as_tensor(sin_t, device=gpu),
-        torch.as_tensor(q, device=gpu), grp, num_kv, torch.as_tensor(cb, device=gpu), dh, G, g, b, page_size)
+        torch.as_tensor(c["pages"], device=gpu), torch.as_tensor(c["ptable"], device=gpu),
+        torch.as_tensor(c["heads"], device=gpu), torch.as_tensor(c["pos"], device=gpu),
+        torch.as_tensor(c["cos_t"], device=gpu), torch.as_tensor(c["sin_t"], device=gpu),
+        torch.as_tensor(c["q"], device=gpu), grp, num_kv, torch.as_tensor(c["cb"], device=gpu), dh, c["G"], c["g"],
+        c["b"], page_size)
     torch.cuda.synchronize()
-    want = oracle.ragged_logits(pages, ptable, heads, pos, cos_t, sin_t, q, grp, cb, dh, G, g, b, page_size)
-    got = got.cpu().numpy()
+    return got.cpu().numpy()
+
+
+@pytest.mark.parametrize("tid,page_size,dh,grp,num_kv", [
+    (1, 128, 128, 4, 2), (3, 128, 128, 4, 2), (3, 16, 128, 4, 2), (2, 128, 64, 4, 2), (1, 16, 128, 8, 2),
+    (3, 32, 64, 6, 2), (2, 48, 128, 1, 2), (1, 16, 64, 3, 2), (1, 24, 128, 4, 2), (2, 128, 128, 9, 2),
+    (1, 16, 128, 8, 9), (2, 32, 64, 5, 11)])
+def test_ragged_logits_reference_page_size_and_tier3(gpu, tid, page_size, dh, grp, num_kv):
+    # the reference's call shape: PAGE_SIZE = 128 pages (config.py:4,
+    # spherical_kv_pipeline.py:1109-1125) and tier-3 decode pages (:1900-1910);
+    # page_size 24 and grp 9 take the general kernel; 9 heads x grp 8 at dh
+    # 128 (q 36 KB, over the LDS budget) the one-chunk-per-wave form; the rest
+    # the pipeline (11 heads: codebooks restaged at each head change).  The
+    # pools' byte sizes are not multiples of 4 (the last dword is partial).
+    L = 300
+    c = _reference_layout_case(tid, page_size, dh, grp, num_kv, L)
+    log(f"ragged tier {tid}, page_size {page_size}, dh {dh}, grp {grp}: {c['ptable'].shape[0]} pages, "
+        f"pool {c['pages'].size} bytes")
+    got = _ragged_gpu(c, gpu, grp, num_kv, dh, page_size)
+    want = oracle.ragged_logits(c["pages"], c["ptable"], c["heads"], c["pos"], c["cos_t"], c["sin_t"], c["q"], grp,
+                                c["cb"], dh, c["G"], c["g"], c["b"], page_size)
     fin = np.isfinite(want)
     assert fin.sum() == num_kv * (L - 1) * grp                  # every token but the masked ones
+    assert (np.isneginf(got) == ~fin).all()
+    assert max_err(got[fin], want[fin]) < 2e-4
+
+
+@pytest.mark.parametrize("tid,page_size,dh,grp,num_kv", [(1, 16, 128, 4, 2), (2, 16, 64, 4, 3), (3, 128, 128, 4, 2),
+                                                          (1, 24, 128, 4, 2)])
+def test_ragged_logits_malformed_rows_contribute_nothing(gpu, tid, page_size, dh, grp, num_kv):
+    # pointer-table rows with a negative offset, a page past the pool's end,
+    # sections past it, or a head id out of range: every slot of such a page
+    # is -inf and every other page's logits are unchanged
+    c = _reference_layout_case(tid, page_size, dh, grp, num_kv)
+    P = c["ptable"].shape[0]
+    bad = {1: "neg_page", 2: "neg_theta", P // 2: "page_past_end", P // 2 + 1: "sections_past_end",
+           P - 2: "head_out_of_range"}
+    want = oracle.ragged_logits(c["pages"], c["ptable"], c["heads"], c["pos"], c["cos_t"], c["sin_t"], c["q"], grp,
+                                c["cb"], dh, c["G"], c["g"], c["b"], page_size)
+    pt, hd = c["ptable"].copy(), c["heads"].copy()
+    nb = c["pages"].size
+    for p, kind in bad.items():
+        if kind == "neg_page":
+            pt[p, 0] = -16
+        elif kind == "neg_theta":
+            pt[p, 1] = -1
+        elif kind == "page_past_end":
+            pt[p] = (nb + 64, nb + 64 + 8 + 4 * c["G"], nb + 64 + 200)
+        elif kind == "sections_past_end":
+            pt[p, 1:] = (nb + 8, nb + 400)
+        else:
+            hd[p] = num_kv + 3
+        want[:, p * page_size:(p + 1) * page_size] = -np.inf
+    log(f"ragged malformed rows: tier {tid}, page_size {page_size}, dh {dh}, {P} pages, bad {sorted(bad)}")
+    got = _ragged_gpu(dict(c, ptable=pt, heads=hd), gpu, grp, num_kv, dh, page_size)
+    fin = np.isfinite(want)
     assert (np.isneginf(got) == ~fin).all()
     assert max_err(got[fin], want[fin]) < 2e-4
 
