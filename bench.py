@@ -118,7 +118,11 @@ ENCODE_TRAFFIC_BYTES = {3: 55598602}
 # tiers' ragged_pipe_kernel launches; profiles/ragged_config2_hbm_traffic.txt),
 # FETCH_SIZE * 2 + WRITE_SIZE as above.
 MODEA_TRAFFIC_BYTES = {16: 80479122}
-RAGGED_TRAFFIC_BYTES = {"fit": 13703189, "table": 47988605}   # phases in the kernel / table rows read
+RAGGED_TRAFFIC_BYTES = {"fit": 13673909, "table": 47988605}   # phases in the kernel / table rows read
+# VALU instructions (MFMA included) of both ragged launches of a step with
+# fitted tables, SQ_INSTS_VALU from the same profile; the VALU-issue bound as
+# for the encode above.
+RAGGED_VALU_INSTS = {"fit": 7574181}
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
@@ -486,7 +490,12 @@ def bench_ragged(args, dev):
                      "kernel_us": round(ms * 1e3, 3),
                      "frac_of": "both tiers' launches back to back (HIP events around the step); algorithmic bytes",
                      "traffic_of": "both launches, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
-                                   "(profiles/ragged_config2_hbm_traffic.txt)"},
+                                   "(profiles/ragged_config2_hbm_traffic.txt)",
+                     **({} if not model else {
+                         "valu_bound_us": round(RAGGED_VALU_INSTS["fit"] * 4 / SIMDS / CLOCK_HZ * 1e6, 2),
+                         "valu_frac": round(RAGGED_VALU_INSTS["fit"] * 4 / SIMDS / CLOCK_HZ / ms * 1e3, 4),
+                         "valu_of": "SQ_INSTS_VALU of both launches (profiles/ragged_config2_hbm_traffic.txt) at "
+                                    "one wave64 instruction per 4 cycles on 1024 SIMDs, 2.4 GHz"})},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
