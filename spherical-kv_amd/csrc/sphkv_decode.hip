@@ -1084,6 +1084,7 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   __shared__ int tc[NS][G3];               // tail codes
   __shared__ int tp[NS];                   // tail positions
   __shared__ float sims[G3][8];
+  __shared__ __attribute__((aligned(16))) float dirs[G3][32];   // the new token's directions
   __shared__ float4 red_v[IL][COLS];
   __shared__ float red_m[IL][COLS], red_l[IL][COLS];
   __shared__ float scl[G3];
@@ -1211,10 +1212,30 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
     // the new token through the tier-3 codebook (_encode_keys_with_codebooks
     // on one token, torch CPU order; N*g*C = 256 < 400 takes ATen's naive
     // loop: multiply, then add, in order)
+    // The 32 divisions of a group are shared by its 8 lanes (lane ec: values
+    // 4 ec .. 4 ec + 3; each quotient is the same correctly rounded one
+    // whichever lane forms it) and exchanged through LDS, so the chain on
+    // the step's critical path holds 4 divisions instead of 32.
     float r_enc = 0.f;
     if (enc_lane) {
       r_enc = torch_norm(x, 32);
-      group_directions<32>(x, __fadd_rn(r_enc, 1e-8f), !t.k_is_fp32, x);    // x becomes dir
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = x[e];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) v[e] = ec == k ? x[4 * k + e] : v[e];
+      }
+      group_directions<4>(v, __fadd_rn(r_enc, 1e-8f), !t.k_is_fp32, v);
+      *reinterpret_cast<float4*>(&dirs[eg][4 * ec]) = float4{v[0], v[1], v[2], v[3]};
+    }
+    wave_lds_sync();
+    if (enc_lane) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float4 d4 = *reinterpret_cast<const float4*>(&dirs[eg][4 * k]);
+        x[4 * k] = d4.x; x[4 * k + 1] = d4.y; x[4 * k + 2] = d4.z; x[4 * k + 3] = d4.w;
+      }
       float sm = 0.f;
 #pragma unroll
       for (int k = 0; k < 32; ++k) sm = __fadd_rn(sm, __fmul_rn(x[k], crow[k]));
