@@ -683,7 +683,8 @@ class DecodeTail:
 
     def runner(self):
         """The fastest call of a step: fn(q_ptr, k_ptr, k_is_fp32, v_ptr, pos_ptr, out_ptr, mode) with raw
-        device addresses (mode 1 decode, 2 append, 3 both) on the current stream; one ctypes call."""
+        device addresses (mode 1 decode, 2 append, 3 both) on the stream current when runner() is called;
+        one ctypes call, no checks of the inputs."""
         run, stream, owner = self._run, _stream(), self
 
         def fn(q, k, k32, v, pos, out, mode):
