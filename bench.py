@@ -818,7 +818,10 @@ def main():
     gbps = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] {us:.2f} us/step  {gbps:.1f} GB/s  ({gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s); "
         f"host {host_us:.2f} us per call to enqueue")
-    # host cost of the checked Python call, for comparison (enqueue only)
+    # host cost of the checked Python call, for comparison (enqueue only;
+    # a few untimed calls first, so one-time costs stay out of short runs)
+    for i in range(10):
+        ops.decode_paged(pools[i % R], q, wl.gqa, wl.rope_theta, out=out, workspace=ws)
     torch.cuda.synchronize()
     h0 = time.perf_counter()
     for i in range(args.steps):
