@@ -1876,7 +1876,7 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
   // the same 1/NX of the positions of every head, so its L2 holds 1/NX of
   // the cos / sin rows (table path) and a workgroup's run mostly stays in
   // one head (one codebook stage).  Its segments, concatenated, are cut into
-  // GPX equal runs, one per workgroup.  Any order of pages is still covered
+  // GPX runs, one per workgroup (below).  Any order of pages is still covered
   // exactly once.  Lane k < K holds segment k's list range and chunk offset;
   // a list position maps to a chunk by a ballot over that table.
   const int NX = (gridDim.x % 8 == 0 && gridDim.x >= 64) ? 8 : 1;
@@ -1900,8 +1900,24 @@ __global__ __launch_bounds__(kRagThreads) void ragged_pipe_kernel(RaggedLaunch a
     seg_base = b0 - (incl - len);
   }
   const int Lx = __builtin_amdgcn_readlane(seg_end, K - 1);
-  const int q0 = (int)((uint32_t)wj * (uint32_t)Lx / (uint32_t)GPX);      // wj < 128, Lx < 2^25
-  const int q1 = (int)((uint32_t)(wj + 1) * (uint32_t)Lx / (uint32_t)GPX);
+  // Workgroups start over several microseconds (the dispatcher places them
+  // one after another: the 768 workgroups of 4 waves of a config-2 call
+  // start over 4.7 us), and a workgroup dispatched late with an equal share
+  // finishes late.  So the XCD's iterations (kRagWaves chunks each) are cut
+  // at whole iterations with shares that fall linearly in dispatch order:
+  // workgroup wj's run ends at F(x) = x + alpha x (1 - x) of them, x =
+  // (wj + 1) / GPX; alpha grows with the grid (the spread) and shrinks with
+  // the iterations per workgroup (the work that absorbs it): 2.4e-3 per
+  // workgroup of the grid over the mean iterations, at most 0.9.
+  const int itot = (Lx + kRagWaves - 1) / kRagWaves;
+  const float alpha = fminf(0.9f, 2.4e-3f * (float)gridDim.x * (float)GPX / (float)max(itot, GPX));
+  auto cut = [&](int w) {                              // list position where workgroup w's run starts
+    if (w >= GPX) return Lx;
+    const float x = (float)w / (float)GPX;
+    const int c = (int)__builtin_rintf((x + alpha * x * (1.f - x)) * (float)itot);   // itot < 2^23
+    return min(kRagWaves * min(max(c, 0), itot), Lx);
+  };
+  const int q0 = cut(wj), q1 = cut(wj + 1);
   const int it1 = (q1 - q0 + kRagWaves - 1) / kRagWaves;
   if (it1 == 0) return;                                // whole workgroup
   auto chunk_of = [&](int q) {                         // list position (< Lx) -> chunk index
