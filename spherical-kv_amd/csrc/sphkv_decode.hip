@@ -449,6 +449,57 @@ __device__ __forceinline__ void set_prio(int lvl) {
 
 template <bool B> struct Flag { static constexpr bool value = B; };
 
+// The step's new pre-RoPE key through the tier-3 codebook as one token
+// (_encode_keys_with_codebooks on kn.unsqueeze(0), spherical_kv_pipeline.py:
+// 2311-2313), bit-exact with torch CPU: N*g*C = 256 < 400 takes ATen's naive
+// loop (multiply, then add, in order).  One wave; lane (eg = lane >> 3, ec =
+// lane & 7) with eg < G3 (enc) holds group eg's 32 key values in x; crow
+// points at centroid ec's row (registers or LDS).  The 32 divisions of a group are shared by its 8
+// lanes (lane ec forms values 4 ec .. 4 ec + 3; each quotient is the same
+// correctly rounded one whichever lane forms it) and exchanged through LDS
+// (dirs [G3][32], sims [G3][8]).  Lanes with ec == 0 return the group's
+// radius and first-maximum code (torch.argmax: the ascending scan with '>').
+__device__ __forceinline__ void encode_new_token(float (&x)[32], const float* crow, int eg, int ec, bool enc,
+                                                 bool fp16_in, float (*dirs)[32], float (*sims)[8], float& r_out,
+                                                 int& code_out) {
+  float r_enc = 0.f;
+  if (enc) {
+    r_enc = torch_norm(x, 32);
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = x[e];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) v[e] = ec == k ? x[4 * k + e] : v[e];
+    }
+    group_directions<4>(v, __fadd_rn(r_enc, 1e-8f), fp16_in, v);
+    *reinterpret_cast<float4*>(&dirs[eg][4 * ec]) = float4{v[0], v[1], v[2], v[3]};
+  }
+  wave_lds_sync();
+  if (enc) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 d4 = *reinterpret_cast<const float4*>(&dirs[eg][4 * k]);
+      x[4 * k] = d4.x; x[4 * k + 1] = d4.y; x[4 * k + 2] = d4.z; x[4 * k + 3] = d4.w;
+    }
+    float sm = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) sm = __fadd_rn(sm, __fmul_rn(x[k], crow[k]));
+    sims[eg][ec] = sm;
+  }
+  wave_lds_sync();
+  int best = 0;
+  if (enc && ec == 0) {
+    float bs = sims[eg][0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k)
+      if (sims[eg][k] > bs) { bs = sims[eg][k]; best = k; }
+  }
+  r_out = r_enc;
+  code_out = best;
+}
+
+
 template <int DH, int GQA>
 __global__ __launch_bounds__(decode_waves<GQA>() * 64)
 __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() / 4))) void decode_kernel(
@@ -472,16 +523,19 @@ __attribute__((amdgpu_waves_per_eu(decode_waves<GQA>() / 4, decode_waves<GQA>() 
   // the work list comes from the caller: an item naming no (seq, head) is
   // empty, rows are clamped to the table and the stride to [1, num_rows]
   // (so no row index below overflows and the page loop is bounded)
-  const int32_t* wi = work + 4 * item;
-  const bool item_ok = wi[0] >= 0 && wi[0] < a.num_sh;
-  const int sh = item_ok ? wi[0] : 0;
-  const int rb = max(wi[1], 0);
-  const int re = item_ok ? min(wi[2], a.num_rows) : 0;
-  const int rstride = min(max(wi[3], 1), max(a.num_rows, 1));   // rows between consecutive pages of the item
+  // One 16-byte scalar load of the item and branch-free clamps: a load or a
+  // division under a condition becomes a branch, and every kernel-argument
+  // load after it then waits for the item first (serial round trips).
+  const int4 wi = *reinterpret_cast<const int4*>(work + 4 * item);
+  const bool item_ok = wi.x >= 0 && wi.x < a.num_sh;
+  const int sh = item_ok ? wi.x : 0;
+  const int rb = max(wi.y, 0);
+  const int re = item_ok ? min(wi.z, a.num_rows) : 0;
+  const int rstride = min(max(wi.w, 1), max(a.num_rows, 1));   // rows between consecutive pages of the item
   const int wstride = kWaves * rstride;                // rows between consecutive pages of a wave
   // pages of this wave (rows rb + rstride (wave + kWaves k) < re)
-  const int npg = re > rb ? (re - rb + rstride - 1) / rstride : 0;
-  const int nwp = npg > wave ? (npg - wave + kWaves - 1) / kWaves : 0;
+  const int npg = (max(re - rb, 0) + rstride - 1) / rstride;
+  const int nwp = max(npg - wave + kWaves - 1, 0) / kWaves;
   const int h = sh % a.num_kv;
   const int seq = sh / a.num_kv;
   const int t = lane & 15;
@@ -1209,46 +1263,12 @@ __global__ __launch_bounds__(kTailThreads) void decode_tail_kernel(DecodeArgs a,
   if (i < NS - 1) tp[i] = sp;
   if (i == 0) tp[NS - 1] = pos_new;
   if (wave == 3) {
-    // the new token through the tier-3 codebook (_encode_keys_with_codebooks
-    // on one token, torch CPU order; N*g*C = 256 < 400 takes ATen's naive
-    // loop: multiply, then add, in order)
-    // The 32 divisions of a group are shared by its 8 lanes (lane ec: values
-    // 4 ec .. 4 ec + 3; each quotient is the same correctly rounded one
-    // whichever lane forms it) and exchanged through LDS, so the chain on
-    // the step's critical path holds 4 divisions instead of 32.
-    float r_enc = 0.f;
-    if (enc_lane) {
-      r_enc = torch_norm(x, 32);
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = x[e];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) v[e] = ec == k ? x[4 * k + e] : v[e];
-      }
-      group_directions<4>(v, __fadd_rn(r_enc, 1e-8f), !t.k_is_fp32, v);
-      *reinterpret_cast<float4*>(&dirs[eg][4 * ec]) = float4{v[0], v[1], v[2], v[3]};
-    }
-    wave_lds_sync();
-    if (enc_lane) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float4 d4 = *reinterpret_cast<const float4*>(&dirs[eg][4 * k]);
-        x[4 * k] = d4.x; x[4 * k + 1] = d4.y; x[4 * k + 2] = d4.z; x[4 * k + 3] = d4.w;
-      }
-      float sm = 0.f;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) sm = __fadd_rn(sm, __fmul_rn(x[k], crow[k]));
-      sims[eg][ec] = sm;
-    }
-    wave_lds_sync();
+    // the new token's encode (encode_new_token; its chain of divisions is
+    // shared by each group's 8 lanes)
+    float r_enc;
+    int best;
+    encode_new_token(x, crow, eg, ec, enc_lane, !t.k_is_fp32, dirs, sims, r_enc, best);
     if (enc_lane && ec == 0) {
-      // first maximum: the ascending scan with '>' (torch.argmax)
-      int best = 0;
-      float bs = sims[eg][0];
-#pragma unroll
-      for (int k = 1; k < 8; ++k)
-        if (sims[eg][k] > bs) { bs = sims[eg][k]; best = k; }
       tr[NS - 1][eg] = r_enc;
       tc[NS - 1][eg] = best;
     }

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle
+import sphkv_format as fmt
 import sphkv_ops as ops
 import sphkv_synth as synth
 from gpu_helpers import log, max_err, pool_from_oracle
@@ -123,6 +124,100 @@ def test_decode_step_matches_oracle(gpu, config, ctx, seqs):
     torch.cuda.synchronize()
     _check_state(wl, pool, tail, orc)
     log(f"  worst {worst:.3e}")
+
+
+@pytest.mark.parametrize("dh,gqa", [(128, 4), (64, 2), (128, 1), (64, 8)])
+def test_decode_step_empty_head_and_shapes(gpu, dh, gqa):
+    # Head 1 has no context pages: its one work item is empty (its partial
+    # holds no token); head 0 holds one token, head 2 a mix of every tier,
+    # head 3 dense tokens.  Steps cross a flush, so the decode page joins
+    # head 1's empty item.
+    rng = np.random.default_rng(5)
+    num_kv, L, steps = 4, 40, 18
+    Ls = [1, 0, 17, 33]
+    tier_of = []
+    for h, n in enumerate(Ls):
+        t = np.zeros(L, np.int32)
+        if h == 2:
+            t[:n] = rng.choice(np.array([1, 2, 3, fmt.DENSE_TIER_ID], np.int32), size=n)
+        elif h == 3:
+            t[:n] = fmt.DENSE_TIER_ID
+        else:
+            t[:n] = 1
+        tier_of.append(t)
+    cbs = synth.make_codebooks(rng, num_kv, dh, [1, 2, 3])
+    K = [(rng.standard_normal((num_kv, L, dh)) * 2).astype(np.float16)]
+    V = [rng.standard_normal((num_kv, L, dh)).astype(np.float16)]
+    q = (rng.standard_normal((1, num_kv * gqa, dh)) * 2).astype(np.float16)
+    pos = [np.sort(rng.choice(120000, size=L, replace=False))]
+    plan = fmt.plan_pages(tier_of, pos, 1, num_kv, dh, 16, rng=rng)
+    wl = synth.Workload(name="edge", dh=dh, num_kv=num_kv, gqa=gqa, num_seqs=1, lengths=[L],
+                        rope_theta=5e5, codebooks=cbs, K=K, V=V, q=q, tier_of=tier_of, plan=plan, positions=pos)
+    st = synth.make_tail_steps(wl, steps)
+    wl.codebooks[3] = st.cb3
+    pool, cpu = pool_from_oracle(wl, gpu)
+    tail = ops.DecodeTail(pool, wl.gqa, wl.rope_theta, capacity=2)
+    orc = TailOracle(wl.num_seqs, wl.num_kv, wl.dh, st.cb3)
+    ws, w = tail.work_start.cpu().numpy(), tail.work.cpu().numpy()
+    assert ws[2] - ws[1] == 1 and w[ws[1], 1] == w[ws[1], 2], "head 1: one empty work item"
+    log(f"decode step, empty head: dh={dh} gqa={gqa} items={tail.num_items}")
+    for t in range(steps):
+        qt, k, v, p = st.q[t], st.k[t], st.v[t], st.pos[t]
+        out = ops.decode_step(pool, tail, _dev(qt, gpu), _dev(k, gpu), _dev(v, gpu), _dev(p, gpu))
+        if t in (0, 1, 15, 16, 17):
+            got = out.float().cpu().numpy()
+            want = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, qt, wl.gqa, wl.rope_theta, tail=orc,
+                                        k_new=k, v_new=v, cur_pos=p)
+            err = max_err(got, want)
+            log(f"  step {t}: staged {len(orc.staged[0])}, decode pages {len(orc.pages[0])}, max abs err {err:.3e}")
+            assert err <= TOL
+        for h in range(wl.num_kv):
+            orc.append(0, h, k[0, h], v[0, h], int(p[0]))
+    torch.cuda.synchronize()
+    _check_state(wl, pool, tail, orc)
+
+
+def test_decode_step_caller_list_without_item(gpu):
+    # A caller's work list may give a (seq, head) no item at all: head 0's
+    # output is then its staged tokens and new token alone (the tail kernel's
+    # merge has no item partial for it), the other heads see their context as
+    # well.  Unbound sphkv_decode_step, no append.
+    import ctypes
+    wl, st, pool, cpu, tail, orc = _setup(gpu, config=1, ctx=256, steps=6, capacity=1)
+    for t in range(5):
+        ops.decode_append(pool, tail, _dev(st.k[t], gpu), _dev(st.v[t], gpu), _dev(st.pos[t], gpu))
+        for h in range(wl.num_kv):
+            orc.append(0, h, st.k[t][0, h], st.v[t][0, h], int(st.pos[t][0]))
+    torch.cuda.synchronize()
+    ws, w = tail.work_start.cpu().numpy(), tail.work.cpu().numpy()
+    w2 = np.ascontiguousarray(w[ws[1]:])                  # sh 0's items removed
+    ws2 = np.concatenate([[0], ws[1:] - ws[1]]).astype(np.int32)
+    w2d, ws2d = _dev(w2, gpu), _dev(ws2, gpu)
+    n2 = int(w2.shape[0])
+    lib = ops.load()
+    nbytes = int(lib.sphkv_decode_paged_workspace_bytes(n2, wl.gqa, wl.dh))
+    wsp = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    q, k, v, p = st.q[5], st.k[5], st.v[5], st.pos[5]
+    qd, kd, vd, pd = (_dev(x, gpu) for x in (q, k, v, p))
+    out = torch.empty_like(qd)
+    c1, c2, c3 = pool.cb_ptrs()
+    parity = tail.counts()[2]
+    rc = lib.sphkv_decode_step(
+        pool.pages.data_ptr(), tail.pages_bytes, tail.ptable.data_ptr(), tail.vslot.data_ptr(),
+        tail.positions.data_ptr(), tail.num_rows, pool.v_pool.data_ptr(), tail.num_vpages, c1, c2, c3,
+        w2d.data_ptr(), n2, ws2d.data_ptr(), wl.num_seqs, wl.num_kv, wl.gqa, qd.data_ptr(), kd.data_ptr(), 0,
+        vd.data_ptr(), pd.data_ptr(), tail.stg_r.data_ptr(), tail.stg_code.data_ptr(), tail.stg_v.data_ptr(),
+        tail.stg_pos.data_ptr(), tail.state.data_ptr(), tail.dec_byte0, tail.dec_vpage0, tail.capacity, 0, parity,
+        out.data_ptr(), wsp.data_ptr(), nbytes, wl.dh, 16, ctypes.c_float(tail.sm_scale), wl.rope_theta,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    ops.check(rc, "sphkv_decode_step")
+    got = out.float().cpu().numpy()
+    ctx_out, ctx_lse = oracle.decode_mode_b(cpu, wl.plan, wl.codebooks, q, wl.gqa, wl.rope_theta, return_lse=True)
+    ctx_lse[:, :wl.gqa] = -np.inf                         # head 0: no context
+    want = step_with_context(ctx_out, ctx_lse, orc, q, wl.gqa, wl.rope_theta, k, v, p)
+    err = max_err(got, want)
+    log(f"caller list without sh 0's item: max abs err {err:.3e}")
+    assert err <= TOL
 
 
 def test_decode_step_full_config2(gpu):
