@@ -263,9 +263,16 @@ def mode_b_logits(q: np.ndarray, pos: np.ndarray, cos_t: np.ndarray, sin_t: np.n
 
 def decode_mode_b(pool: Dict[str, np.ndarray], plan, codebooks: Dict[int, np.ndarray],
                   q: np.ndarray, gqa: int, rope_theta: float, return_lse: bool = False,
-                  tail=None, k_new=None, v_new=None, cur_pos=None):
+                  tail=None, k_new=None, v_new=None, cur_pos=None, r_exact: Optional[np.ndarray] = None):
     """fp64 Mode-B decode over a placed pool.  q [num_seqs, num_kv*gqa, dh]
     (fp16 values).  Returns out [num_seqs, num_kv*gqa, dh] fp64.
+
+    Compressed pages are scored on the page-decoded radius r_hat = code / 127
+    * r_scale (the parity definition).  r_exact [P, ps, Gmax] (build_pool's
+    "r": the encoder's fp32 radii) scores them on the unquantised radii
+    instead, as the reference's torch path does (K_tier's fp32 radii,
+    spherical_kv_pipeline.py:2137, 2175-2176): the gap between the two is the
+    format's error, not a kernel's.
 
     tail (oracle.tail.TailOracle): adds each (seq, head)'s decode pages and
     staged tokens, and with k_new / v_new [num_seqs, num_kv, dh], cur_pos
@@ -295,6 +302,8 @@ def decode_mode_b(pool: Dict[str, np.ndarray], plan, codebooks: Dict[int, np.nda
                 g, _ = TIER_GEOMETRY[tid]
                 G = dh // g
                 codes, r_hat = unpack_page(pages, plan.ptable[p], tid, n, dh)
+                if r_exact is not None:
+                    r_hat = r_exact[p, :n, :G].astype(np.float64)
                 cb = codebooks[tid][h].astype(np.float64)                  # [G, C, g]
                 cw = cb[np.arange(G)[None, :], codes]                       # [n, G, g]
                 logits.append(mode_b_logits(qh, pos, cos_t, sin_t, cw, r_hat, None, G, g))

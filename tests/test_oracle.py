@@ -238,6 +238,41 @@ def test_decode_oracle_matches_torch_golden():
         assert np.abs(out - z[name + "__out"]).max() < 2e-5
 
 
+@pytest.mark.parametrize("config, ctx", [(1, 4096), (2, 4096)])
+def test_radius_format_error(config, ctx):
+    # The parity definition scores compressed pages on the page-decoded radius
+    # r_hat = code / 127 * r_scale; the reference's torch path scores its
+    # fp32 radii (spherical_kv_pipeline.py:2137, 2175-2176).  Their gap is the
+    # format's error, reported here apart from any kernel's error.
+    wl = synth.make_decode_workload(config, ctx_override=ctx)
+    pool = oracle.build_pool(wl, with_codes=True)
+    plan, dh = wl.plan, wl.dh
+    args = (pool, plan, wl.codebooks, wl.q, wl.gqa, wl.rope_theta)
+    o_hat = oracle.decode_mode_b(*args)
+    o_r = oracle.decode_mode_b(*args, r_exact=pool["r"])
+    # r_exact replaces r_hat: passing r_hat itself reproduces the default
+    r_hat_all = np.zeros(pool["r"].shape, np.float64)
+    for p in range(plan.num_rows):
+        tid, n = int(plan.tier[p]), int(plan.count[p])
+        if tid != fmt.DENSE_TIER_ID:
+            G = dh // fmt.TIER_GEOMETRY[tid][0]
+            r_hat_all[p, :n, :G] = oracle.unpack_page(pool["pages"], plan.ptable[p], tid, n, dh)[1]
+    assert np.array_equal(oracle.decode_mode_b(*args, r_exact=r_hat_all), o_hat)
+    gap = np.abs(o_r - o_hat).max()
+    assert gap > 0
+    # bound: |r - r_hat| <= scale / 254 per group, and |<q_g, c>| <= ||q_g||
+    # for unit centroids (sum over groups <= sqrt(G) ||q||), so every logit
+    # moves by at most delta; softmax weights then move by a factor within
+    # e^(+-2 delta), so |d out| <= (e^(2 delta) - 1) max |V|
+    scale_max = max(float(np.abs(pool["r"][p]).max()) for p in range(plan.num_rows))
+    qn = np.linalg.norm(wl.q.astype(np.float64), axis=-1).max()
+    delta = math.sqrt(dh // 16) * qn * scale_max / 254 / math.sqrt(dh)
+    vmax = max(float(np.abs(v.astype(np.float64)).max()) for v in wl.V)
+    assert gap <= (math.exp(2 * delta) - 1) * vmax
+    print(f"config {config} ctx {ctx}: max |out(r) - out(r_hat)| = {gap:.3e} "
+          f"(mean {np.abs(o_r - o_hat).mean():.3e}; bound {(math.exp(2 * delta) - 1) * vmax:.3e})")
+
+
 def test_unpack_page_round_trip():
     wl = synth.make_decode_workload(2, ctx_override=400)
     pool = oracle.build_pool(wl, with_codes=True)
