@@ -131,6 +131,12 @@ def measured_traffic(config, layout):
     return None if v is None else int(v)
 
 
+def counter_gbps(config, layout, kern_ms):
+    """The counters' HBM bytes per launch over the live kernel time (GB/s)."""
+    v = measured_traffic(config, layout)
+    return None if v is None or kern_ms <= 0 else round(v / (kern_ms * 1e-3) / 1e9, 1)
+
+
 def host_cpu() -> dict:
     """The host CPU this process runs on: model name, logical CPUs of the
     machine, CPUs in this process's affinity mask, the cgroup CPU quota (if
@@ -720,12 +726,14 @@ def bench_step(args, dev):
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": measured_traffic(args.config, args.layout),
+                     "traffic_gbps": counter_gbps(args.config, args.layout, kern_ms),
                      "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
                      "frac_of": "decode_kernel alone (the step's dominant kernel), kernel-only start / stop "
                                 "timestamps of each launch (hipExtLaunchKernel); algorithmic bytes of its launch "
                                 "(pages, dense K, V, positions, pointer-table rows)",
                      "traffic_of": "decode_kernel launch, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
-                                   "(profiles/decode_config2_hbm_traffic.txt)",
+                                   "(profiles/decode_config2_hbm_traffic.txt); traffic_gbps: those bytes "
+                                   "over kernel_us",
                      "whole_step_achieved": round(gbps, 1),
                      "whole_step_frac": round(gbps / PEAK_HBM_GBPS, 4),
                      "whole_step_of": "the headline value: both kernels, HIP events around the steps; algorithmic "
@@ -873,11 +881,13 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": measured_traffic(args.config, args.layout),
+                     "traffic_gbps": counter_gbps(args.config, args.layout, kern_ms),
                      "kernel": "decode_kernel", "kernel_us": round(kern_ms * 1e3, 3),
                      "frac_of": "decode_kernel alone, HIP events around back-to-back launches (launch gap "
                                 "included); algorithmic bytes of its launch",
                      "traffic_of": "decode_kernel launch, rocprofv3 FETCH_SIZE x2 + WRITE_SIZE "
-                                   "(profiles/decode_config2_hbm_traffic.txt)",
+                                   "(profiles/decode_config2_hbm_traffic.txt); traffic_gbps: those bytes "
+                                   "over kernel_us",
                      "whole_step_achieved": round(gbps, 1),
                      "whole_step_frac": round(gbps / PEAK_HBM_GBPS, 4),
                      "whole_step_of": "the value: decode_kernel + decode_merge_kernel, HIP events around the steps"},
