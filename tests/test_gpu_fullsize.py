@@ -9,6 +9,12 @@ the device (sphkv_synth kv_device) and the pools encoded by the GPU encoder.
 Every output must be finite, no page may be reported malformed, and a seeded
 sample of (seq, kv head) pairs must match the fp64 oracle (pages and V
 bit-exact against the oracle's encode of that head, outputs within 2e-3).
+
+Every (seq, kv head), at full size, also meets a size-independent property:
+with q = 0 every logit is exactly 0 and every weight exactly 1, so each
+output is the plain mean of that head's V rows (a page or token dropped,
+doubled or mis-masked by the work split, the page loop or the merge moves
+it).
 """
 import numpy as np
 import pytest
@@ -19,6 +25,27 @@ import sphkv_synth as synth
 from gpu_helpers import check_sampled_heads, log
 
 pytestmark = pytest.mark.gpu
+
+
+def _mean_v_per_head(wl, pool):
+    """fp64 mean of each (seq, kv head)'s V rows, from the pool's V pages
+    (dim-major: token n of dim d at d * page_size + n) over the plan's rows."""
+    plan, dev, dh = wl.plan, pool.device, wl.dh
+    num_sh = wl.num_seqs * wl.num_kv
+    vs = torch.as_tensor(plan.vslot.astype(np.int64), device=dev)
+    cnt = torch.as_tensor(plan.count.astype(np.int64), device=dev)
+    shr = torch.as_tensor(plan.seq_head.astype(np.int64), device=dev)
+    tot = torch.zeros((num_sh, dh), dtype=torch.float64, device=dev)
+    tok = torch.zeros(num_sh, dtype=torch.float64, device=dev)
+    slot = torch.arange(plan.page_size, device=dev)
+    for a in range(0, plan.num_rows, 65536):
+        b = min(a + 65536, plan.num_rows)
+        v = pool.v_pool.index_select(0, vs[a:b]).view(b - a, dh, plan.page_size).double()
+        m = (slot[None, :] < cnt[a:b, None]).double()
+        tot.index_add_(0, shr[a:b], (v * m[:, None, :]).sum(-1))
+        tok.index_add_(0, shr[a:b], cnt[a:b].double())
+    assert bool((tok > 0).all())
+    return tot / tok[:, None]
 
 
 @pytest.mark.parametrize("config,heads", [(4, 16), (5, 6)])
@@ -36,3 +63,10 @@ def test_full_size_decode_matches_oracle_on_sampled_heads(gpu, config, heads):
     if config == 4:
         assert int(wl.plan.vslot.max()) >= (1 << 20)
     check_sampled_heads(wl, pool, out, heads, seed=100 + config)
+    log("  q = 0 on every head: outputs against each head's mean V row")
+    out0 = ops.decode_paged(pool, torch.zeros_like(q), wl.gqa, wl.rope_theta, check=True)
+    want = _mean_v_per_head(wl, pool).view(wl.num_seqs, wl.num_kv, 1, wl.dh)
+    want = want.expand(-1, -1, wl.gqa, -1).reshape(wl.num_seqs, wl.num_kv * wl.gqa, wl.dh)
+    err = float((out0.double() - want).abs().max())
+    log(f"  every head, q = 0: max abs err {err:.3e}")
+    assert err <= 1e-3
