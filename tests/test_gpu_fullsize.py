@@ -10,12 +10,19 @@ Every output must be finite, no page may be reported malformed, and a seeded
 sample of (seq, kv head) pairs must match the fp64 oracle (pages and V
 bit-exact against the oracle's encode of that head, outputs within 2e-3).
 
-Every (seq, kv head), at full size, also meets a size-independent property:
-with q = 0 every logit is exactly 0 and every weight exactly 1, so each
-output is the plain mean of that head's V rows (a page or token dropped,
-doubled or mis-masked by the work split, the page loop or the merge moves
-it).
+Every (seq, kv head), at full size, also meets two size-independent
+properties:
+* with q = 0 every logit is exactly 0 and every weight exactly 1, so each
+  output is the plain mean of that head's V rows (a page or token dropped,
+  doubled or mis-masked by the work split, the page loop or the merge moves
+  it);
+* with the seeded q, the output does not depend on how the head's rows are
+  split into work items (another split moves every item boundary, every
+  wave's page set and the merge's inputs; only fp32 summation order and the
+  fp16 rounding of P against another running maximum may differ).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -70,3 +77,11 @@ def test_full_size_decode_matches_oracle_on_sampled_heads(gpu, config, heads):
     err = float((out0.double() - want).abs().max())
     log(f"  every head, q = 0: max abs err {err:.3e}")
     assert err <= 1e-3
+    rpi = 97                                           # an odd split: item boundaries move everywhere
+    work, work_start = ops._work_device(wl.plan.row_start, rpi, gpu)
+    assert work.shape[0] != pool.num_items
+    out2 = ops.decode_paged(dataclasses.replace(pool, work=work, work_start=work_start), q, wl.gqa,
+                            wl.rope_theta, check=True)
+    err2 = float((out2.float() - out.float()).abs().max())
+    log(f"  every head, {work.shape[0]} items of {rpi} rows against {pool.num_items}: max abs diff {err2:.3e}")
+    assert err2 <= 1e-3
