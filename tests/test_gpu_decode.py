@@ -209,10 +209,11 @@ def test_decode_masked_positions(gpu):
     assert max_err(got, want) <= TOL
 
 
-@pytest.mark.parametrize("ctx", [3000, 8192])
+@pytest.mark.parametrize("ctx", [3000, 8192, 32768])
 def test_ragged_logits_matches_oracle(gpu, ctx):
     # 8192 tokens: > 2048 tier-1 chunks, so the pipelined kernel runs its full
-    # 512-workgroup grid with the XCD-aware work split
+    # grid with the XCD-aware work split; 32768: config 2 at full size (the
+    # bench line's workload)
     import fused_decode
     wl = synth.make_decode_workload(2, ctx_override=ctx)
     cpu = oracle.build_pool(wl)
