@@ -304,3 +304,137 @@ def test_decode_runner_closure_keeps_its_plan_alive(monkeypatch):
     del fn
     gc.collect()
     assert alive() is None                            # and released with it (its plan destroyed)
+
+
+# ------------------------------------------------- decode step and its plan --
+_FAKE = 1 << 20                                      # non-null stand-in address, never dereferenced
+
+
+def _step_plan_args(**kw):
+    """sphkv_step_plan_create's arguments for 1 sequence x 8 kv heads at dh 128,
+    gqa 4, 8 items, room for 2 decode pages per (seq, head); plan_out last."""
+    d = dict(pages=_FAKE, pages_bytes=1 << 16, ptable=_FAKE, vslot=_FAKE, positions=_FAKE, num_rows=8,
+             v_pool=_FAKE, num_vpages=64, cb1=_FAKE, cb2=None, cb3=_FAKE, work=_FAKE, num_items=8,
+             work_start=_FAKE, num_seqs=1, num_kv=8, gqa=4, stg_r=_FAKE, stg_code=_FAKE, stg_v=_FAKE,
+             stg_pos=_FAKE, tail_state=_FAKE, dec_byte0=4096, dec_vpage0=8, dec_cap=2, staged=0, flushed=0,
+             step_parity=0, workspace=_FAKE, workspace_bytes=1 << 20, dh=128, page_size=16, sm_scale=0.1,
+             rope_theta=500000.0)
+    d.update(kw)
+    return list(d.values())
+
+
+@pytest.mark.parametrize("kw, msg", [
+    (dict(staged=16), "staged must be 0..15"),
+    (dict(flushed=3), "flushed 0..dec_cap"),
+    (dict(dec_byte0=4100), "16-byte aligned"),
+    (dict(dec_cap=1000), "leaves the byte pool"),
+    (dict(dec_vpage0=60), "V slots leave the V pool"),
+    (dict(cb3=None), "tier-3 codebook is required"),
+    (dict(stg_v=None), "null pointer"),
+    (dict(num_seqs=0), "num_seqs must be > 0"),
+    (dict(num_items=7), "one work item per (seq, head)"),
+    (dict(workspace_bytes=1024), "workspace too small"),
+    (dict(step_parity=2), "step_parity must be 0 or 1"),
+    (dict(gqa=3), "gqa must be"),
+])
+def test_step_plan_argument_errors(kw, msg):
+    lib = sphkv_lib.load()
+    h = ctypes.c_void_p()
+    assert lib.sphkv_step_plan_create(*_step_plan_args(**kw), ctypes.byref(h)) == -1
+    assert msg in lib.sphkv_last_error().decode()
+    assert h.value is None
+
+
+def test_step_plan_counts_and_capacity():
+    # plan creation checks arguments only; a run that would need a decode
+    # page past dec_cap, or whose mode or inputs are bad, fails before any
+    # launch and leaves the host's counts unchanged
+    lib = sphkv_lib.load()
+    h = ctypes.c_void_p()
+    assert lib.sphkv_step_plan_create(*_step_plan_args(staged=15, flushed=2, step_parity=1), ctypes.byref(h)) == 0
+    a, b, p = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    assert lib.sphkv_step_plan_counts(h, ctypes.byref(a), ctypes.byref(b), ctypes.byref(p)) == 0
+    assert (a.value, b.value, p.value) == (15, 2, 1)
+    for mode in (2, 3):                                # appending: the 16th token needs a third page
+        assert lib.sphkv_step_plan_run(h, _FAKE, _FAKE, 0, _FAKE, _FAKE, _FAKE, mode, None) == -1
+        assert "no decode-page slot left" in lib.sphkv_last_error().decode()
+    for mode in (0, 4):
+        assert lib.sphkv_step_plan_run(h, _FAKE, _FAKE, 0, _FAKE, _FAKE, _FAKE, mode, None) == -1
+        assert "mode must be" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_step_plan_run(h, _FAKE, None, 0, _FAKE, _FAKE, _FAKE, 3, None) == -1
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    assert lib.sphkv_step_plan_run(h, None, _FAKE, 0, _FAKE, _FAKE, _FAKE, 1, None) == -1   # decode needs q
+    assert lib.sphkv_step_plan_counts(h, ctypes.byref(a), ctypes.byref(b), ctypes.byref(p)) == 0
+    assert (a.value, b.value, p.value) == (15, 2, 1)
+    lib.sphkv_step_plan_destroy(h)
+    assert lib.sphkv_step_plan_run(None, _FAKE, _FAKE, 0, _FAKE, _FAKE, _FAKE, 3, None) == -1
+    assert lib.sphkv_step_plan_counts(None, ctypes.byref(a), ctypes.byref(b), ctypes.byref(p)) == -1
+    lib.sphkv_step_plan_destroy(None)                  # a no-op
+
+
+def _step_args(**kw):
+    """sphkv_decode_step's arguments (shapes as _step_plan_args), stream last."""
+    d = dict(pages=_FAKE, pages_bytes=1 << 16, ptable=_FAKE, vslot=_FAKE, positions=_FAKE, num_rows=8,
+             v_pool=_FAKE, num_vpages=64, cb1=_FAKE, cb2=None, cb3=_FAKE, work=_FAKE, num_items=8,
+             work_start=_FAKE, num_seqs=1, num_kv=8, gqa=4, q=_FAKE, k_new=_FAKE, k_is_fp32=0, v_new=_FAKE,
+             cur_pos=_FAKE, stg_r=_FAKE, stg_code=_FAKE, stg_v=_FAKE, stg_pos=_FAKE, tail_state=_FAKE,
+             dec_byte0=4096, dec_vpage0=8, dec_cap=2, append=1, step_parity=0, out=_FAKE, workspace=_FAKE,
+             workspace_bytes=1 << 20, dh=128, page_size=16, sm_scale=0.1, rope_theta=500000.0, stream=None)
+    d.update(kw)
+    return list(d.values())
+
+
+@pytest.mark.parametrize("kw, msg", [
+    (dict(append=2), "append must be 0 or 1"),
+    (dict(step_parity=-1), "step_parity must be 0 or 1"),
+    (dict(pages_bytes=(1 << 16) + 2), "multiple of 4"),
+    (dict(rope_theta=1.0), "rope_theta must be > 1"),
+    (dict(k_new=None), "null pointer"),
+    (dict(out=None), "null pointer"),
+    (dict(dec_cap=1000), "leaves the byte pool"),
+    (dict(page_size=128), "page_size must be 16"),
+])
+def test_decode_step_argument_errors(kw, msg):
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_step(*_step_args(**kw)) == -1
+    assert msg in lib.sphkv_last_error().decode()
+
+
+def test_decode_step_and_append_with_no_sequence_are_no_ops():
+    lib = sphkv_lib.load()
+    assert lib.sphkv_decode_step(*_step_args(num_seqs=0, q=None, k_new=None, out=None)) == 0
+    # (pages, bytes, positions, rows, v_pool, vpages, cb3, work, items, work_start, seqs, kv, k_new,
+    #  k_is_fp32, v_new, cur_pos, stg_r, stg_code, stg_v, stg_pos, tail_state, dec_byte0, dec_vpage0,
+    #  dec_cap, step_parity, dh, page_size, stream)
+    app = [_FAKE, 1 << 16, _FAKE, 8, _FAKE, 64, _FAKE, _FAKE, 8, _FAKE, 0, 8, None, 0, None, None, _FAKE, _FAKE,
+           _FAKE, _FAKE, _FAKE, 4096, 8, 2, 0, 128, 16, None]
+    assert lib.sphkv_decode_append(*app) == 0
+    app[10] = 1
+    assert lib.sphkv_decode_append(*app) == -1         # a sequence, no k_new
+    assert "null pointer" in lib.sphkv_last_error().decode()
+    app[12], app[14], app[15] = _FAKE, _FAKE, _FAKE
+    app[6] = None
+    assert lib.sphkv_decode_append(*app) == -1
+    assert "tier-3 codebook is required" in lib.sphkv_last_error().decode()
+    app[6] = _FAKE
+    app[24] = 5
+    assert lib.sphkv_decode_append(*app) == -1
+    assert "step_parity must be 0 or 1" in lib.sphkv_last_error().decode()
+
+
+def test_tail_relayout_argument_errors():
+    lib = sphkv_lib.load()
+    # (row_start, num_sh, num_rows, ptable, vslot, positions, dec_cap, dec_byte0, dec_vpage0, dh,
+    #  ptable_d, vslot_d, positions_d, stream)
+    args = [_FAKE, 8, 100, _FAKE, _FAKE, _FAKE, 4, 4096, 100, 128, _FAKE, _FAKE, _FAKE, None]
+    bad = [(dict(i=9, v=96), "dh must be 64 or 128"), (dict(i=7, v=4100), "16-byte aligned"),
+           (dict(i=6, v=-1), "bad size"), (dict(i=6, v=1 << 28), "outgrows int32"),
+           (dict(i=10, v=None), "null pointer")]
+    for b, msg in bad:
+        a = list(args)
+        a[b["i"]] = b["v"]
+        assert lib.sphkv_tail_relayout(*a) == -1
+        assert msg in lib.sphkv_last_error().decode()
+    a = list(args)
+    a[1], a[2], a[3], a[4], a[5] = 0, 0, None, None, None
+    assert lib.sphkv_tail_relayout(*a) == 0            # nothing to lay out
