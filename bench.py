@@ -104,7 +104,7 @@ def clone_pool(pool: ops.PagedPool) -> ops.PagedPool:
 # KiB) and WRITE_SIZE all of them (262144 KiB), hence the factor 2.  Measured
 # with `bench.py --calibrate` under rocprofv3 --pmc (summary and commands in
 # profiles/decode_config2_hbm_traffic.txt); re-measured when the kernel changes.
-TRAFFIC_BYTES = {(2, "default"): 86506939}
+TRAFFIC_BYTES = {(2, "default"): 86515541}
 
 # encode_pages_kernel at config 3, from rocprofv3 --pmc on MI355X
 # (profiles/encode_config3_counters.txt): VALU instructions per launch (MFMA
