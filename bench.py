@@ -118,11 +118,11 @@ ENCODE_TRAFFIC_BYTES = {3: 55598602}
 # tiers' ragged_pipe_kernel launches; profiles/ragged_config2_hbm_traffic.txt),
 # FETCH_SIZE * 2 + WRITE_SIZE as above.
 MODEA_TRAFFIC_BYTES = {16: 80479122}
-RAGGED_TRAFFIC_BYTES = {"fit": 13673909, "table": 47988605}   # phases in the kernel / table rows read
+RAGGED_TRAFFIC_BYTES = {"fit": 13705673, "table": 47988605}   # phases in the kernel / table rows read
 # VALU instructions (MFMA included) of both ragged launches of a step with
 # fitted tables, SQ_INSTS_VALU from the same profile; the VALU-issue bound as
 # for the encode above.
-RAGGED_VALU_INSTS = {"fit": 7574181}
+RAGGED_VALU_INSTS = {"fit": 7657312}
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
