@@ -111,8 +111,8 @@ TRAFFIC_BYTES = {(2, "default"): 86515541}
 # included) and HBM bytes (FETCH_SIZE * 2 + WRITE_SIZE).  The VALU-issue bound
 # is that count at one wave64 VALU instruction per 4 cycles on each of the
 # 1024 SIMDs at 2.4 GHz.
-ENCODE_VALU_INSTS = {3: 6770579}
-ENCODE_TRAFFIC_BYTES = {3: 55598602}
+ENCODE_VALU_INSTS = {3: 7061123}
+ENCODE_TRAFFIC_BYTES = {3: 55632656}
 # HBM bytes per Mode-A decode (modea_fast_kernel, page_size 16; profiles/
 # modea_config2shape_counters.txt) and per fused_decode_ragged step (both
 # tiers' ragged_pipe_kernel launches; profiles/ragged_config2_hbm_traffic.txt),
